@@ -1,0 +1,287 @@
+#!/usr/bin/env python3
+"""Fused-MoE benchmark on one MI355X.
+
+A step is one fused-MoE layer call (alignment, GEMM1 + silu, GEMM2 + top-k
+weight, top-k sum) on the Mixtral-8x7B-shaped bf16 layer at M=4096 tokens,
+with every input already resident in HBM. Prints ONE JSON line:
+
+* ``value``: TFLOP/s of the whole layer at M=4096 (FLOPs = 6*M*topk*K*N),
+  ``ms_per_step`` = ms/layer;
+* ``roofline``: the dominant kernel (largest stage time, measured with HIP
+  events recorded around each stage on the launch stream, over the timed
+  region) against MI355X's peak;
+* ``sweep``: ms/layer, TFLOP/s, GB/s and roofline fractions at every M of
+  the configuration (M = 1 .. 4096), each with its own warmup and timing;
+* ``cpu_baseline``: the repo's CPU torch reference (oracle/) on a bounded
+  sample of the same workload, on this host's cores.
+
+Options: ``--config`` picks another configuration of
+flaggems_sglang.testing.CONFIGS (its largest M is then the headline),
+``--no-sweep`` / ``--no-cpu`` skip those legs (profiling runs).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "flaggems-sglang_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = ("fused-MoE ms/layer, TFLOP/s & HBM GB/s (% roofline) at M=1..4096, "
+          "1 GPU")
+PEAK_HBM_GBS = 8000.0
+PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "int8": 5000.0}
+FLUSH_BYTES = 512 << 20  # > MALL (256 MB): flush between steps when small
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="mixtral")
+    ap.add_argument("--m", type=int, default=None, help="headline M")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep-steps", type=int, default=10)
+    return ap.parse_args()
+
+
+class Layer:
+    """One configuration's weights plus a token batch, ready to call."""
+
+    def __init__(self, cfg, weights, M, device):
+        from flaggems_sglang import testing
+
+        self.cfg, self.w, self.M = cfg, weights, M
+        self.x, self.tw, self.ti = testing.make_tokens(
+            M, cfg.K, cfg.E, cfg.topk, cfg.scoring, cfg.hot_experts,
+            cfg.hot_bias, device=device, seed=M + cfg.K + cfg.N + cfg.E + cfg.topk)
+        self.kw = weights.kwargs(cfg.mode)
+        self.flops = testing.layer_flops(M, cfg)
+        self.bytes = testing.layer_bytes(M, cfg.K, cfg.N, cfg.topk, cfg.mode,
+                                         self.ti, cfg.E)
+        self.touched = int(self.ti.unique().numel())
+
+    def __call__(self):
+        import flaggems_sglang
+
+        return flaggems_sglang.fused_moe(self.x, self.w.w1, self.w.w2, self.tw,
+                                         self.ti, **self.kw)
+
+
+def time_layer(layer, steps, warmup, flush):
+    """Times `steps` calls (after `warmup`), returns (ms/call, stage ms)."""
+    import ctypes
+
+    import torch
+
+    from flaggems_sglang import _capi
+
+    lib = _capi.load()
+    scratch = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda") if flush else None
+    for _ in range(warmup):
+        layer()
+    torch.cuda.synchronize()
+    stage = (ctypes.c_float * 6)()
+    lib.fgs_moe_profile_read(stage, 6)  # drop anything recorded before
+    total = 0.0
+    if flush:
+        # cold weights each step: a 512 MiB write evicts L2 and MALL; only
+        # the layer call itself is inside the events.
+        for _ in range(steps):
+            scratch.fill_(1)
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            lib.fgs_moe_profile_enable(1)
+            a.record()
+            layer()
+            b.record()
+            lib.fgs_moe_profile_enable(0)
+            torch.cuda.synchronize()
+            total += a.elapsed_time(b)
+        ms = total / steps
+    else:
+        lib.fgs_moe_profile_enable(1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            layer()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        lib.fgs_moe_profile_enable(0)
+    n = lib.fgs_moe_profile_read(stage, 6)
+    stages = dict(zip(_capi.PROFILE_STAGES, [float(v) for v in stage])) if n > 0 else {}
+    return ms, stages
+
+
+def dominant(layer, stages):
+    """Roofline object for the slowest stage (a GEMM in every config)."""
+    cfg = layer.cfg
+    name = max(("gemm1", "gemm2"), key=lambda s: stages.get(s, 0.0))
+    t = stages[name] * 1e-3
+    M, k, K, N = layer.M, cfg.topk, cfg.K, cfg.N
+    bw = 2 if cfg.mode == "bf16" else 1
+    if name == "gemm1":
+        flops = 4.0 * M * k * K * N
+        wbytes = layer.touched * 2 * N * K * bw
+        io = M * K * bw + M * k * N * 2
+    else:
+        flops = 2.0 * M * k * K * N
+        wbytes = layer.touched * K * N * bw
+        io = M * k * N * bw + M * k * K * 2
+    tflops = flops / t / 1e12
+    gbs = (wbytes + io) / t / 1e9
+    frac_mfma = tflops / PEAK_TFLOPS[cfg.mode]
+    frac_hbm = gbs / PEAK_HBM_GBS
+    if frac_mfma >= frac_hbm:
+        return {"kernel": f"moe_gemm ({name})", "bound": "mfma",
+                "achieved": round(tflops, 2), "peak": PEAK_TFLOPS[cfg.mode],
+                "unit": "TFLOP/s", "frac": round(frac_mfma, 4), "traffic": None,
+                "per_unit": f"{'4' if name == 'gemm1' else '2'}*M*topk*K*N flops",
+                "avg_ms": round(stages[name], 4)}
+    return {"kernel": f"moe_gemm ({name})", "bound": "hbm",
+            "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(frac_hbm, 4), "traffic": None,
+            "per_unit": "touched_experts * weight bytes + activations",
+            "avg_ms": round(stages[name], 4)}
+
+
+def row(layer, ms, stages):
+    cfg = layer.cfg
+    t = ms * 1e-3
+    tflops = layer.flops / t / 1e12
+    gbs = layer.bytes / t / 1e9
+    return {
+        "M": layer.M, "ms": round(ms, 4), "tflops": round(tflops, 2),
+        "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+        "frac_mfma": round(tflops / PEAK_TFLOPS[cfg.mode], 4),
+        "experts_touched": layer.touched,
+        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
+    }
+
+
+def cpu_baseline(layer, budget_s=25.0):
+    """The repo's CPU torch reference (oracle/) on a bounded token sample of
+    the same layer, on every core this process may use."""
+    import torch
+
+    from oracle import moe_ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cfg = layer.cfg
+    x = layer.x.cpu()
+    tw, ti = layer.tw.cpu(), layer.ti.cpu()
+    w1 = layer.w.w1.cpu()
+    w2 = layer.w.w2.cpu()
+    s1 = layer.w.w1_scale.cpu() if layer.w.w1_scale is not None else None
+    s2 = layer.w.w2_scale.cpu() if layer.w.w2_scale is not None else None
+    n = min(layer.M, 512)
+    toks = list(range(n))
+    t0 = time.perf_counter()
+    moe_ref.fused_moe(x, w1, w2, tw, ti, mode=cfg.mode, w1_scale=s1,
+                      w2_scale=s2, tokens=toks)
+    dt = time.perf_counter() - t0
+    reps = 1
+    if dt * 2 < budget_s:
+        t0 = time.perf_counter()
+        moe_ref.fused_moe(x, w1, w2, tw, ti, mode=cfg.mode, w1_scale=s1,
+                          w2_scale=s2, tokens=toks)
+        dt = min(dt, time.perf_counter() - t0)
+        reps = 2
+    flops = 6.0 * n * cfg.topk * cfg.K * cfg.N
+    return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "ms_per_layer_sample": round(dt * 1e3, 1),
+            "sample": f"oracle.moe_ref.fused_moe (torch fp32 on CPU) on the first "
+                      f"{n} of {layer.M} tokens of the same {cfg.name} layer, "
+                      f"best of {reps}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the fused-MoE path has no "
+              f"multi-GPU part here); --gpus {args.gpus} is not supported",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from flaggems_sglang import _capi, testing
+
+    _capi.load()
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(dev)
+    log(f"device: {props.name} CUs={props.multi_processor_count} "
+        f"mem={props.total_memory / 2**30:.0f} GiB")
+    cfg = testing.CONFIGS[args.config]
+    M = args.m or max(cfg.Ms)
+    t0 = time.perf_counter()
+    weights = testing.make_weights(cfg.K, cfg.N, cfg.E, cfg.mode, cfg.w_scale,
+                                   device=dev)
+    torch.cuda.synchronize()
+    log(f"weights {weights.nbytes() / 1e9:.2f} GB in {time.perf_counter() - t0:.1f}s")
+
+    head = Layer(cfg, weights, M, dev)
+    small_ws = head.bytes < FLUSH_BYTES
+    ms, stages = time_layer(head, args.steps, args.warmup, flush=small_ws)
+    log(f"headline {cfg.name} M={M}: {ms:.4f} ms/layer stages={stages}")
+
+    sweep = []
+    if not args.no_sweep:
+        for m in cfg.Ms:
+            lay = head if m == M else Layer(cfg, weights, m, dev)
+            flush = lay.bytes < FLUSH_BYTES
+            sms, sst = time_layer(lay, args.sweep_steps, 3, flush)
+            r = row(lay, sms, sst)
+            r["roofline"] = dominant(lay, sst)
+            sweep.append(r)
+            log(f"sweep M={m}: {json.dumps(r)}")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(head)
+        log(f"cpu baseline: {cpu}")
+
+    tflops = head.flops / (ms * 1e-3) / 1e12
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg.mode,
+        "data": "synthetic (seeded randn activations, randn*0.02 weights, "
+                "softmax/sigmoid top-k routing)",
+        "config": {"workload": f"{cfg.name} fused-MoE layer, M={M}",
+                   "M": M, "K": cfg.K, "N": cfg.N, "E": cfg.E,
+                   "topk": cfg.topk, "mode": cfg.mode,
+                   "experts_touched": head.touched,
+                   "layer_flops": head.flops, "layer_bytes": head.bytes,
+                   "gb_s": round(head.bytes / (ms * 1e-3) / 1e9, 1),
+                   "cold_cache": small_ws},
+        "roofline": dominant(head, stages),
+        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+        "device": {"name": props.name, "cus": props.multi_processor_count},
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

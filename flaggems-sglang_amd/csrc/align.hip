@@ -1,0 +1,184 @@
+// moe_align_block_size for gfx950.
+//
+// Replaces the routing conversion of the reference
+// (src/flaggems_sglang/ops/fused_moe.py:130-139): a stable argsort of the
+// flattened expert ids (:134) and a per-expert histogram (:137-139). The
+// output is the block-padded, expert-grouped order the grouped GEMMs consume.
+//
+// One workgroup of 16 wave64s. Wave w owns the contiguous slot segment
+// [w*seg, (w+1)*seg). Pass 1 counts ids per (wave, expert) in LDS; pass 2
+// turns the counts into per-expert padded offsets plus per-wave offsets
+// inside each expert (exclusive over waves, so lower slots come first);
+// pass 3 walks each segment in slot order, 64 slots at a time, ranking each
+// slot among equal ids of the chunk with ballots over the id bits. Nothing
+// order-deciding uses atomics, so the result is bit-exact and stable.
+#include <mutex>
+#include <string>
+
+#include "fgs_common.h"
+
+namespace fgs {
+
+constexpr int kAlignWaves = 16;
+constexpr int kAlignThreads = kAlignWaves * kWave;
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int num_experts,
+    int block_size, int id_bits, int32_t* __restrict__ sorted_ids,
+    int32_t* __restrict__ expert_ids, int32_t* __restrict__ num_post_pad,
+    int64_t max_padded) {
+  // cnt[w * E + e]: pass 1 count, then (after pass 2) the slot cursor.
+  extern __shared__ int32_t smem[];
+  int32_t* cnt = smem;                                  // [16][E]
+  int32_t* off = smem + kAlignWaves * num_experts;      // [E + 1]
+  int32_t* tot = off + num_experts + 1;                 // [E]
+  __shared__ int32_t scan_tmp[kAlignThreads / kWave];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int E = num_experts;
+
+  for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) cnt[i] = 0;
+  __syncthreads();
+
+  // Segment per wave, a multiple of 64 slots.
+  const int64_t seg =
+      ((numel + kAlignWaves - 1) / kAlignWaves + kWave - 1) / kWave * kWave;
+  const int64_t beg = static_cast<int64_t>(wave) * seg;
+  const int64_t end = beg + seg < numel ? beg + seg : numel;
+
+  // Pass 1: per-(wave, expert) histogram.
+  for (int64_t i = beg + lane; i < end; i += kWave) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
+  }
+  __syncthreads();
+
+  // Pass 2a: per expert, total and exclusive offsets over waves.
+  for (int e = tid; e < E; e += kAlignThreads) {
+    int run = 0;
+    for (int w = 0; w < kAlignWaves; ++w) {
+      const int c = cnt[w * E + e];
+      cnt[w * E + e] = run;
+      run += c;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+
+  // Pass 2b: exclusive scan of padded sizes over experts (block scan over
+  // chunks of kAlignThreads experts).
+  int carry = 0;
+  for (int base = 0; base < E; base += kAlignThreads) {
+    const int e = base + tid;
+    const int padded =
+        e < E ? (tot[e] + block_size - 1) / block_size * block_size : 0;
+    // inclusive scan within the wave
+    int v = padded;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int t = __shfl_up(v, d, kWave);
+      if (lane >= d) v += t;
+    }
+    if (lane == kWave - 1) scan_tmp[wave] = v;
+    __syncthreads();
+    int wave_base = 0;
+    int all = 0;
+    for (int w = 0; w < kAlignThreads / kWave; ++w) {
+      const int s = scan_tmp[w];
+      if (w < wave) wave_base += s;
+      all += s;
+    }
+    if (e < E) off[e] = carry + wave_base + v - padded;
+    carry += all;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    off[E] = carry;
+    num_post_pad[0] = carry;
+  }
+  __syncthreads();
+
+  const int total_padded = off[E];
+
+  // Pass 2c: sentinel fill of pads and of the tail, and block -> expert map.
+  for (int e = wave; e < E; e += kAlignWaves) {
+    const int64_t p0 = static_cast<int64_t>(off[e]) + tot[e];
+    const int64_t p1 = off[e + 1];
+    for (int64_t p = p0 + lane; p < p1; p += kWave)
+      sorted_ids[p] = static_cast<int32_t>(numel);
+    for (int b = off[e] / block_size + lane; b < off[e + 1] / block_size;
+         b += kWave)
+      expert_ids[b] = e;
+  }
+  for (int64_t p = total_padded + tid; p < max_padded; p += kAlignThreads)
+    sorted_ids[p] = static_cast<int32_t>(numel);
+  for (int64_t b = total_padded / block_size + tid; b < max_padded / block_size;
+       b += kAlignThreads)
+    expert_ids[b] = -1;
+
+  // Pass 3: stable scatter. Chunks of 64 consecutive slots; rank among equal
+  // ids of the chunk from ballots over the id bits.
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  for (int64_t c0 = beg; c0 < end; c0 += kWave) {
+    const int64_t i = c0 + lane;
+    int e = -1;
+    if (i < end) {
+      e = ids[i];
+      if (e < 0 || e >= E) e = -1;
+    }
+    const bool valid = e >= 0;
+    uint64_t match = __ballot(valid);
+    for (int b = 0; b < id_bits; ++b) {
+      const bool bit = valid && ((e >> b) & 1);
+      const uint64_t on = __ballot(bit);
+      match &= bit ? on : ~on;
+    }
+    int base = 0;
+    if (valid) base = cnt[wave * E + e];
+    const int rank = __popcll(match & lt_mask);
+    // Highest matching lane advances the cursor after every lane has read it.
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      sorted_ids[off[e] + base + rank] = static_cast<int32_t>(i);
+      const bool leader = (match >> lane) == 1ull;
+      if (leader) cnt[wave * E + e] = base + __popcll(match);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+size_t align_smem_bytes(int num_experts) {
+  return sizeof(int32_t) *
+         (static_cast<size_t>(kAlignWaves) * num_experts + 2 * num_experts + 1);
+}
+
+int launch_align(const int32_t* ids, int64_t numel, int num_experts,
+                 int block_size, int32_t* sorted_ids, int32_t* expert_ids,
+                 int32_t* num_post_pad, int64_t max_padded,
+                 hipStream_t stream) {
+  int id_bits = 0;
+  while ((1 << id_bits) < num_experts) ++id_bits;
+  const size_t smem = align_smem_bytes(num_experts);
+  if (smem > 64 * 1024) {
+    // gfx950 has 160 KiB of LDS per CU; opt in beyond the 64 KiB default.
+    static std::once_flag once;
+    static hipError_t attr_err = hipSuccess;
+    std::call_once(once, [] {
+      attr_err = hipFuncSetAttribute(
+          reinterpret_cast<const void*>(&moe_align_kernel),
+          hipFuncAttributeMaxDynamicSharedMemorySize,
+          static_cast<int>(align_smem_bytes(1024)));
+    });
+    if (attr_err != hipSuccess)
+      return fail(FGS_ELAUNCH, std::string("moe_align_kernel LDS opt-in: ") +
+                                   hipGetErrorString(attr_err));
+  }
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), smem,
+                     stream, ids, numel, num_experts, block_size, id_bits,
+                     sorted_ids, expert_ids, num_post_pad, max_padded);
+  return check_launch("moe_align_kernel");
+}
+
+}  // namespace fgs

@@ -1,0 +1,480 @@
+// C ABI of libfgs_moe.so (declared in include/fgs_moe.h): host-side
+// validation, the kernel schedule of one fused-MoE call, the workspace
+// layout and the launch sequence. No device allocation, no synchronisation.
+#include <string.h>
+
+#include <algorithm>
+#include <array>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "fgs_moe_kernels.h"
+
+namespace fgs {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  set_error(msg);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return fail(FGS_ELAUNCH, std::string(what) + ": " + hipGetErrorString(err));
+  return FGS_OK;
+}
+
+static hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+static int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+constexpr int kMaxExperts = 1024;
+constexpr int kKnownFlags = FGS_FLAG_ROUTER_WEIGHT_ON_INPUT |
+                            FGS_FLAG_FORCE_DECODE | FGS_FLAG_FORCE_PREFILL;
+
+static int max_padded_of(int64_t numel, int e, int block) {
+  return static_cast<int>(numel + static_cast<int64_t>(e) * (block - 1));
+}
+
+// ------------------------------------------------------------- schedule ---
+struct Plan {
+  int dt;
+  int block_m;     // alignment block = rows per GEMM row block
+  int mt;          // 16-row MFMA tiles per row block (streaming kernels)
+  int kw1, kw2;    // waves splitting the contraction of GEMM1 / GEMM2
+  int64_t max_padded, n_blocks;
+  // workspace layout (byte offsets)
+  int64_t o_sorted, o_eids, o_npp, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, total;
+};
+
+static int pick_kw(int64_t kdim, int step, int cap) {
+  const int64_t steps = kdim / step;
+  int kw = 1;
+  while (kw * 2 <= cap && kw * 2 <= steps) kw *= 2;
+  return kw;
+}
+
+static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
+                     int qmode, int flags, Plan* pl) {
+  const int64_t numel = m * topk;
+  Plan p{};
+  p.dt = qmode == FGS_QMODE_FP8_BLOCK ? kDtFp8
+         : qmode == FGS_QMODE_INT8_CHANNEL ? kDtInt8 : kDtBf16;
+  const double rows_per_expert = static_cast<double>(numel) / e;
+  p.mt = rows_per_expert <= 16 ? 1 : rows_per_expert <= 32 ? 2 : 4;
+  (void)flags;
+  p.block_m = 16 * p.mt;
+  const int step = stream_step_k(p.dt);
+  p.kw1 = pick_kw(hidden, step, 4);
+  p.kw2 = pick_kw(inter, step, 8);
+  p.max_padded = max_padded_of(numel, e, p.block_m);
+  p.n_blocks = p.max_padded / p.block_m;
+
+  const int64_t esz = p.dt == kDtBf16 ? 2 : 1;
+  int64_t o = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = o;
+    o = align_up(o + bytes, 256);
+    return at;
+  };
+  p.o_sorted = take(p.max_padded * 4);
+  p.o_eids = take(std::max<int64_t>(p.n_blocks, 1) * 4);
+  p.o_npp = take(4);
+  p.o_a2 = take(p.max_padded * inter * 2);
+  p.o_xq = p.o_xs = p.o_a2q = p.o_a2s = -1;
+  if (p.dt != kDtBf16) {
+    p.o_xq = take(m * hidden * esz);
+    p.o_xs = take(p.dt == kDtFp8 ? m * (hidden / 128) * 4 : m * 4);
+    p.o_a2q = take(p.max_padded * inter * esz);
+    p.o_a2s = take(p.dt == kDtFp8 ? p.max_padded * (inter / 128) * 4
+                                  : p.max_padded * 4);
+  }
+  p.o_y = take(numel * hidden * 2);
+  p.total = o;
+  *pl = p;
+  return FGS_OK;
+}
+
+static int validate(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
+                    int qmode, int flags, int64_t ws_bytes, bool check_ws) {
+  if (m < 0) return fail(FGS_EINVAL, "m must be >= 0");
+  if (hidden <= 0 || inter <= 0)
+    return fail(FGS_EINVAL, "hidden and inter must be > 0");
+  if (e < 1 || e > kMaxExperts)
+    return fail(FGS_EINVAL, "num_experts must be in [1, 1024]");
+  if (topk < 1 || topk > e)
+    return fail(FGS_EINVAL, "topk must be in [1, num_experts]");
+  if (qmode != FGS_QMODE_BF16 && qmode != FGS_QMODE_FP8_BLOCK &&
+      qmode != FGS_QMODE_INT8_CHANNEL)
+    return fail(FGS_EINVAL, "unknown qmode");
+  if (flags & ~kKnownFlags) return fail(FGS_EINVAL, "unknown flag bits");
+  if ((flags & FGS_FLAG_FORCE_DECODE) && (flags & FGS_FLAG_FORCE_PREFILL))
+    return fail(FGS_EINVAL, "FORCE_DECODE and FORCE_PREFILL are exclusive");
+  const int64_t numel = m * topk;
+  if (numel + static_cast<int64_t>(e) * 64 >= (int64_t(1) << 31))
+    return fail(FGS_EUNSUPPORTED, "m * topk too large for int32 slot ids");
+  const int dt = qmode == FGS_QMODE_FP8_BLOCK ? kDtFp8
+                 : qmode == FGS_QMODE_INT8_CHANNEL ? kDtInt8 : kDtBf16;
+  const int step = stream_step_k(dt);
+  if (hidden % step != 0 || inter % step != 0)
+    return fail(FGS_EUNSUPPORTED, "hidden and inter must be multiples of " +
+                                      std::to_string(step));
+  if ((inter / 16) > 65535 || (hidden / 16) > 65535)
+    return fail(FGS_EUNSUPPORTED, "hidden / inter too large");
+  if (check_ws) {
+    Plan p;
+    make_plan(m, hidden, inter, e, topk, qmode, flags, &p);
+    if (ws_bytes < p.total)
+      return fail(FGS_EINVAL, "workspace too small: need " +
+                                  std::to_string(p.total) + " bytes");
+  }
+  return FGS_OK;
+}
+
+// ------------------------------------------------------ stage profiler ---
+// Per-thread record of HIP events around the stages of each fused call.
+struct StageProfiler {
+  bool on = false;
+  std::vector<std::array<hipEvent_t, FGS_PROFILE_STAGES + 1>> calls;
+  std::vector<std::array<hipEvent_t, FGS_PROFILE_STAGES + 1>> pool;
+  std::array<hipEvent_t, FGS_PROFILE_STAGES + 1>* cur = nullptr;
+
+  ~StageProfiler() {
+    for (auto* v : {&calls, &pool})
+      for (auto& a : *v)
+        for (hipEvent_t e : a) (void)hipEventDestroy(e);
+  }
+  // Starts a call record; returns false (profiling silently off) on failure.
+  bool begin() {
+    cur = nullptr;
+    if (!on) return false;
+    std::array<hipEvent_t, FGS_PROFILE_STAGES + 1> ev;
+    if (!pool.empty()) {
+      ev = pool.back();
+      pool.pop_back();
+    } else {
+      for (auto& e : ev)
+        if (hipEventCreate(&e) != hipSuccess) return false;
+    }
+    calls.push_back(ev);
+    cur = &calls.back();
+    return true;
+  }
+  void mark(int i, hipStream_t s) {
+    if (cur) (void)hipEventRecord((*cur)[i], s);
+  }
+};
+static thread_local StageProfiler g_prof;
+
+// ------------------------------------------------------- fused pipeline ---
+struct FusedArgs {
+  int qmode;
+  const void* x;
+  const void* w13;
+  const void* w2;
+  const float* w13_scale;
+  const float* w2_scale;
+  const float* topk_weights;
+  const int32_t* topk_ids;
+  int64_t m, hidden, inter;
+  int e, topk, flags;
+  void* ws;
+  int64_t ws_bytes;
+  void* out;
+  hipStream_t stream;
+};
+
+static int run_fused(const FusedArgs& a) {
+  int rc = validate(a.m, a.hidden, a.inter, a.e, a.topk, a.qmode, a.flags,
+                    a.ws_bytes, true);
+  if (rc) return rc;
+  if (!a.x || !a.w13 || !a.w2 || !a.topk_weights || !a.topk_ids || !a.out ||
+      !a.ws)
+    return fail(FGS_EINVAL, "null pointer argument");
+  if (a.qmode != FGS_QMODE_BF16 && (!a.w13_scale || !a.w2_scale))
+    return fail(FGS_EINVAL, "quantised mode needs w13_scale and w2_scale");
+  if (a.m == 0) return FGS_OK;
+  if (reinterpret_cast<uintptr_t>(a.x) % 16 || reinterpret_cast<uintptr_t>(a.w13) % 16 ||
+      reinterpret_cast<uintptr_t>(a.w2) % 16 || reinterpret_cast<uintptr_t>(a.out) % 16 ||
+      reinterpret_cast<uintptr_t>(a.ws) % 256)
+    return fail(FGS_EINVAL, "tensors must be 16-byte aligned (workspace 256)");
+
+  Plan p;
+  make_plan(a.m, a.hidden, a.inter, a.e, a.topk, a.qmode, a.flags, &p);
+  uint8_t* ws = static_cast<uint8_t*>(a.ws);
+  int32_t* sorted = reinterpret_cast<int32_t*>(ws + p.o_sorted);
+  int32_t* eids = reinterpret_cast<int32_t*>(ws + p.o_eids);
+  int32_t* npp = reinterpret_cast<int32_t*>(ws + p.o_npp);
+  uint16_t* a2 = reinterpret_cast<uint16_t*>(ws + p.o_a2);
+  uint16_t* y = reinterpret_cast<uint16_t*>(ws + p.o_y);
+  const int64_t numel = a.m * a.topk;
+
+  g_prof.begin();
+  g_prof.mark(0, a.stream);
+  rc = launch_align(a.topk_ids, numel, a.e, p.block_m, sorted, eids, npp,
+                    p.max_padded, a.stream);
+  if (rc) return rc;
+  g_prof.mark(1, a.stream);
+
+  const bool on_input = (a.flags & FGS_FLAG_ROUTER_WEIGHT_ON_INPUT) != 0;
+  const uint8_t* act = static_cast<const uint8_t*>(a.x);
+  const float* act_scale = nullptr;
+  if (p.dt == kDtFp8) {
+    rc = launch_quant_fp8_group(a.x, ws + p.o_xq,
+                                reinterpret_cast<float*>(ws + p.o_xs), a.m,
+                                a.hidden, 128, a.stream);
+    if (rc) return rc;
+    act = ws + p.o_xq;
+    act_scale = reinterpret_cast<const float*>(ws + p.o_xs);
+  } else if (p.dt == kDtInt8) {
+    rc = launch_quant_int8_token(a.x, reinterpret_cast<int8_t*>(ws + p.o_xq),
+                                 reinterpret_cast<float*>(ws + p.o_xs), a.m,
+                                 a.hidden, a.stream);
+    if (rc) return rc;
+    act = ws + p.o_xq;
+    act_scale = reinterpret_cast<const float*>(ws + p.o_xs);
+  }
+
+  g_prof.mark(2, a.stream);
+  GemmParams g1{};
+  g1.a = act;
+  g1.a_scale = act_scale;
+  g1.w = static_cast<const uint8_t*>(a.w13);
+  g1.w_scale = a.w13_scale;
+  g1.sorted_ids = sorted;
+  g1.expert_ids = eids;
+  g1.num_post_pad = npp;
+  g1.topk_w = a.topk_weights;
+  g1.out = a2;
+  g1.kdim = a.hidden;
+  g1.n_out = a.inter;
+  g1.nrows_w = 2 * a.inter;
+  g1.numel = numel;
+  g1.topk = a.topk;
+  g1.weight_on_input = on_input;
+  rc = launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
+                          static_cast<int>(p.n_blocks), a.stream);
+  if (rc) return rc;
+  g_prof.mark(3, a.stream);
+
+  const uint8_t* act2 = reinterpret_cast<const uint8_t*>(a2);
+  const float* act2_scale = nullptr;
+  if (p.dt == kDtFp8) {
+    rc = launch_quant_fp8_group(a2, ws + p.o_a2q,
+                                reinterpret_cast<float*>(ws + p.o_a2s),
+                                p.max_padded, a.inter, 128, a.stream);
+    if (rc) return rc;
+    act2 = ws + p.o_a2q;
+    act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
+  } else if (p.dt == kDtInt8) {
+    rc = launch_quant_int8_token(a2, reinterpret_cast<int8_t*>(ws + p.o_a2q),
+                                 reinterpret_cast<float*>(ws + p.o_a2s),
+                                 p.max_padded, a.inter, a.stream);
+    if (rc) return rc;
+    act2 = ws + p.o_a2q;
+    act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
+  }
+
+  g_prof.mark(4, a.stream);
+  GemmParams g2 = g1;
+  g2.a = act2;
+  g2.a_scale = act2_scale;
+  g2.w = static_cast<const uint8_t*>(a.w2);
+  g2.w_scale = a.w2_scale;
+  g2.out = y;
+  g2.kdim = a.inter;
+  g2.n_out = a.hidden;
+  g2.nrows_w = a.hidden;
+  rc = launch_gemm_stream(p.dt, false, g2, p.mt, p.kw2,
+                          static_cast<int>(p.n_blocks), a.stream);
+  if (rc) return rc;
+  g_prof.mark(5, a.stream);
+
+  rc = launch_moe_sum_routed(y, a.out, a.m, a.topk, a.hidden, a.topk_ids,
+                             a.e, a.stream);
+  g_prof.mark(6, a.stream);
+  return rc;
+}
+
+}  // namespace fgs
+
+using namespace fgs;
+
+extern "C" {
+
+const char* fgs_moe_version(void) { return "fgs_moe 0.1.0 gfx950"; }
+
+const char* fgs_moe_last_error(void) { return g_last_error.c_str(); }
+
+int64_t fgs_moe_align_max_padded(int64_t numel, int32_t num_experts,
+                                 int32_t block_size) {
+  if (numel < 0 || num_experts < 1 || block_size < 1) return -1;
+  return numel + static_cast<int64_t>(num_experts) * (block_size - 1);
+}
+
+int32_t fgs_moe_align_block_size(const int32_t* topk_ids, int64_t numel,
+                                 int32_t num_experts, int32_t block_size,
+                                 int32_t* sorted_ids, int32_t* expert_ids,
+                                 int32_t* num_post_pad, int64_t max_padded,
+                                 void* stream) {
+  if (numel < 0) return fail(FGS_EINVAL, "numel must be >= 0");
+  if (num_experts < 1 || num_experts > kMaxExperts)
+    return fail(FGS_EINVAL, "num_experts must be in [1, 1024]");
+  if (block_size < 1 || block_size > 4096)
+    return fail(FGS_EINVAL, "block_size must be in [1, 4096]");
+  const int64_t need = numel + static_cast<int64_t>(num_experts) * (block_size - 1);
+  if (max_padded < need)
+    return fail(FGS_EINVAL, "max_padded must be >= numel + E*(block_size-1) = " +
+                                std::to_string(need));
+  if (max_padded >= (int64_t(1) << 31))
+    return fail(FGS_EUNSUPPORTED, "max_padded must fit in int32");
+  if ((numel > 0 && !topk_ids) || !sorted_ids || !expert_ids || !num_post_pad)
+    return fail(FGS_EINVAL, "null pointer argument");
+  return launch_align(topk_ids, numel, num_experts, block_size, sorted_ids,
+                      expert_ids, num_post_pad, max_padded, as_stream(stream));
+}
+
+int32_t fgs_moe_silu_and_mul(const void* in, void* out, int64_t rows,
+                             int64_t n, void* stream) {
+  if (rows < 0 || n <= 0) return fail(FGS_EINVAL, "rows >= 0 and n > 0 required");
+  if (n % 8) return fail(FGS_EUNSUPPORTED, "n must be a multiple of 8");
+  if (rows > 0 && (!in || !out)) return fail(FGS_EINVAL, "null pointer argument");
+  if (reinterpret_cast<uintptr_t>(in) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+    return fail(FGS_EINVAL, "tensors must be 16-byte aligned");
+  return launch_silu_and_mul(in, out, rows, n, as_stream(stream));
+}
+
+int32_t fgs_moe_sum(const void* in, void* out, int64_t m, int32_t topk,
+                    int64_t k, void* stream) {
+  if (m < 0 || topk < 1 || k <= 0)
+    return fail(FGS_EINVAL, "m >= 0, topk >= 1 and k > 0 required");
+  if (k % 8) return fail(FGS_EUNSUPPORTED, "k must be a multiple of 8");
+  if (m > 0 && (!in || !out)) return fail(FGS_EINVAL, "null pointer argument");
+  if (reinterpret_cast<uintptr_t>(in) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+    return fail(FGS_EINVAL, "tensors must be 16-byte aligned");
+  return launch_moe_sum(in, out, m, topk, k, as_stream(stream));
+}
+
+int32_t fgs_moe_quant_fp8_group(const void* x, void* q, float* scales,
+                                int64_t rows, int64_t cols, int32_t group,
+                                void* stream) {
+  if (rows < 0 || cols <= 0) return fail(FGS_EINVAL, "rows >= 0 and cols > 0 required");
+  if (group < 8 || group > 512 || group % 8 || cols % group)
+    return fail(FGS_EUNSUPPORTED,
+                "group must be a multiple of 8 in [8, 512] dividing cols");
+  if (rows > 0 && (!x || !q || !scales))
+    return fail(FGS_EINVAL, "null pointer argument");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(q) % 8)
+    return fail(FGS_EINVAL, "x must be 16-byte and q 8-byte aligned");
+  return launch_quant_fp8_group(x, q, scales, rows, cols, group,
+                                as_stream(stream));
+}
+
+int32_t fgs_moe_quant_int8_token(const void* x, int8_t* q, float* scales,
+                                 int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0) return fail(FGS_EINVAL, "rows >= 0 and cols > 0 required");
+  if (cols % 8) return fail(FGS_EUNSUPPORTED, "cols must be a multiple of 8");
+  if (rows > 0 && (!x || !q || !scales))
+    return fail(FGS_EINVAL, "null pointer argument");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(q) % 8)
+    return fail(FGS_EINVAL, "x must be 16-byte and q 8-byte aligned");
+  return launch_quant_int8_token(x, q, scales, rows, cols, as_stream(stream));
+}
+
+int64_t fgs_moe_workspace_bytes(int64_t m, int64_t hidden, int64_t inter,
+                                int32_t num_experts, int32_t topk,
+                                int32_t qmode, int32_t flags) {
+  if (validate(m, hidden, inter, num_experts, topk, qmode, flags, 0, false))
+    return -1;
+  Plan p;
+  make_plan(m, hidden, inter, num_experts, topk, qmode, flags, &p);
+  return p.total;
+}
+
+int32_t fgs_moe_validate(int64_t m, int64_t hidden, int64_t inter,
+                         int32_t num_experts, int32_t topk, int32_t qmode,
+                         int32_t flags, int64_t ws_bytes) {
+  return validate(m, hidden, inter, num_experts, topk, qmode, flags, ws_bytes,
+                  true);
+}
+
+int32_t fgs_moe_profile_enable(int32_t on) {
+  g_prof.on = on != 0;
+  return FGS_OK;
+}
+
+int32_t fgs_moe_profile_read(float* stage_ms, int32_t n_stages) {
+  if (!stage_ms || n_stages < 1 || n_stages > FGS_PROFILE_STAGES)
+    return fail(FGS_EINVAL, "stage_ms must hold 1..FGS_PROFILE_STAGES floats");
+  for (int i = 0; i < n_stages; ++i) stage_ms[i] = 0.f;
+  const int n = static_cast<int>(g_prof.calls.size());
+  for (auto& ev : g_prof.calls) {
+    if (hipEventSynchronize(ev[FGS_PROFILE_STAGES]) != hipSuccess)
+      return fail(FGS_ELAUNCH, "profile: event synchronisation failed");
+    for (int i = 0; i < n_stages; ++i) {
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess)
+        stage_ms[i] += ms;
+    }
+    g_prof.pool.push_back(ev);
+  }
+  g_prof.calls.clear();
+  g_prof.cur = nullptr;
+  if (n > 0)
+    for (int i = 0; i < n_stages; ++i) stage_ms[i] /= n;
+  return n;
+}
+
+int32_t fgs_moe_fused_bf16(const void* x, const void* w13, const void* w2,
+                           const float* topk_weights, const int32_t* topk_ids,
+                           int64_t m, int64_t hidden, int64_t inter,
+                           int32_t num_experts, int32_t topk, int32_t flags,
+                           void* workspace, int64_t ws_bytes, void* out,
+                           void* stream) {
+  FusedArgs a{FGS_QMODE_BF16, x,      w13,    w2,          nullptr,
+              nullptr,        topk_weights, topk_ids, m,      hidden,
+              inter,          num_experts,  topk,     flags,  workspace,
+              ws_bytes,       out,          as_stream(stream)};
+  return run_fused(a);
+}
+
+int32_t fgs_moe_fused_fp8_block(const void* x, const void* w13,
+                                const void* w2, const float* w13_scale,
+                                const float* w2_scale, int32_t block_n,
+                                int32_t block_k, const float* topk_weights,
+                                const int32_t* topk_ids, int64_t m,
+                                int64_t hidden, int64_t inter,
+                                int32_t num_experts, int32_t topk,
+                                int32_t flags, void* workspace,
+                                int64_t ws_bytes, void* out, void* stream) {
+  if (block_n != 128 || block_k != 128)
+    return fail(FGS_EUNSUPPORTED, "fp8 block scales must be 128x128");
+  FusedArgs a{FGS_QMODE_FP8_BLOCK, x,     w13,      w2,       w13_scale,
+              w2_scale,            topk_weights, topk_ids, m,  hidden,
+              inter,               num_experts,  topk,     flags, workspace,
+              ws_bytes,            out,          as_stream(stream)};
+  return run_fused(a);
+}
+
+int32_t fgs_moe_fused_int8_channel(const void* x, const void* w13,
+                                   const void* w2, const float* w13_scale,
+                                   const float* w2_scale,
+                                   const float* topk_weights,
+                                   const int32_t* topk_ids, int64_t m,
+                                   int64_t hidden, int64_t inter,
+                                   int32_t num_experts, int32_t topk,
+                                   int32_t flags, void* workspace,
+                                   int64_t ws_bytes, void* out, void* stream) {
+  FusedArgs a{FGS_QMODE_INT8_CHANNEL, x,     w13,      w2,       w13_scale,
+              w2_scale,               topk_weights, topk_ids, m,  hidden,
+              inter,                  num_experts,  topk,     flags, workspace,
+              ws_bytes,               out,          as_stream(stream)};
+  return run_fused(a);
+}
+
+}  // extern "C"

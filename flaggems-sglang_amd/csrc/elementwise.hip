@@ -1,0 +1,226 @@
+// Bandwidth-bound kernels of the fused-MoE path: silu_and_mul, moe_sum and
+// the dynamic activation quantisers. Every thread moves 16-byte vectors;
+// a row is processed by consecutive threads so each wave touches one or two
+// contiguous 1 KiB spans per instruction.
+#include "fgs_common.h"
+
+namespace fgs {
+
+// ----------------------------------------------------------- silu_and_mul ---
+// out[r, c] = bf16(silu(f32(in[r, c])) * f32(in[r, n + c]))
+// (ops/fused_moe.py:44-63). Requires n % 8 == 0; 8 columns per thread.
+__global__ __launch_bounds__(256) void silu_and_mul_kernel(
+    const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int64_t rows,
+    int64_t n) {
+  const int64_t vec_per_row = n / 8;
+  const int64_t total = rows * vec_per_row;
+  for (int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+       v < total; v += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = v / vec_per_row;
+    const int64_t c = (v - r * vec_per_row) * 8;
+    const u32x4 g = *reinterpret_cast<const u32x4*>(in + r * 2 * n + c);
+    const u32x4 u = *reinterpret_cast<const u32x4*>(in + r * 2 * n + n + c);
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float g0 = __uint_as_float(g[j] << 16);
+      const float g1 = __uint_as_float(g[j] & 0xffff0000u);
+      const float u0 = __uint_as_float(u[j] << 16);
+      const float u1 = __uint_as_float(u[j] & 0xffff0000u);
+      o[j] = pack_bf16x2(silu_mul(g0, u0), silu_mul(g1, u1));
+    }
+    *reinterpret_cast<u32x4*>(out + r * n + c) = o;
+  }
+}
+
+// ---------------------------------------------------------------- moe_sum ---
+// out[t, c] = bf16(sum_j f32(in[t, j, c])): the top-k reduction that
+// matmul_ogs performs when given scatter_indx (ops/fused_moe.py:224-231).
+// Requires k % 8 == 0. With `ids` given, slots whose expert id lies outside
+// [0, num_experts) were never computed and contribute nothing.
+__global__ __launch_bounds__(256) void moe_sum_kernel(
+    const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int64_t m,
+    int topk, int64_t k, const int32_t* __restrict__ ids, int num_experts) {
+  const int64_t vec_per_row = k / 8;
+  const int64_t total = m * vec_per_row;
+  for (int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+       v < total; v += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t t = v / vec_per_row;
+    const int64_t c = (v - t * vec_per_row) * 8;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const uint16_t* src = in + t * topk * k + c;
+    for (int j = 0; j < topk; ++j) {
+      if (ids) {
+        const int e = ids[t * topk + j];
+        if (e < 0 || e >= num_experts) continue;
+      }
+      const u32x4 x = *reinterpret_cast<const u32x4*>(src + j * k);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[2 * q] += __uint_as_float(x[q] << 16);
+        acc[2 * q + 1] += __uint_as_float(x[q] & 0xffff0000u);
+      }
+    }
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
+    *reinterpret_cast<u32x4*>(out + t * k + c) = o;
+  }
+}
+
+// ------------------------------------------------------ fp8 group quant ---
+// One wave per (row, group of `group` columns); group % 8 == 0, group <= 512.
+// scale = max(amax, 1e-10) / 448; q = e4m3fn(clamp(x / scale, +-448)).
+__global__ __launch_bounds__(256) void quant_fp8_group_kernel(
+    const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
+    float* __restrict__ scales, int64_t rows, int64_t cols, int group) {
+  const int lane = threadIdx.x & 63;
+  const int64_t groups_per_row = cols / group;
+  const int64_t n_items = rows * groups_per_row;
+  const int64_t item = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / 64;
+  if (item >= n_items) return;
+  const int64_t r = item / groups_per_row;
+  const int64_t g = item - r * groups_per_row;
+  const uint16_t* src = x + r * cols + g * group;
+  uint8_t* dst = q + r * cols + g * group;
+  // Each lane holds up to 8 columns.
+  const bool active = lane * 8 < group;
+  float v[8];
+  float amax = 0.f;
+  if (active) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(src + lane * 8);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = __uint_as_float(w[j] << 16);
+      v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  const float scale = fmaxf(amax, 1e-10f) / 448.0f;
+  if (active) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = fminf(fmaxf(v[2 * j] / scale, -448.f), 448.f);
+      const float b = fminf(fmaxf(v[2 * j + 1] / scale, -448.f), 448.f);
+      const uint32_t p = cvt_pk_fp8(a, b);
+      if (j < 2)
+        lo |= p << (16 * j);
+      else
+        hi |= p << (16 * (j - 2));
+    }
+    uint2 o;
+    o.x = lo;
+    o.y = hi;
+    *reinterpret_cast<uint2*>(dst + lane * 8) = o;
+  }
+  if (lane == 0) scales[r * groups_per_row + g] = scale;
+}
+
+// ----------------------------------------------------- int8 token quant ---
+// One workgroup (256 threads) per row; cols % 8 == 0.
+// scale = max(amax, 1e-10) / 127; q = clamp(rne(x / scale), -127, 127).
+__global__ __launch_bounds__(256) void quant_int8_token_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+    float* __restrict__ scales, int64_t cols) {
+  const int64_t r = blockIdx.x;
+  const uint16_t* src = x + r * cols;
+  int8_t* dst = q + r * cols;
+  float amax = 0.f;
+  for (int64_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(src + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      amax = fmaxf(amax, fabsf(__uint_as_float(w[j] << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(w[j] & 0xffff0000u)));
+    }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float scale = fmaxf(amax, 1e-10f) / 127.0f;
+  for (int64_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(src + c);
+    uint32_t packed[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = (j & 1) ? __uint_as_float(w[j / 2] & 0xffff0000u)
+                              : __uint_as_float(w[j / 2] << 16);
+      float rq = __builtin_rintf(f / scale);
+      rq = fminf(fmaxf(rq, -127.f), 127.f);
+      const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(rq)) & 0xffu;
+      packed[j / 4] |= b << (8 * (j & 3));
+    }
+    uint2 o;
+    o.x = packed[0];
+    o.y = packed[1];
+    *reinterpret_cast<uint2*>(dst + c) = o;
+  }
+  if (threadIdx.x == 0) scales[r] = scale;
+}
+
+// ------------------------------------------------------------- launchers ---
+static unsigned grid_for(int64_t work_items, int threads) {
+  int64_t g = (work_items + threads - 1) / threads;
+  const int64_t cap = 256 * 64;  // enough waves to fill 256 CUs many times
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return static_cast<unsigned>(g);
+}
+
+int launch_silu_and_mul(const void* in, void* out, int64_t rows, int64_t n,
+                        hipStream_t stream) {
+  if (rows == 0) return FGS_OK;
+  hipLaunchKernelGGL(silu_and_mul_kernel, dim3(grid_for(rows * (n / 8), 256)),
+                     dim3(256), 0, stream, static_cast<const uint16_t*>(in),
+                     static_cast<uint16_t*>(out), rows, n);
+  return check_launch("silu_and_mul_kernel");
+}
+
+int launch_moe_sum(const void* in, void* out, int64_t m, int topk, int64_t k,
+                   hipStream_t stream) {
+  if (m == 0) return FGS_OK;
+  hipLaunchKernelGGL(moe_sum_kernel, dim3(grid_for(m * (k / 8), 256)),
+                     dim3(256), 0, stream, static_cast<const uint16_t*>(in),
+                     static_cast<uint16_t*>(out), m, topk, k, nullptr, 0);
+  return check_launch("moe_sum_kernel");
+}
+
+int launch_moe_sum_routed(const void* in, void* out, int64_t m, int topk,
+                          int64_t k, const int32_t* ids, int num_experts,
+                          hipStream_t stream) {
+  if (m == 0) return FGS_OK;
+  hipLaunchKernelGGL(moe_sum_kernel, dim3(grid_for(m * (k / 8), 256)),
+                     dim3(256), 0, stream, static_cast<const uint16_t*>(in),
+                     static_cast<uint16_t*>(out), m, topk, k, ids, num_experts);
+  return check_launch("moe_sum_kernel");
+}
+
+int launch_quant_fp8_group(const void* x, void* q, float* scales,
+                           int64_t rows, int64_t cols, int group,
+                           hipStream_t stream) {
+  const int64_t items = rows * (cols / group);
+  if (items == 0) return FGS_OK;
+  const int64_t blocks = (items * 64 + 255) / 256;
+  hipLaunchKernelGGL(quant_fp8_group_kernel, dim3(static_cast<unsigned>(blocks)),
+                     dim3(256), 0, stream, static_cast<const uint16_t*>(x),
+                     static_cast<uint8_t*>(q), scales, rows, cols, group);
+  return check_launch("quant_fp8_group_kernel");
+}
+
+int launch_quant_int8_token(const void* x, int8_t* q, float* scales,
+                            int64_t rows, int64_t cols, hipStream_t stream) {
+  if (rows == 0) return FGS_OK;
+  hipLaunchKernelGGL(quant_int8_token_kernel, dim3(static_cast<unsigned>(rows)),
+                     dim3(256), 0, stream, static_cast<const uint16_t*>(x), q,
+                     scales, cols);
+  return check_launch("quant_int8_token_kernel");
+}
+
+}  // namespace fgs

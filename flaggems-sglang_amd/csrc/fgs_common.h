@@ -1,0 +1,90 @@
+// Shared definitions of the gfx950 fused-MoE kernels: vector types, MFMA
+// wrappers, bf16 / fp8 conversions and the host-side error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "fgs_moe.h"
+
+namespace fgs {
+
+// ---------------------------------------------------------------- types ----
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+
+constexpr int kWave = 64;
+
+// bf16 is carried as its 16-bit pattern in memory; conversions are explicit.
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even f32 -> bf16 bit pattern (NaN stays a quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+    return static_cast<uint16_t>((u >> 16) | 0x40);
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) |
+         (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+}
+
+// silu(g) * u in fp32, the activation of the reference's
+// _silu_and_mul_kernel (ops/fused_moe.py:58-62): g / (1 + exp(-g)) * u.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g / (1.0f + __expf(-g)) * u;
+}
+
+// ------------------------------------------------------------------ MFMA ---
+// v_mfma_f32_16x16x32_bf16: A 16x32, B 32x16, C 16x16 fp32.
+// Lane l holds A row (l & 15) / B column (l & 15), eight consecutive
+// k values of lane group (l >> 4); C: column (l & 15), rows 4*(l>>4)+i.
+__device__ __forceinline__ f32x4 mfma16_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_32x32x16_bf16: A 32x16, B 16x32, C 32x32 fp32 in 16 regs.
+// Lane l holds A row (l & 31), k values 8*(l>>5)..+7; C column (l & 31),
+// rows 8*(i>>2) + 4*(l>>5) + (i&3) for register i.
+__device__ __forceinline__ f32x16 mfma32_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_16x16x128_f8f6f4 with both operands OCP e4m3 (format 0) and
+// unit (e8m0 = 127) block scales: A 16x128, B 128x16, 32 bytes per lane.
+__device__ __forceinline__ f32x4 mfma16_fp8(i32x8 a, i32x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0,
+                                                          127, 0, 127);
+}
+
+// v_mfma_i32_16x16x64_i8: A 16x64, B 64x16 int8, 16 bytes per lane.
+__device__ __forceinline__ i32x4 mfma16_i8(i32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------ fp8 e4m3fn ---
+// Two floats -> two OCP e4m3fn bytes (hardware RNE conversion on gfx950),
+// placed in the low 16 bits of the result.
+__device__ __forceinline__ uint32_t cvt_pk_fp8(float a, float b) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false)) &
+         0xffffu;
+}
+
+// --------------------------------------------------------- host helpers ---
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+}  // namespace fgs

@@ -1,0 +1,57 @@
+// Internal interface between the C-ABI layer (capi.hip) and the kernel
+// translation units. Nothing here is exported from libfgs_moe.so.
+#pragma once
+
+#include "fgs_common.h"
+
+namespace fgs {
+
+enum : int { kDtBf16 = 0, kDtFp8 = 1, kDtInt8 = 2 };
+
+// One grouped GEMM over the expert-sorted, block-padded row order.
+//   GEMM1: a = activations [m, kdim] gathered by token = sorted_id / topk,
+//          w = w13 [E, 2*n_out, kdim], out = a2 bf16 [rows_pad, n_out].
+//   GEMM2: a = a2 [rows_pad, kdim] (row = padded position),
+//          w = w2 [E, n_out, kdim], out = per-slot y bf16 [numel, n_out].
+struct GemmParams {
+  const uint8_t* a;
+  const float* a_scale;   // fp8: [rows, kdim/128]; int8: [rows]; else null
+  const uint8_t* w;
+  const float* w_scale;   // fp8: [E, nrows_w/128, kdim/128]; int8: [E, nrows_w]
+  const int32_t* sorted_ids;
+  const int32_t* expert_ids;
+  const int32_t* num_post_pad;
+  const float* topk_w;    // [numel]
+  void* out;
+  int64_t kdim;
+  int64_t n_out;
+  int64_t nrows_w;
+  int64_t numel;
+  int32_t topk;
+  int32_t weight_on_input;
+};
+
+size_t align_smem_bytes(int num_experts);
+int launch_align(const int32_t* ids, int64_t numel, int num_experts,
+                 int block_size, int32_t* sorted_ids, int32_t* expert_ids,
+                 int32_t* num_post_pad, int64_t max_padded, hipStream_t stream);
+
+int launch_silu_and_mul(const void* in, void* out, int64_t rows, int64_t n,
+                        hipStream_t stream);
+int launch_moe_sum(const void* in, void* out, int64_t m, int topk, int64_t k,
+                   hipStream_t stream);
+int launch_moe_sum_routed(const void* in, void* out, int64_t m, int topk,
+                          int64_t k, const int32_t* ids, int num_experts,
+                          hipStream_t stream);
+int launch_quant_fp8_group(const void* x, void* q, float* scales, int64_t rows,
+                           int64_t cols, int group, hipStream_t stream);
+int launch_quant_int8_token(const void* x, int8_t* q, float* scales,
+                            int64_t rows, int64_t cols, hipStream_t stream);
+
+// k elements per pipeline step of the streaming kernels (kdim must be a
+// multiple of it).
+int stream_step_k(int dt);
+int launch_gemm_stream(int dt, bool gemm1, const GemmParams& p, int mt, int kw,
+                       int row_blocks, hipStream_t stream);
+
+}  // namespace fgs

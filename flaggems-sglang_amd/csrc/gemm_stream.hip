@@ -1,0 +1,342 @@
+// Streaming grouped GEMMs of the fused-MoE path (decode regime: few rows per
+// expert, the layer is bound by reading every touched expert's weights once).
+//
+// A workgroup owns one row block (16*MT rows of the expert-sorted, padded
+// order from moe_align_block_size) and one 16-column output tile. Its KW
+// waves split the contraction; each wave streams its share of the 16 (or,
+// for GEMM1, 16 gate + 16 up) weight rows straight from HBM into MFMA
+// operand registers, with no LDS staging: every lane reads LB contiguous
+// bytes of one weight row per step, the four lane groups of a row cover
+// 4*LB contiguous bytes. The MFMA k index is only a label, so activations
+// are read with the identical lane -> k mapping and the contraction is
+// exact. Partial sums meet in LDS; wave 0 runs the epilogue:
+//   GEMM1 (replaces matmul_ogs with gather + _silu_and_mul_triton,
+//          ops/fused_moe.py:205-218): a2[row, c] = bf16(silu(g) * u)
+//   GEMM2 (replaces matmul_ogs with scatter + gammas, :224-231):
+//          y[slot, c] = bf16(gamma[slot] * acc)   (top-k sum: moe_sum)
+#include "fgs_moe_kernels.h"
+
+namespace fgs {
+
+template <int DT>
+struct StreamTraits;
+
+// bf16: 16x16x32 MFMA, 16 B per lane per MFMA, 4 MFMAs per 128-k step.
+template <>
+struct StreamTraits<kDtBf16> {
+  static constexpr int kLaneBytes = 64;           // bytes per lane per step
+  static constexpr int kStepK = 128;              // k elements per step
+  static constexpr int kVecs = kLaneBytes / 16;   // u32x4 per lane per step
+  typedef f32x4 Acc;
+};
+// fp8 e4m3: 16x16x128 MFMA, 32 B per lane, one MFMA per 128-k scale group.
+template <>
+struct StreamTraits<kDtFp8> {
+  static constexpr int kLaneBytes = 32;
+  static constexpr int kStepK = 128;
+  static constexpr int kVecs = 2;
+  typedef f32x4 Acc;
+};
+// int8: 16x16x64 MFMA, 16 B per lane per MFMA, 4 MFMAs per 256-k step.
+template <>
+struct StreamTraits<kDtInt8> {
+  static constexpr int kLaneBytes = 64;
+  static constexpr int kStepK = 256;
+  static constexpr int kVecs = 4;
+  typedef i32x4 Acc;
+};
+
+template <int DT, int NV>
+__device__ __forceinline__ void load_frag(u32x4 (&f)[NV], const uint8_t* p,
+                                          bool valid) {
+  if (valid) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+      f[v] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + v);
+  } else {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) f[v] = u32x4{0, 0, 0, 0};
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void load_act(u32x4 (&f)[NV], const uint8_t* p,
+                                         bool valid) {
+  if (valid) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) f[v] = reinterpret_cast<const u32x4*>(p)[v];
+  } else {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) f[v] = u32x4{0, 0, 0, 0};
+  }
+}
+
+template <int DT, int NV>
+__device__ __forceinline__ void mma_step(f32x4& acc, const u32x4 (&a)[NV],
+                                         const u32x4 (&b)[NV]) {
+  if constexpr (DT == kDtBf16) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+      acc = mfma16_bf16(__builtin_bit_cast(bf16x8, a[v]),
+                        __builtin_bit_cast(bf16x8, b[v]), acc);
+  }
+}
+
+template <int DT, int NV>
+__device__ __forceinline__ void mma_step_i8(i32x4& acc, const u32x4 (&a)[NV],
+                                            const u32x4 (&b)[NV]) {
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+    acc = mfma16_i8(__builtin_bit_cast(i32x4, a[v]),
+                    __builtin_bit_cast(i32x4, b[v]), acc);
+}
+
+__device__ __forceinline__ f32x4 mma_fp8(const u32x4 (&a)[2],
+                                         const u32x4 (&b)[2]) {
+  i32x8 av, bv;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    av[j] = static_cast<int>(a[0][j]);
+    av[4 + j] = static_cast<int>(a[1][j]);
+    bv[j] = static_cast<int>(b[0][j]);
+    bv[4 + j] = static_cast<int>(b[1][j]);
+  }
+  return mfma16_fp8(av, bv, f32x4{0.f, 0.f, 0.f, 0.f});
+}
+
+template <int DT, int MT, int KW, bool GEMM1>
+__global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
+    const GemmParams p) {
+  typedef StreamTraits<DT> T;
+  typedef typename T::Acc Acc;
+  constexpr int NB = GEMM1 ? 2 : 1;  // weight row groups: gate/up or one
+  constexpr int NV = T::kVecs;
+  constexpr int ESZ = (DT == kDtBf16) ? 2 : 1;
+  constexpr int BM = 16 * MT;
+
+  const int rb = blockIdx.x;
+  const int n0 = blockIdx.y * 16;
+  if (rb * BM >= p.num_post_pad[0]) return;
+  const int e = p.expert_ids[rb];
+  if (e < 0) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int ln = lane & 15;
+  const int lg = lane >> 4;
+
+  // Activation row of lane ln in each row tile.
+  const uint8_t* arow[MT];
+  bool avalid[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int r = rb * BM + mt * 16 + ln;
+    const int sid = p.sorted_ids[r];
+    avalid[mt] = sid < p.numel;
+    const int64_t src = GEMM1 ? (avalid[mt] ? sid / p.topk : 0) : r;
+    arow[mt] = p.a + (src * p.kdim) * ESZ + lg * T::kLaneBytes;
+  }
+  // Weight rows of lane ln.
+  const uint8_t* brow[NB];
+  const int64_t wbase = static_cast<int64_t>(e) * p.nrows_w;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int64_t n = wbase + (nb ? p.n_out : 0) + n0 + ln;
+    brow[nb] = p.w + (n * p.kdim) * ESZ + lg * T::kLaneBytes;
+  }
+
+  // fp8 / int8 activation scales of this lane's accumulator rows.
+  int64_t crow[MT][4];
+  bool cvalid[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rb * BM + mt * 16 + lg * 4 + i;
+      const int sid = p.sorted_ids[r];
+      cvalid[mt][i] = sid < p.numel;
+      crow[mt][i] = GEMM1 ? (cvalid[mt][i] ? sid / p.topk : 0) : r;
+    }
+
+  Acc acc[NB][MT];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[nb][mt] = Acc{0, 0, 0, 0};
+
+  const int steps = static_cast<int>(p.kdim / T::kStepK);
+  const int s0 = wave * steps / KW;
+  const int s1 = (wave + 1) * steps / KW;
+  const int64_t step_bytes = static_cast<int64_t>(T::kStepK) * ESZ;
+  const int kblocks = static_cast<int>(p.kdim / 128);
+
+  u32x4 bf[2][NB][NV];
+  u32x4 af[2][MT][NV];
+  if (s0 < s1) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      load_frag<DT>(bf[0][nb], brow[nb] + s0 * step_bytes, true);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      load_act(af[0][mt], arow[mt] + s0 * step_bytes, avalid[mt]);
+  }
+  for (int s = s0; s < s1; s += 2) {
+    // Two-deep register pipeline: fetch s+1 while s is multiplied.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int cur = s + h;
+      if (cur >= s1) break;
+      const int nxt = cur + 1;
+      if (nxt < s1) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          load_frag<DT>(bf[h ^ 1][nb], brow[nb] + nxt * step_bytes, true);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          load_act(af[h ^ 1][mt], arow[mt] + nxt * step_bytes, avalid[mt]);
+      }
+      if constexpr (DT == kDtBf16) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            mma_step<DT>(acc[nb][mt], af[h][mt], bf[h][nb]);
+      } else if constexpr (DT == kDtInt8) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            mma_step_i8<DT>(acc[nb][mt], af[h][mt], bf[h][nb]);
+      } else {
+        // fp8 block scales: one 128-k group per step.
+        const int kb = cur;
+        float sw[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int64_t wrow = (nb ? p.n_out : 0) + n0;
+          sw[nb] = p.w_scale[(static_cast<int64_t>(e) * (p.nrows_w / 128) +
+                              wrow / 128) * kblocks + kb];
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          float sa[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            sa[i] = cvalid[mt][i] ? p.a_scale[crow[mt][i] * kblocks + kb] : 0.f;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const f32x4 t = mma_fp8(af[h][mt], bf[h][nb]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[nb][mt][i] += t[i] * (sa[i] * sw[nb]);
+          }
+        }
+      }
+    }
+  }
+
+  // Cross-wave reduction of the split contraction.
+  __shared__ Acc red[KW > 1 ? KW - 1 : 1][NB][MT][64];
+  if (KW > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[wave - 1][nb][mt][lane] = acc[nb][mt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < KW - 1; ++w)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[nb][mt] += red[w][nb][mt][lane];
+  }
+
+  // Epilogue (wave 0): lane owns column n0+ln, rows lg*4+i of each tile.
+  const int col = n0 + ln;
+  uint16_t* out = static_cast<uint16_t*>(p.out);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = rb * BM + mt * 16 + lg * 4 + i;
+      const bool valid = cvalid[mt][i];
+      const int sid = p.sorted_ids[r];
+      float v[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        float x;
+        if constexpr (DT == kDtInt8) {
+          const float sa = valid ? p.a_scale[crow[mt][i]] : 0.f;
+          const float sw = p.w_scale[static_cast<int64_t>(e) * p.nrows_w +
+                                     (nb ? p.n_out : 0) + col];
+          x = static_cast<float>(acc[nb][mt][i]) * sa * sw;
+        } else {
+          x = acc[nb][mt][i];
+        }
+        v[nb] = x;
+      }
+      if constexpr (GEMM1) {
+        float g = v[0], u = v[NB - 1];
+        if (p.weight_on_input && valid) {
+          const float gm = p.topk_w[sid];
+          g *= gm;
+          u *= gm;
+        }
+        out[static_cast<int64_t>(r) * p.n_out + col] =
+            f32_to_bf16_bits(silu_mul(g, u));
+      } else {
+        if (valid) {
+          float y = v[0];
+          if (!p.weight_on_input) y *= p.topk_w[sid];
+          out[static_cast<int64_t>(sid) * p.n_out + col] = f32_to_bf16_bits(y);
+        }
+      }
+    }
+  }
+}
+
+template <int DT, int MT, int KW, bool GEMM1>
+static int launch_one(const GemmParams& p, int row_blocks, hipStream_t stream) {
+  dim3 grid(row_blocks, static_cast<unsigned>(p.n_out / 16));
+  hipLaunchKernelGGL((moe_gemm_stream_kernel<DT, MT, KW, GEMM1>), grid,
+                     dim3(KW * 64), 0, stream, p);
+  return check_launch("moe_gemm_stream_kernel");
+}
+
+template <int DT, bool GEMM1>
+static int dispatch_kw(const GemmParams& p, int mt, int kw, int row_blocks,
+                       hipStream_t stream) {
+#define FGS_CASE(MT_, KW_)                                           \
+  if (mt == MT_ && kw == KW_)                                        \
+    return launch_one<DT, MT_, KW_, GEMM1>(p, row_blocks, stream);
+  FGS_CASE(1, 1) FGS_CASE(1, 2) FGS_CASE(1, 4) FGS_CASE(1, 8)
+  FGS_CASE(2, 1) FGS_CASE(2, 2) FGS_CASE(2, 4) FGS_CASE(2, 8)
+  FGS_CASE(4, 1) FGS_CASE(4, 2) FGS_CASE(4, 4) FGS_CASE(4, 8)
+#undef FGS_CASE
+  return fail(FGS_EUNSUPPORTED, "stream GEMM: no kernel for this tile");
+}
+
+int stream_step_k(int dt) {
+  return dt == kDtInt8 ? StreamTraits<kDtInt8>::kStepK : 128;
+}
+
+int launch_gemm_stream(int dt, bool gemm1, const GemmParams& p, int mt, int kw,
+                       int row_blocks, hipStream_t stream) {
+  if (row_blocks <= 0) return FGS_OK;
+  switch (dt) {
+    case kDtBf16:
+      return gemm1 ? dispatch_kw<kDtBf16, true>(p, mt, kw, row_blocks, stream)
+                   : dispatch_kw<kDtBf16, false>(p, mt, kw, row_blocks, stream);
+    case kDtFp8:
+      return gemm1 ? dispatch_kw<kDtFp8, true>(p, mt, kw, row_blocks, stream)
+                   : dispatch_kw<kDtFp8, false>(p, mt, kw, row_blocks, stream);
+    case kDtInt8:
+      return gemm1 ? dispatch_kw<kDtInt8, true>(p, mt, kw, row_blocks, stream)
+                   : dispatch_kw<kDtInt8, false>(p, mt, kw, row_blocks, stream);
+  }
+  return fail(FGS_EUNSUPPORTED, "stream GEMM: unknown dtype");
+}
+
+}  // namespace fgs

@@ -1,0 +1,196 @@
+/*
+ * fgs_moe.h -- C ABI of the MI355X (gfx950) fused-MoE library `libfgs_moe.so`.
+ *
+ * The library replaces the fused-MoE operator path of FlagGems-sglang
+ * (reference: src/flaggems_sglang/ops/fused_moe.py). The reference has no
+ * native FFI of its own -- its Python entry points launch Triton JIT kernels
+ * and call `triton_kernels.matmul_ogs`. Each entry point below names the
+ * reference function (file:line) whose work it takes over; the Python host
+ * layer (flaggems_sglang.ops.fused_moe) binds them with ctypes.
+ *
+ * Conventions
+ *   - Plain pointers to device memory and plain integer sizes. bf16 tensors
+ *     are passed as `void*` (IEEE bfloat16, little endian); fp8 tensors are
+ *     OCP e4m3fn bytes (max 448); int8 tensors are two's complement.
+ *   - `stream` is a `hipStream_t` passed as `void*` (NULL = legacy stream).
+ *   - Every launching entry point is asynchronous and stream ordered. The
+ *     library never allocates or frees device memory and never synchronises;
+ *     scratch memory comes in through the caller's `workspace` argument,
+ *     sized with fgs_moe_workspace_bytes().
+ *   - All arguments are validated on the host before any launch. Return
+ *     codes: FGS_OK (0); FGS_EINVAL (-1) invalid argument; FGS_EUNSUPPORTED
+ *     (-2) valid but unsupported combination; FGS_ELAUNCH (-3) HIP error.
+ *     fgs_moe_last_error() returns the message of the calling thread's last
+ *     failure.
+ *   - Thread-safe and re-entrant: no mutable globals besides the
+ *     thread-local error string and device properties cached once.
+ */
+#ifndef FGS_MOE_H_
+#define FGS_MOE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FGS_OK 0
+#define FGS_EINVAL (-1)
+#define FGS_EUNSUPPORTED (-2)
+#define FGS_ELAUNCH (-3)
+
+/* Quantisation modes (`qmode` arguments). */
+#define FGS_QMODE_BF16 0        /* bf16 weights and activations               */
+#define FGS_QMODE_FP8_BLOCK 1   /* e4m3fn w8a8, 128x128 weight blocks, 1x128  */
+#define FGS_QMODE_INT8_CHANNEL 2 /* int8 w8a8, per-channel w, per-token a     */
+
+/* `flags` bits of the fused entry points. */
+#define FGS_FLAG_ROUTER_WEIGHT_ON_INPUT 0x1 /* gammas on GEMM1 output rows */
+#define FGS_FLAG_FORCE_DECODE 0x100         /* schedule: streaming kernels  */
+#define FGS_FLAG_FORCE_PREFILL 0x200        /* schedule: LDS-tiled kernels  */
+
+/* Library version string, e.g. "fgs_moe 0.1.0 gfx950". */
+const char* fgs_moe_version(void);
+
+/* Message of the calling thread's most recent failed call ("" if none). */
+const char* fgs_moe_last_error(void);
+
+/* Size of the padded sorted-id buffer the alignment writes:
+ * numel + num_experts * (block_size - 1). Returns -1 on invalid input. */
+int64_t fgs_moe_align_max_padded(int64_t numel, int32_t num_experts,
+                                 int32_t block_size);
+
+/* moe_align_block_size: expert-grouped, block-padded routing order.
+ * Replaces the routing conversion of _standard_topk_to_triton_kernels
+ * (ops/fused_moe.py:119-146: stable argsort :134, histogram :137-139).
+ *   topk_ids     int32 [numel] (numel = M * topk), expert id per slot.
+ *   sorted_ids   int32 [max_padded]: for each expert e in ascending order,
+ *                the flat slot indices i with topk_ids[i] == e in ascending
+ *                i (stable), then pad entries = numel up to a multiple of
+ *                block_size; entries past the padded total are numel too.
+ *   expert_ids   int32 [max_padded / block_size]: expert of each block,
+ *                -1 past the padded total.
+ *   num_post_pad int32 [1]: padded total.
+ * Slots whose id is outside [0, num_experts) are dropped (not routed).
+ * Bit-exact and deterministic (no atomics decide any order). */
+int32_t fgs_moe_align_block_size(const int32_t* topk_ids, int64_t numel,
+                                 int32_t num_experts, int32_t block_size,
+                                 int32_t* sorted_ids, int32_t* expert_ids,
+                                 int32_t* num_post_pad, int64_t max_padded,
+                                 void* stream);
+
+/* silu_and_mul: out[r, c] = bf16(silu(f32(in[r, c])) * f32(in[r, n + c])).
+ * in bf16 [rows, 2n], out bf16 [rows, n].
+ * Replaces _silu_and_mul_triton / _silu_and_mul_kernel
+ * (ops/fused_moe.py:44-63, 88-116). */
+int32_t fgs_moe_silu_and_mul(const void* in, void* out, int64_t rows,
+                             int64_t n, void* stream);
+
+/* moe_sum: out[t, c] = bf16(sum_j f32(in[t, j, c])), in bf16 [m, topk, k],
+ * out bf16 [m, k]. Replaces the top-k reduction that matmul_ogs performs
+ * with `scatter_indx` (ops/fused_moe.py:224-231). */
+int32_t fgs_moe_sum(const void* in, void* out, int64_t m, int32_t topk,
+                    int64_t k, void* stream);
+
+/* Dynamic per-(row, group) fp8 quantisation: x bf16 [rows, cols],
+ * q e4m3fn [rows, cols], scales f32 [rows, cols / group] with
+ * scale = max(amax, 1e-10) / 448 and q = e4m3fn(clamp(x / scale, +-448)).
+ * No reference counterpart (the reference asserts fp8 off,
+ * ops/fused_moe.py:170-172); needed by the fp8 w8a8 path. */
+int32_t fgs_moe_quant_fp8_group(const void* x, void* q, float* scales,
+                                int64_t rows, int64_t cols, int32_t group,
+                                void* stream);
+
+/* Dynamic per-row int8 quantisation: scale = max(amax, 1e-10) / 127,
+ * q = clamp(rne(x / scale), -127, 127). x bf16 [rows, cols], q int8,
+ * scales f32 [rows]. No reference counterpart (ops/fused_moe.py:173-175
+ * asserts per-channel quant off); needed by the int8 w8a8 path. */
+int32_t fgs_moe_quant_int8_token(const void* x, int8_t* q, float* scales,
+                                 int64_t rows, int64_t cols, void* stream);
+
+/* Workspace bytes one fused call needs for the given problem.
+ * m tokens, hidden K, inter N (per-expert intermediate), num_experts E,
+ * topk, qmode, flags (schedule bits matter). Returns -1 on invalid input. */
+int64_t fgs_moe_workspace_bytes(int64_t m, int64_t hidden, int64_t inter,
+                                int32_t num_experts, int32_t topk,
+                                int32_t qmode, int32_t flags);
+
+/* Host-only validation of a problem (no device access). Returns FGS_OK or
+ * the status and message the fused entry point would return. */
+int32_t fgs_moe_validate(int64_t m, int64_t hidden, int64_t inter,
+                         int32_t num_experts, int32_t topk, int32_t qmode,
+                         int32_t flags, int64_t ws_bytes);
+
+/* Fused MoE, bf16. Replaces triton_kernel_fused_experts
+ * (ops/fused_moe.py:149-232): routing conversion, GEMM1 (matmul_ogs with
+ * gather, :205-212), silu_and_mul (:214-218), GEMM2 with top-k gammas and
+ * scatter-reduce (:224-231).
+ *   x            bf16 [m, hidden]
+ *   w13          bf16 [E, 2*inter, hidden]  (gate rows 0..inter-1, then up)
+ *   w2           bf16 [E, hidden, inter]
+ *   topk_weights f32  [m, topk]
+ *   topk_ids     int32 [m, topk]
+ *   out          bf16 [m, hidden]
+ *   out = sum_j w[t,j] * (silu(x W13g^T) * (x W13u^T)) W2^T  per token.
+ * With FGS_FLAG_ROUTER_WEIGHT_ON_INPUT the gamma scales the GEMM1 output
+ * rows (before the activation) and GEMM2 is unweighted
+ * (ops/fused_moe.py:202-203). */
+int32_t fgs_moe_fused_bf16(const void* x, const void* w13, const void* w2,
+                           const float* topk_weights, const int32_t* topk_ids,
+                           int64_t m, int64_t hidden, int64_t inter,
+                           int32_t num_experts, int32_t topk, int32_t flags,
+                           void* workspace, int64_t ws_bytes, void* out,
+                           void* stream);
+
+/* Fused MoE, fp8 w8a8 with block scales (block_n = block_k = 128).
+ *   w13 e4m3fn [E, 2*inter, hidden], w13_scale f32 [E, 2*inter/128, hidden/128]
+ *   w2  e4m3fn [E, hidden, inter],   w2_scale  f32 [E, hidden/128, inter/128]
+ * Activations (x and the GEMM1 output) are quantised dynamically per 1x128
+ * group inside the call. No reference counterpart: the reference rejects
+ * use_fp8_w8a8 / w*_scale / block_shape (ops/fused_moe.py:170-185). */
+int32_t fgs_moe_fused_fp8_block(const void* x, const void* w13,
+                                const void* w2, const float* w13_scale,
+                                const float* w2_scale, int32_t block_n,
+                                int32_t block_k, const float* topk_weights,
+                                const int32_t* topk_ids, int64_t m,
+                                int64_t hidden, int64_t inter,
+                                int32_t num_experts, int32_t topk,
+                                int32_t flags, void* workspace,
+                                int64_t ws_bytes, void* out, void* stream);
+
+/* Fused MoE, int8 w8a8 with per-output-channel weight scales.
+ *   w13 int8 [E, 2*inter, hidden], w13_scale f32 [E, 2*inter]
+ *   w2  int8 [E, hidden, inter],   w2_scale  f32 [E, hidden]
+ * Activations are quantised dynamically per token (row) inside the call.
+ * No reference counterpart (per_channel_quant asserted off,
+ * ops/fused_moe.py:173-175). */
+int32_t fgs_moe_fused_int8_channel(const void* x, const void* w13,
+                                   const void* w2, const float* w13_scale,
+                                   const float* w2_scale,
+                                   const float* topk_weights,
+                                   const int32_t* topk_ids, int64_t m,
+                                   int64_t hidden, int64_t inter,
+                                   int32_t num_experts, int32_t topk,
+                                   int32_t flags, void* workspace,
+                                   int64_t ws_bytes, void* out, void* stream);
+
+/* Stage timing for benchmarks. No reference counterpart (the reference
+ * times the whole op with triton.testing.do_bench,
+ * benchmark/performance_utils.py:365-377). While enabled on the calling
+ * thread, every fused call records HIP events on its stream between its
+ * stages: 0 alignment, 1 activation quantisation, 2 GEMM1 (+activation),
+ * 3 GEMM2-input quantisation, 4 GEMM2, 5 top-k sum. Stages a mode does not
+ * run read ~0. */
+#define FGS_PROFILE_STAGES 6
+int32_t fgs_moe_profile_enable(int32_t on);
+
+/* Waits for the recorded events, writes the mean milliseconds of each stage
+ * over the calls recorded since the last read into stage_ms[0..n_stages),
+ * clears the record and returns the number of calls averaged (or < 0). */
+int32_t fgs_moe_profile_read(float* stage_ms, int32_t n_stages);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* FGS_MOE_H_ */

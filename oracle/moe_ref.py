@@ -1,0 +1,260 @@
+"""CPU oracle of the fused-MoE path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may import this module; the product path
+(``flaggems_sglang``) never does.
+
+It restates, on the CPU in torch fp32 (plus the C alignment in
+``align_ref.c``), what the reference path computes:
+
+* routing: softmax / sigmoid -> top-k -> renormalise
+  (reference tests/test_fused_moe.py:37-41);
+* alignment: stable expert grouping (src/flaggems_sglang/ops/fused_moe.py:
+  130-139), via ``align_ref.c``;
+* ``silu_and_mul`` (ops/fused_moe.py:44-63, fp32 math, bf16 store);
+* the fused expert computation (ops/fused_moe.py:197-232) with the rounding
+  points of an unfused pipeline: GEMM1 output rounded to bf16, activation
+  rounded to bf16, GEMM2 output rounded to bf16, fp32 weighted top-k sum
+  rounded to bf16. ``apply_router_weight_on_input`` puts the gate scale on the
+  GEMM1 output rows (:202-203, gammas of the first matmul_ogs call);
+* fp8 / int8 w8a8: the reference rejects them (ops/fused_moe.py:170-185); the
+  quantisers and dequantising MoE here define them: e4m3fn with 128x128
+  weight blocks and 1x128 activation groups (scale = max(amax, 1e-10)/448),
+  int8 with per-output-channel weight scales and per-token activation scales
+  (scale = max(amax, 1e-10)/127, round half to even).
+
+How each function is pinned (closed forms, brute force, library routines,
+invariants) is listed in tests/test_oracle.py. ``_standard_topk_to_triton_kernels``'s
+``compute_expt_data_torch`` metadata and ``matmul_ogs``'s exact accumulation
+order live in the un-vendored ``triton_kernels`` package and are not
+restated: parity of the GEMM arithmetic is to tolerance, not bit-exact.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+_lib = None
+
+FP8_MAX = 448.0
+INT8_MAX = 127.0
+QUANT_EPS = 1e-10
+
+
+def _clib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle library missing: run `make -C {_HERE}`")
+        lib = ctypes.CDLL(_LIB_PATH)
+        lib.oracle_align.restype = ctypes.c_int
+        lib.oracle_align.argtypes = [
+            ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+        ]
+        _lib = lib
+    return _lib
+
+
+# --------------------------------------------------------------- routing ---
+def route(logits: torch.Tensor, topk: int, scoring: str = "softmax",
+          renormalize: bool = True):
+    """``(topk_weights f32 [M, k], topk_ids int32 [M, k])`` from router logits
+    (reference tests/test_fused_moe.py:37-41; sigmoid scoring for the
+    DeepSeek-shaped config)."""
+    logits = logits.float()
+    if scoring == "softmax":
+        scores = torch.softmax(logits, dim=-1)
+    elif scoring == "sigmoid":
+        scores = torch.sigmoid(logits)
+    else:
+        raise ValueError(scoring)
+    w, ids = torch.topk(scores, k=topk, dim=-1)
+    if renormalize:
+        w = w / w.sum(dim=-1, keepdim=True)
+    return w.float(), ids.to(torch.int32)
+
+
+# ------------------------------------------------------------- alignment ---
+def align(topk_ids, num_experts: int, block_size: int):
+    """Stable block-padded expert grouping (C restatement in align_ref.c).
+    Returns numpy ``(sorted_ids, expert_ids, num_post_pad)``."""
+    ids = np.ascontiguousarray(np.asarray(topk_ids, dtype=np.int32).reshape(-1))
+    numel = ids.size
+    max_padded = numel + num_experts * (block_size - 1)
+    sorted_ids = np.empty(max_padded, dtype=np.int32)
+    expert_ids = np.empty(max(max_padded // block_size, 1), dtype=np.int32)
+    npp = np.zeros(1, dtype=np.int32)
+    rc = _clib().oracle_align(
+        ids.ctypes.data, numel, num_experts, block_size, sorted_ids.ctypes.data,
+        expert_ids.ctypes.data, npp.ctypes.data, max_padded)
+    if rc != 0:
+        raise ValueError("oracle_align: invalid arguments")
+    return sorted_ids, expert_ids[: max_padded // block_size], int(npp[0])
+
+
+# --------------------------------------------------------- element-wise ---
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    """bf16(silu(f32 gate) * f32 up) over x = [gate | up]
+    (ops/fused_moe.py:58-62)."""
+    n = x.shape[-1] // 2
+    g = x[..., :n].float()
+    u = x[..., n:].float()
+    return (g / (1.0 + torch.exp(-g)) * u).to(torch.bfloat16)
+
+
+def moe_sum(y: torch.Tensor) -> torch.Tensor:
+    """[M, k, K] -> bf16(fp32 sum over k)."""
+    return y.float().sum(dim=1).to(torch.bfloat16)
+
+
+# ------------------------------------------------------------ quantisers ---
+def quant_fp8_group(x: torch.Tensor, group: int = 128):
+    """Dynamic per-(row, group) e4m3fn quantisation of a 2D tensor:
+    scale = max(amax, 1e-10)/448, q = e4m3fn(clamp(x/scale, +-448))."""
+    rows, cols = x.shape
+    xg = x.float().reshape(rows, cols // group, group)
+    amax = xg.abs().amax(dim=-1)
+    scale = torch.clamp(amax, min=QUANT_EPS) / FP8_MAX
+    q = torch.clamp(xg / scale[..., None], -FP8_MAX, FP8_MAX)
+    return q.to(torch.float8_e4m3fn).reshape(rows, cols), scale
+
+
+def dequant_fp8_group(q: torch.Tensor, scale: torch.Tensor, group: int = 128):
+    rows, cols = q.shape
+    return (q.float().reshape(rows, cols // group, group) *
+            scale[..., None]).reshape(rows, cols)
+
+
+def quant_int8_token(x: torch.Tensor):
+    """Dynamic per-row int8: scale = max(amax, 1e-10)/127,
+    q = clamp(round_half_even(x/scale), -127, 127)."""
+    xf = x.float()
+    amax = xf.abs().amax(dim=-1)
+    scale = torch.clamp(amax, min=QUANT_EPS) / INT8_MAX
+    q = torch.clamp(torch.round(xf / scale[:, None]), -INT8_MAX, INT8_MAX)
+    return q.to(torch.int8), scale
+
+
+def quant_weight_fp8_block(w: torch.Tensor, block: int = 128):
+    """One expert's [R, C] weight -> (e4m3fn [R, C], fp32 [R/128, C/128]),
+    scale = max(block amax, 1e-10)/448."""
+    r, c = w.shape
+    wb = w.float().reshape(r // block, block, c // block, block)
+    amax = wb.abs().amax(dim=(1, 3))
+    scale = torch.clamp(amax, min=QUANT_EPS) / FP8_MAX
+    q = torch.clamp(wb / scale[:, None, :, None], -FP8_MAX, FP8_MAX)
+    return q.to(torch.float8_e4m3fn).reshape(r, c), scale
+
+
+def dequant_weight_fp8_block(q: torch.Tensor, scale: torch.Tensor,
+                             block: int = 128) -> torch.Tensor:
+    r, c = q.shape
+    return (q.float().reshape(r // block, block, c // block, block) *
+            scale[:, None, :, None]).reshape(r, c)
+
+
+def quant_weight_int8_channel(w: torch.Tensor):
+    """One expert's [R, C] weight -> (int8 [R, C], fp32 [R]) per output row."""
+    wf = w.float()
+    amax = wf.abs().amax(dim=-1)
+    scale = torch.clamp(amax, min=QUANT_EPS) / INT8_MAX
+    q = torch.clamp(torch.round(wf / scale[:, None]), -INT8_MAX, INT8_MAX)
+    return q.to(torch.int8), scale
+
+
+# ----------------------------------------------------------- fused MoE ---
+def _expert_weights(mode, w1, w2, w1_scale, w2_scale, e):
+    """fp32 (dequantised) weights of expert e: W13 [2N, K], W2 [K, N].
+    Only this expert is copied to the host, so the weights may stay on the
+    GPU and be checked at full model size."""
+    a, b = w1[e].cpu(), w2[e].cpu()
+    if mode == "bf16":
+        return a.float(), b.float()
+    if mode == "fp8":
+        return (dequant_weight_fp8_block(a, w1_scale[e].cpu()),
+                dequant_weight_fp8_block(b, w2_scale[e].cpu()))
+    if mode == "int8":
+        return (a.float() * w1_scale[e].cpu().float()[:, None],
+                b.float() * w2_scale[e].cpu().float()[:, None])
+    raise ValueError(mode)
+
+
+def _quant_dequant_act(mode, a: torch.Tensor) -> torch.Tensor:
+    """What the w8a8 kernels feed the MFMA: quantise then dequantise."""
+    if mode == "bf16":
+        return a.float()
+    if mode == "fp8":
+        q, s = quant_fp8_group(a, 128)
+        return dequant_fp8_group(q, s, 128)
+    q, s = quant_int8_token(a)
+    return q.float() * s[:, None]
+
+
+def fused_moe(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+              topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+              mode: str = "bf16", w1_scale: Optional[torch.Tensor] = None,
+              w2_scale: Optional[torch.Tensor] = None,
+              apply_router_weight_on_input: bool = False,
+              tokens: Optional[Sequence[int]] = None) -> torch.Tensor:
+    """Reference fused MoE on CPU tensors (SGLang layout: w1 [E, 2N, K],
+    w2 [E, K, N]). Returns bf16 [len(tokens), K] (all tokens by default).
+
+    Every token's output depends only on its own row and routing, so any
+    subset of tokens can be checked exactly at full layer size.
+    """
+    x = x.cpu()
+    topk_weights = topk_weights.cpu().float()
+    topk_ids = topk_ids.cpu().long()
+    if tokens is None:
+        tokens = range(x.shape[0])
+    tok = torch.as_tensor(list(tokens), dtype=torch.long)
+    xs = x[tok]
+    ids = topk_ids[tok]
+    wts = topk_weights[tok]
+    T, k = ids.shape
+    K = x.shape[1]
+    N = w2.shape[2]
+    E = w1.shape[0]
+    # x as the GEMM1 kernel sees it (per-token quantisation is row-local, so
+    # quantising the subset equals quantising all rows then selecting).
+    xq = _quant_dequant_act(mode, xs)
+    y = torch.zeros(T, k, K, dtype=torch.float32)
+    for e in torch.unique(ids).tolist():
+        if e < 0 or e >= E:
+            continue
+        rows, slots = torch.nonzero(ids == e, as_tuple=True)
+        w13e, w2e = _expert_weights(mode, w1, w2, w1_scale, w2_scale, e)
+        h = xq[rows] @ w13e.t()
+        if apply_router_weight_on_input:
+            h = h * wts[rows, slots][:, None]
+        h = h.to(torch.bfloat16)
+        a = silu_and_mul(h)
+        aq = _quant_dequant_act(mode, a)
+        ye = (aq @ w2e.t()).to(torch.bfloat16).float()
+        y[rows, slots] = ye
+    if apply_router_weight_on_input:
+        out = y.sum(dim=1)
+    else:
+        out = (y * wts[:, :, None]).sum(dim=1)
+    return out.to(torch.bfloat16)
+
+
+def compare(res: torch.Tensor, ref: torch.Tensor, atol: float, rtol: float):
+    """Tolerance check used by the parity tests:
+    |res - ref| <= atol + rtol * |ref| elementwise, plus max-abs and
+    mean-rel (sum|res - ref| / sum|ref|) for reporting."""
+    r = res.float().cpu()
+    f = ref.float().cpu()
+    diff = (r - f).abs()
+    ok = bool((diff <= atol + rtol * f.abs()).all()) and bool(torch.isfinite(r).all())
+    max_abs = float(diff.max()) if diff.numel() else 0.0
+    mean_rel = float(diff.sum() / f.abs().sum().clamp(min=1e-30)) if diff.numel() else 0.0
+    return ok, max_abs, mean_rel

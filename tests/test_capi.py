@@ -1,0 +1,213 @@
+"""The C-ABI boundary on the CPU: the library loads, exports every symbol
+include/fgs_moe.h declares, and validates arguments on the host (no kernel
+is launched by anything here). Also the Python-level argument checks and the
+operator registry."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from flaggems_sglang import _capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fgs_moe.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(fgs_moe_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _capi.load()
+    declared = _declared_symbols()
+    assert len(declared) >= 13
+    for name in declared:
+        assert hasattr(lib, name), name
+    # the ctypes table covers exactly the header
+    assert sorted(_capi.SIGNATURES) == declared
+
+
+def test_version_and_error_string():
+    lib = _capi.load()
+    assert lib.fgs_moe_version().decode().startswith("fgs_moe")
+    assert isinstance(_capi.last_error(), str)
+
+
+def test_align_max_padded():
+    lib = _capi.load()
+    assert lib.fgs_moe_align_max_padded(16, 8, 16) == 16 + 8 * 15
+    assert lib.fgs_moe_align_max_padded(-1, 8, 16) == -1
+    assert lib.fgs_moe_align_max_padded(4, 0, 16) == -1
+
+
+@pytest.mark.parametrize(
+    "args,code,msg",
+    [
+        ((1, 4096, 14336, 8, 2, 0, 0), 0, ""),
+        ((-1, 4096, 14336, 8, 2, 0, 0), _capi.FGS_EINVAL, "m must be"),
+        ((1, 0, 14336, 8, 2, 0, 0), _capi.FGS_EINVAL, "hidden and inter"),
+        ((1, 4096, 14336, 0, 2, 0, 0), _capi.FGS_EINVAL, "num_experts"),
+        ((1, 4096, 14336, 2000, 2, 0, 0), _capi.FGS_EINVAL, "num_experts"),
+        ((1, 4096, 14336, 8, 9, 0, 0), _capi.FGS_EINVAL, "topk"),
+        ((1, 4096, 14336, 8, 2, 7, 0), _capi.FGS_EINVAL, "qmode"),
+        ((1, 4096, 14336, 8, 2, 0, 0x40), _capi.FGS_EINVAL, "flag"),
+        ((1, 4096, 14336, 8, 2, 0, 0x300), _capi.FGS_EINVAL, "exclusive"),
+        ((1, 4000, 14336, 8, 2, 0, 0), _capi.FGS_EUNSUPPORTED, "multiples"),
+        ((1, 3584, 2560, 64, 8, 2, 0), 0, ""),
+        ((1, 3584 - 128, 2560, 64, 8, 2, 0), _capi.FGS_EUNSUPPORTED, "multiples"),
+    ],
+)
+def test_validate(args, code, msg):
+    lib = _capi.load()
+    need = lib.fgs_moe_workspace_bytes(*args)
+    rc = lib.fgs_moe_validate(*args, max(need, 0))
+    assert rc == code, _capi.last_error()
+    if code:
+        assert need == -1
+        assert msg in _capi.last_error()
+    else:
+        assert need > 0
+
+
+def test_validate_workspace_too_small():
+    lib = _capi.load()
+    need = lib.fgs_moe_workspace_bytes(64, 1024, 512, 8, 2, 0, 0)
+    assert lib.fgs_moe_validate(64, 1024, 512, 8, 2, 0, 0, need - 1) == _capi.FGS_EINVAL
+    assert "workspace too small" in _capi.last_error()
+
+
+def test_workspace_grows_with_tokens_and_quant_mode():
+    lib = _capi.load()
+    a = lib.fgs_moe_workspace_bytes(1, 7168, 2048, 256, 8, 0, 0)
+    b = lib.fgs_moe_workspace_bytes(4096, 7168, 2048, 256, 8, 0, 0)
+    c = lib.fgs_moe_workspace_bytes(4096, 7168, 2048, 256, 8, 1, 0)
+    assert 0 < a < b < c
+
+
+def test_entry_points_reject_bad_arguments_before_launch():
+    """Invalid calls return an error code without touching a device."""
+    lib = _capi.load()
+    nul = None
+    # max_padded below numel + E*(B-1)
+    assert lib.fgs_moe_align_block_size(nul, 8, 4, 16, nul, nul, nul, 10, nul) == -1
+    assert "max_padded" in _capi.last_error()
+    assert lib.fgs_moe_align_block_size(nul, 8, 0, 16, nul, nul, nul, 100, nul) == -1
+    assert lib.fgs_moe_silu_and_mul(nul, nul, 4, 12, nul) == -2
+    assert lib.fgs_moe_silu_and_mul(nul, nul, 4, 16, nul) == -1  # null pointers
+    assert lib.fgs_moe_sum(nul, nul, 4, 0, 16, nul) == -1
+    assert lib.fgs_moe_quant_fp8_group(nul, nul, nul, 4, 256, 100, nul) == -2
+    assert lib.fgs_moe_quant_int8_token(nul, nul, nul, 4, 12, nul) == -2
+    need = lib.fgs_moe_workspace_bytes(4, 256, 128, 4, 2, 0, 0)
+    rc = lib.fgs_moe_fused_bf16(nul, nul, nul, nul, nul, 4, 256, 128, 4, 2, 0,
+                                nul, need, nul, nul)
+    assert rc == -1 and "null pointer" in _capi.last_error()
+    rc = lib.fgs_moe_fused_fp8_block(nul, nul, nul, nul, nul, 64, 128, nul, nul,
+                                     4, 256, 128, 4, 2, 0, nul, need, nul, nul)
+    assert rc == -2 and "128x128" in _capi.last_error()
+    rc = lib.fgs_moe_fused_int8_channel(nul, nul, nul, nul, nul, nul, nul, 4,
+                                        256, 256, 4, 2, 0, nul, 0, nul, nul)
+    assert rc == -1 and "workspace" in _capi.last_error()
+
+
+def test_error_codes_map_to_python_exceptions():
+    with pytest.raises(ValueError):
+        _capi.check(_capi.FGS_EINVAL, "x")
+    with pytest.raises(NotImplementedError):
+        _capi.check(_capi.FGS_EUNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _capi.check(_capi.FGS_ELAUNCH, "x")
+    _capi.check(_capi.FGS_OK, "x")
+
+
+def test_error_string_is_thread_local():
+    import threading
+
+    lib = _capi.load()
+    lib.fgs_moe_validate(-1, 1, 1, 1, 1, 0, 0, 0)
+    seen = {}
+
+    def other():
+        seen["msg"] = _capi.last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == ""
+    assert "m must be" in _capi.last_error()
+
+
+# ------------------------------------------------------ python boundary ---
+def test_registry_surface():
+    import flaggems_sglang
+
+    names = flaggems_sglang.all_registered_ops()
+    for n in ("fused_moe", "triton_kernel_fused_experts", "moe_align_block_size",
+              "silu_and_mul", "moe_sum"):
+        assert n in names
+        assert getattr(flaggems_sglang, n) is flaggems_sglang.get_op(n)
+    assert flaggems_sglang.get_op("nope") is None
+    assert flaggems_sglang.device == "cuda"
+    assert flaggems_sglang.vendor_name == "amd"
+
+
+def _cpu_inputs():
+    x = torch.randn(4, 256, dtype=torch.bfloat16)
+    w1 = torch.randn(4, 256, 256, dtype=torch.bfloat16)
+    w2 = torch.randn(4, 256, 128, dtype=torch.bfloat16)
+    tw = torch.full((4, 2), 0.5)
+    ti = torch.zeros(4, 2, dtype=torch.int32)
+    return x, w1, w2, tw, ti
+
+
+def test_unsupported_flags_keep_reference_messages():
+    from flaggems_sglang import fused_moe, triton_kernel_fused_experts
+
+    x, w1, w2, tw, ti = _cpu_inputs()
+    with pytest.raises(AssertionError, match="expert_map is not supported"):
+        fused_moe(x, w1, w2, tw, ti, expert_map=torch.zeros(4))
+    with pytest.raises(AssertionError, match="a1_scale is not supported"):
+        fused_moe(x, w1, w2, tw, ti, a1_scale=torch.ones(1))
+    with pytest.raises(AssertionError, match="Inplace is not supported"):
+        fused_moe(x, w1, w2, tw, ti, inplace=True)
+    with pytest.raises(ValueError, match="Unsupported FusedMoe activation"):
+        fused_moe(x, w1, w2, tw, ti, activation="relu")
+    with pytest.raises(AssertionError, match="use_fp8_w8a8 is not supported"):
+        triton_kernel_fused_experts(x, w1, w2, None, None, None, use_fp8_w8a8=True)
+    with pytest.raises(AssertionError, match="block_shape is not supported"):
+        triton_kernel_fused_experts(x, w1, w2, None, None, None, block_shape=[128, 128])
+
+
+def test_no_cpu_fallback():
+    from flaggems_sglang import fused_moe, moe_align_block_size, silu_and_mul
+
+    x, w1, w2, tw, ti = _cpu_inputs()
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        fused_moe(x, w1, w2, tw, ti)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        moe_align_block_size(ti, 4, 16)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        silu_and_mul(x)
+
+
+def test_standard_topk_to_routing_roundtrip_cpu():
+    """The routing-format converter and its inverse are torch index ops and
+    run on any device; the round trip restores (weights, ids) with ids
+    ascending inside each token (ops/fused_moe.py:130)."""
+    from flaggems_sglang.ops.fused_moe import (_routing_to_topk,
+                                               standard_topk_to_routing)
+
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(9, 16, generator=g)
+    w, ids = torch.topk(torch.softmax(logits, -1), 4, dim=-1)
+    w = w / w.sum(-1, keepdim=True)
+    rd, gi, si = standard_topk_to_routing(w, ids.int(), 16)
+    assert rd.n_expts_act == 4 and rd.expt_hist.sum() == 36
+    w2, ids2 = _routing_to_topk(rd, gi, 9)
+    order = torch.argsort(ids, dim=1)
+    assert torch.equal(ids2.long(), torch.gather(ids, 1, order))
+    assert torch.equal(w2, torch.gather(w, 1, order))
+    assert torch.equal(gi.dst_indx[gi.src_indx.long()], torch.arange(36, dtype=torch.int32))

@@ -1,0 +1,133 @@
+"""GPU parity of the bandwidth kernels against the CPU oracle: alignment
+(bit-exact), silu_and_mul, moe_sum, and the activation quantisers
+(bit-exact). Each call goes through the C ABI via the package's ops."""
+
+import numpy as np
+import pytest
+import torch
+
+from flaggems_sglang import ops  # noqa: F401
+from flaggems_sglang.ops import fused_moe as fm
+from oracle import moe_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _routing(M, E, k, seed, device, hot=(), bias=0.0, scoring="softmax"):
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(M, E, generator=g)
+    if hot:
+        logits[:, list(hot)] += bias
+    w, ids = moe_ref.route(logits, k, scoring)
+    return w, ids
+
+
+ALIGN_CASES = [
+    # (M, k, E, block)
+    (1, 2, 8, 16), (7, 2, 8, 16), (33, 4, 16, 32), (64, 2, 8, 16),
+    (1, 8, 128, 64), (16, 8, 128, 64), (256, 8, 128, 64), (2048, 8, 128, 64),
+    (8192, 8, 128, 64), (4096, 8, 256, 16), (1024, 8, 64, 32),
+    (300, 3, 1024, 16), (5, 1, 1, 7), (8192, 2, 8, 128),
+]
+
+
+@pytest.mark.parametrize("M,k,E,B", ALIGN_CASES)
+def test_align_bit_exact(gpu, M, k, E, B):
+    w, ids = _routing(M, E, k, seed=M + k + E + B, device=gpu)
+    s, eids, npp = fm.moe_align_block_size(ids.to(gpu), E, B)
+    rs, reids, rnpp = moe_ref.align(ids.numpy(), E, B)
+    torch.cuda.synchronize()
+    assert int(npp.item()) == rnpp
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(eids.cpu().numpy(), reids)
+
+
+@pytest.mark.parametrize("skew", [False, True])
+def test_align_qwen3_skewed_block64(gpu, skew):
+    hot = (3, 17, 31, 45, 59, 73, 87, 101)
+    for M in (1, 16, 256, 2048, 8192):
+        _, ids = _routing(M, 128, 8, seed=M + 2048 + 768 + 128 + 8, device=gpu,
+                          hot=hot if skew else (), bias=2.0)
+        s, eids, npp = fm.moe_align_block_size(ids.to(gpu), 128, 64)
+        rs, reids, rnpp = moe_ref.align(ids.numpy(), 128, 64)
+        assert int(npp.item()) == rnpp, M
+        assert np.array_equal(s.cpu().numpy(), rs), M
+        assert np.array_equal(eids.cpu().numpy(), reids), M
+
+
+def test_align_edge_cases(gpu):
+    # empty input
+    ids = torch.zeros((0, 2), dtype=torch.int32, device=gpu)
+    s, eids, npp = fm.moe_align_block_size(ids, 4, 8)
+    rs, reids, rnpp = moe_ref.align(np.zeros((0, 2), np.int32), 4, 8)
+    assert int(npp.item()) == rnpp == 0
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(eids.cpu().numpy(), reids)
+    # out-of-range ids are dropped, all slots on one expert, repeated ids
+    raw = np.array([[-1, 3], [7, 3], [3, 3], [0, 100]], dtype=np.int32)
+    s, eids, npp = fm.moe_align_block_size(torch.from_numpy(raw).to(gpu), 4, 4)
+    rs, reids, rnpp = moe_ref.align(raw, 4, 4)
+    assert int(npp.item()) == rnpp
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(eids.cpu().numpy(), reids)
+
+
+def test_align_deterministic(gpu):
+    _, ids = _routing(8192, 128, 8, seed=11, device=gpu)
+    ids = ids.to(gpu)
+    first = fm.moe_align_block_size(ids, 128, 64)[0].cpu()
+    for _ in range(3):
+        assert torch.equal(fm.moe_align_block_size(ids, 128, 64)[0].cpu(), first)
+
+
+def _ulp_diff_bf16(a, b):
+    ai = a.view(torch.int16).to(torch.int32)
+    bi = b.view(torch.int16).to(torch.int32)
+    # map sign-magnitude to a monotone integer line
+    ai = torch.where(ai < 0, -(ai & 0x7FFF), ai)
+    bi = torch.where(bi < 0, -(bi & 0x7FFF), bi)
+    return (ai - bi).abs()
+
+
+@pytest.mark.parametrize("rows,n", [(1, 256), (7, 3072), (513, 768), (64, 14336)])
+def test_silu_and_mul(gpu, rows, n):
+    g = torch.Generator().manual_seed(rows + n)
+    x = (torch.randn(rows, 2 * n, generator=g) * 3).to(torch.bfloat16)
+    out = fm.silu_and_mul(x.to(gpu)).cpu()
+    ref = moe_ref.silu_and_mul(x)
+    assert _ulp_diff_bf16(out, ref).max() <= 1
+
+
+@pytest.mark.parametrize("m,k,K", [(1, 2, 4096), (33, 8, 2048), (4096, 2, 1024),
+                                   (5, 1, 128)])
+def test_moe_sum(gpu, m, k, K):
+    g = torch.Generator().manual_seed(m + k + K)
+    y = torch.randn(m, k, K, generator=g).to(torch.bfloat16)
+    out = fm.moe_sum(y.to(gpu)).cpu()
+    ref = moe_ref.moe_sum(y)
+    assert _ulp_diff_bf16(out, ref).max() <= 1
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 128), (37, 7168), (512, 2048)])
+def test_quant_fp8_group_bit_exact(gpu, rows, cols):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * 2).to(torch.bfloat16)
+    x[0, :5] = 0.0
+    if rows > 1:
+        x[1, :128] = 0.0  # all-zero group: scale = 1e-10/448
+    q, s = fm.per_token_group_quant_fp8(x.to(gpu), 128)
+    rq, rsc = moe_ref.quant_fp8_group(x, 128)
+    assert torch.equal(s.cpu(), rsc)
+    assert torch.equal(q.cpu().view(torch.uint8), rq.view(torch.uint8))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 128), (37, 3584), (300, 2560)])
+def test_quant_int8_token_bit_exact(gpu, rows, cols):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * 2).to(torch.bfloat16)
+    if rows > 1:
+        x[1] = 0.0
+    q, s = fm.per_token_quant_int8(x.to(gpu))
+    rq, rsc = moe_ref.quant_int8_token(x)
+    assert torch.equal(s.cpu(), rsc)
+    assert torch.equal(q.cpu(), rq)

@@ -1,0 +1,308 @@
+"""Pins the CPU oracle (oracle/) before any GPU result is compared with it.
+
+Each oracle function is checked against something that does not restate its
+own formula: hand-worked known answers, the reference's own routing steps
+re-run with torch library ops, float64 brute force, the OCP e4m3 code table
+decoded from the bit layout, and exact invariants (permutations, scaling,
+expert relabelling, token subsets). CPU only.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref
+
+
+# ------------------------------------------------------------ alignment ---
+def test_align_known_answer_small():
+    # ids per token: t0 -> (2, 0), t1 -> (0, 1), t2 -> (2, 1); E=3, B=4.
+    ids = np.array([[2, 0], [0, 1], [2, 1]], dtype=np.int32)
+    s, e, npp = moe_ref.align(ids, 3, 4)
+    S = 6  # sentinel = numel
+    assert npp == 12
+    assert s.tolist() == [1, 2, S, S, 3, 5, S, S, 0, 4, S, S, S, S, S]
+    assert e.tolist() == [0, 1, 2]
+
+
+def test_align_known_answer_unused_expert_block1():
+    ids = np.array([[3, 1]], dtype=np.int32)
+    s, e, npp = moe_ref.align(ids, 4, 1)
+    assert npp == 2 and s.tolist() == [1, 0] and e.tolist() == [1, 3]
+
+
+def test_align_known_answer_dropped_and_empty():
+    ids = np.array([[-1, 0], [5, 0]], dtype=np.int32)  # -1 and 5 not routed (E=2)
+    s, e, npp = moe_ref.align(ids, 2, 2)
+    assert npp == 2 and s[:2].tolist() == [1, 3] and (s[2:] == 4).all()
+    assert e.tolist() == [0, -1, -1]  # max_padded = 4 + 2*(2-1) = 6
+    s, e, npp = moe_ref.align(np.zeros((0, 2), np.int32), 3, 4)
+    assert npp == 0 and (s == 0).all() and (e == -1).all()
+
+
+def _reference_routing_steps(topk_weights, topk_ids, n_expts_tot):
+    """The reference's conversion steps (ops/fused_moe.py:130-139) run with
+    torch library ops: per-row sort, stable argsort, gather, histc."""
+    expt_indx_2d, sort_indices = torch.sort(topk_ids, dim=1)
+    expt_scal = torch.gather(topk_weights, 1, sort_indices).reshape(-1)
+    expt_indx = expt_indx_2d.reshape(-1).to(torch.int32)
+    topk_indx = torch.argsort(expt_indx, stable=True)
+    gate_scal = expt_scal[topk_indx]
+    hist = torch.histc(expt_indx.float(), bins=n_expts_tot,
+                       max=n_expts_tot - 1).int()
+    return topk_indx, gate_scal, hist
+
+
+@pytest.mark.parametrize("M,k,E,B", [(1, 2, 8, 16), (7, 2, 8, 16),
+                                     (33, 4, 16, 32), (257, 8, 128, 64),
+                                     (64, 8, 256, 16), (100, 1, 3, 5)])
+def test_align_matches_reference_stable_order(M, k, E, B):
+    g = torch.Generator().manual_seed(M + k + E + B)
+    logits = torch.randn(M, E, generator=g)
+    w, ids = moe_ref.route(logits, k)
+    s, eids, npp = moe_ref.align(ids.numpy(), E, B)
+    topk_indx, gate_scal, hist = _reference_routing_steps(w, ids.long(), E)
+    valid = s[s < M * k]
+    # same per-expert token sequence as the reference's stable argsort
+    assert np.array_equal(valid // k, topk_indx.numpy() // k)
+    # the gathered gate scales are the reference's gate_scal bit for bit
+    assert torch.equal(w.reshape(-1)[torch.from_numpy(valid).long()], gate_scal)
+    # per-expert padded segments
+    padded = (hist.numpy() + B - 1) // B * B
+    off = np.concatenate([[0], np.cumsum(padded)])
+    assert npp == off[-1]
+    for e in range(E):
+        seg = s[off[e]:off[e + 1]]
+        c = hist[e].item()
+        assert (ids.numpy().reshape(-1)[seg[:c]] == e).all()
+        assert (np.diff(seg[:c]) > 0).all()
+        assert (seg[c:] == M * k).all()
+        assert (eids[off[e] // B:off[e + 1] // B] == e).all()
+    assert (eids[npp // B:] == -1).all()
+
+
+# -------------------------------------------------------------- silu*mul ---
+def test_silu_and_mul_closed_form_float64():
+    g = torch.Generator().manual_seed(0)
+    x = (torch.randn(64, 256, generator=g) * 4).to(torch.bfloat16)
+    got = moe_ref.silu_and_mul(x).float().numpy()
+    xd = x.double().numpy()
+    gd, ud = xd[:, :128], xd[:, 128:]
+    want = gd * ud / (1.0 + np.exp(-gd))
+    # one bf16 rounding of the exact value: relative error <= 2^-8
+    assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-30)
+
+
+def test_silu_and_mul_special_cases():
+    x = torch.tensor([[0.0, 20.0, -30.0, 3.0, 2.0, 1.0]], dtype=torch.bfloat16)
+    out = moe_ref.silu_and_mul(x).float()[0]
+    assert out[0] == 0.0                      # silu(0) * u = 0
+    assert abs(out[1] - 40.0) < 0.2           # silu(g) * u -> g * u, large g
+    assert abs(out[2]) < 1e-10                # silu(g) -> 0 for very negative g
+
+
+# ------------------------------------------------------------ quantisers ---
+def _e4m3fn_decode(code: int) -> float:
+    """OCP FP8 E4M3 (fn): 1 sign, 4 exponent (bias 7), 3 mantissa bits,
+    subnormals, no infinities, S.1111.111 = NaN."""
+    s = -1.0 if code & 0x80 else 1.0
+    e = (code >> 3) & 0xF
+    m = code & 0x7
+    if e == 0xF and m == 0x7:
+        return math.nan
+    if e == 0:
+        return s * m * 2.0 ** -9
+    return s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+
+
+def test_fp8_code_table_matches_ocp_layout():
+    codes = torch.arange(256, dtype=torch.uint8)
+    vals = codes.view(torch.float8_e4m3fn).float().tolist()
+    for c in range(256):
+        want = _e4m3fn_decode(c)
+        if math.isnan(want):
+            assert math.isnan(vals[c])
+        else:
+            assert vals[c] == want, c
+    assert max(v for v in vals if not math.isnan(v)) == 448.0
+
+
+def test_fp8_cast_is_round_to_nearest_even():
+    table = sorted({_e4m3fn_decode(c) for c in range(256)} - {math.nan},
+                   key=float)
+    table = np.array([v for v in table if not math.isnan(v)])
+    g = torch.Generator().manual_seed(1)
+    x = (torch.rand(4000, generator=g) * 2 - 1) * 460
+    x = torch.clamp(x, -448, 448)
+    got = x.to(torch.float8_e4m3fn).float().numpy()
+    for xi, gi in zip(x.numpy(), got):
+        d = np.abs(table - xi)
+        best = table[d == d.min()]
+        if len(best) == 1:
+            assert gi == best[0]
+        else:  # tie: even mantissa (the candidate whose code is even)
+            codes = [c for c in range(256) if _e4m3fn_decode(c) in best]
+            even = [_e4m3fn_decode(c) for c in codes if c % 2 == 0]
+            assert gi in even
+
+
+def test_fp8_group_quant_roundtrip_and_amax():
+    g = torch.Generator().manual_seed(2)
+    x = (torch.randn(16, 512, generator=g) * 3).to(torch.bfloat16)
+    q, s = moe_ref.quant_fp8_group(x, 128)
+    assert q.dtype == torch.float8_e4m3fn and s.shape == (16, 4)
+    xf = x.float().reshape(16, 4, 128)
+    assert torch.equal(s, xf.abs().amax(-1) / 448.0)
+    deq = moe_ref.dequant_fp8_group(q, s, 128).reshape(16, 4, 128)
+    # e4m3 has 3 mantissa bits: relative error <= 2^-4 above the subnormal range
+    err = (deq - xf).abs()
+    bound = 2.0 ** -4 * xf.abs() + 2.0 ** -10 * s[..., None]
+    assert (err <= bound).all()
+    # the group's amax element maps to +-448 exactly
+    qa = q.float().reshape(16, 4, 128).abs().amax(-1)
+    assert (qa == 448.0).all()
+
+
+def test_int8_token_quant_roundtrip():
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(8, 256, generator=g)).to(torch.bfloat16)
+    q, s = moe_ref.quant_int8_token(x)
+    xf = x.float()
+    assert torch.equal(s, xf.abs().amax(-1) / 127.0)
+    assert ((q.float() * s[:, None] - xf).abs() <= s[:, None] / 2 * (1 + 1e-6)).all()
+    assert (q.abs().amax(-1) == 127).all()
+    # round half to even on exact ties
+    t = torch.tensor([[127.0, 0.5, 1.5, 2.5, -0.5]], dtype=torch.bfloat16)
+    q2, s2 = moe_ref.quant_int8_token(t)
+    assert s2.item() == 1.0 and q2.tolist() == [[127, 0, 2, 2, 0]]
+
+
+def test_weight_quantisers():
+    g = torch.Generator().manual_seed(4)
+    w = torch.randn(256, 384, generator=g) * 0.02
+    q, s = moe_ref.quant_weight_fp8_block(w)
+    assert s.shape == (2, 3)
+    assert torch.allclose(s, w.reshape(2, 128, 3, 128).abs().amax((1, 3)) / 448)
+    deq = moe_ref.dequant_weight_fp8_block(q, s)
+    sb = s.repeat_interleave(128, 0).repeat_interleave(128, 1)
+    assert ((deq - w).abs() <= 2.0 ** -4 * w.abs() + 2.0 ** -10 * sb).all()
+    qi, si = moe_ref.quant_weight_int8_channel(w)
+    assert ((qi.float() * si[:, None] - w).abs() <= si[:, None] / 2 * 1.000001).all()
+
+
+# ------------------------------------------------------------- fused MoE ---
+def _brute_force_moe(x, w1, w2, tw, tid):
+    """Token-by-token float64 MoE (no intermediate rounding)."""
+    x = x.double().numpy()
+    w1 = w1.double().numpy()
+    w2 = w2.double().numpy()
+    N = w2.shape[2]
+    out = np.zeros((x.shape[0], x.shape[1]))
+    for t in range(x.shape[0]):
+        for j in range(tid.shape[1]):
+            e = int(tid[t, j])
+            h = w1[e] @ x[t]
+            gte, up = h[:N], h[N:]
+            a = gte / (1.0 + np.exp(-gte)) * up
+            out[t] += float(tw[t, j]) * (w2[e] @ a)
+    return out
+
+
+def _inputs(M, K, N, E, k, seed, scale=0.1):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(E, 2 * N, K, generator=g) * scale).to(torch.bfloat16)
+    w2 = (torch.randn(E, K, N, generator=g) * scale).to(torch.bfloat16)
+    w, ids = moe_ref.route(torch.randn(M, E, generator=g), k)
+    return x, w1, w2, w, ids
+
+
+@pytest.mark.parametrize("M,K,N,E,k", [(5, 32, 48, 4, 2), (9, 64, 16, 6, 3)])
+def test_moe_matches_float64_brute_force(M, K, N, E, k):
+    x, w1, w2, w, ids = _inputs(M, K, N, E, k, seed=M + K + N + E + k)
+    got = moe_ref.fused_moe(x, w1, w2, w, ids).double().numpy()
+    want = _brute_force_moe(x, w1, w2, w, ids)
+    # three bf16 roundings on the way (h, a, y) plus the output rounding
+    assert np.allclose(got, want, rtol=3e-2, atol=3e-2 * np.abs(want).max())
+
+
+def test_moe_top1_unit_weight_is_plain_mlp():
+    x, w1, w2, _, _ = _inputs(6, 32, 24, 1, 1, seed=5)
+    ones = torch.ones(6, 1)
+    zeros = torch.zeros(6, 1, dtype=torch.int32)
+    got = moe_ref.fused_moe(x, w1, w2, ones, zeros).double()
+    xd, w1d, w2d = x.double(), w1[0].double(), w2[0].double()
+    h = xd @ w1d.t()
+    a = torch.nn.functional.silu(h[:, :24]) * h[:, 24:]
+    want = a @ w2d.t()
+    assert torch.allclose(got, want, rtol=3e-2, atol=3e-2 * want.abs().max())
+
+
+def test_moe_exact_invariants():
+    x, w1, w2, w, ids = _inputs(12, 64, 32, 5, 2, seed=6)
+    base = moe_ref.fused_moe(x, w1, w2, w, ids)
+    # permuting tokens permutes the output rows
+    perm = torch.randperm(12, generator=torch.Generator().manual_seed(0))
+    assert torch.equal(moe_ref.fused_moe(x[perm], w1, w2, w[perm], ids[perm]),
+                       base[perm])
+    # relabelling experts changes nothing
+    relabel = torch.tensor([3, 0, 4, 1, 2])
+    inv = torch.argsort(relabel)
+    assert torch.equal(
+        moe_ref.fused_moe(x, w1[inv], w2[inv], w, relabel[ids.long()].int()), base)
+    # doubling the gate weights doubles the output exactly (fp32 sum, bf16 out)
+    assert torch.equal(moe_ref.fused_moe(x, w1, w2, 2 * w, ids).float(),
+                       2 * base.float())
+    # a token subset equals the same rows of the full result
+    sub = [11, 0, 5]
+    assert torch.equal(moe_ref.fused_moe(x, w1, w2, w, ids, tokens=sub), base[sub])
+    # on-input gating with unit top-1 weights equals output gating
+    ones = torch.ones(12, 1)
+    a1 = moe_ref.fused_moe(x, w1, w2, ones, ids[:, :1])
+    a2 = moe_ref.fused_moe(x, w1, w2, ones, ids[:, :1],
+                           apply_router_weight_on_input=True)
+    assert torch.equal(a1, a2)
+
+
+def test_moe_slot_order_and_dropped_slots():
+    x, w1, w2, w, ids = _inputs(8, 64, 32, 4, 2, seed=7)
+    base = moe_ref.fused_moe(x, w1, w2, w, ids)
+    swapped = moe_ref.fused_moe(x, w1, w2, w.flip(1), ids.flip(1))
+    assert torch.allclose(swapped.float(), base.float(), atol=1e-2, rtol=1e-2)
+    # a slot routed to an out-of-range expert contributes nothing
+    ids2 = ids.clone()
+    ids2[:, 1] = -1
+    w1only = w.clone()
+    w1only[:, 1] = 0
+    assert torch.equal(moe_ref.fused_moe(x, w1, w2, w, ids2),
+                       moe_ref.fused_moe(x, w1, w2, w1only, ids))
+
+
+def test_moe_quantised_modes_track_bf16():
+    x, w1, w2, w, ids = _inputs(16, 256, 128, 4, 2, seed=8, scale=0.05)
+    base = moe_ref.fused_moe(x, w1, w2, w, ids).float()
+    q1 = [moe_ref.quant_weight_fp8_block(w1[e]) for e in range(4)]
+    q2 = [moe_ref.quant_weight_fp8_block(w2[e]) for e in range(4)]
+    fp8 = moe_ref.fused_moe(
+        x, torch.stack([a for a, _ in q1]), torch.stack([a for a, _ in q2]), w,
+        ids, mode="fp8", w1_scale=torch.stack([b for _, b in q1]),
+        w2_scale=torch.stack([b for _, b in q2])).float()
+    i1 = [moe_ref.quant_weight_int8_channel(w1[e]) for e in range(4)]
+    i2 = [moe_ref.quant_weight_int8_channel(w2[e]) for e in range(4)]
+    int8 = moe_ref.fused_moe(
+        x, torch.stack([a for a, _ in i1]), torch.stack([a for a, _ in i2]), w,
+        ids, mode="int8", w1_scale=torch.stack([b for _, b in i1]),
+        w2_scale=torch.stack([b for _, b in i2])).float()
+    for q in (fp8, int8):
+        rel = (q - base).abs().sum() / base.abs().sum()
+        assert rel < 0.08, rel
+
+
+def test_compare_helper():
+    a = torch.tensor([1.0, 2.0, 3.0])
+    ok, mx, mr = moe_ref.compare(a + 0.01, a, atol=2e-2, rtol=0)
+    assert ok and abs(mx - 0.01) < 1e-6 and abs(mr - 0.005) < 1e-6
+    ok, _, _ = moe_ref.compare(a + 0.5, a, atol=2e-2, rtol=1e-2)
+    assert not ok

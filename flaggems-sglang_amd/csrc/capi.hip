@@ -193,12 +193,12 @@ static int run_fused(const FusedArgs& a) {
   int rc = validate(a.m, a.hidden, a.inter, a.e, a.topk, a.qmode, a.flags,
                     a.ws_bytes, true);
   if (rc) return rc;
+  if (a.m == 0) return FGS_OK;  // nothing to read or write
   if (!a.x || !a.w13 || !a.w2 || !a.topk_weights || !a.topk_ids || !a.out ||
       !a.ws)
     return fail(FGS_EINVAL, "null pointer argument");
   if (a.qmode != FGS_QMODE_BF16 && (!a.w13_scale || !a.w2_scale))
     return fail(FGS_EINVAL, "quantised mode needs w13_scale and w2_scale");
-  if (a.m == 0) return FGS_OK;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 || reinterpret_cast<uintptr_t>(a.w13) % 16 ||
       reinterpret_cast<uintptr_t>(a.w2) % 16 || reinterpret_cast<uintptr_t>(a.out) % 16 ||
       reinterpret_cast<uintptr_t>(a.ws) % 256)
@@ -296,7 +296,8 @@ static int run_fused(const FusedArgs& a) {
   g_prof.mark(5, a.stream);
 
   rc = launch_moe_sum_routed(y, a.out, a.m, a.topk, a.hidden, a.topk_ids,
-                             a.e, a.stream);
+                             a.e, on_input ? nullptr : a.topk_weights,
+                             a.stream);
   g_prof.mark(6, a.stream);
   return rc;
 }

@@ -37,10 +37,14 @@ __global__ __launch_bounds__(256) void silu_and_mul_kernel(
 // out[t, c] = bf16(sum_j f32(in[t, j, c])): the top-k reduction that
 // matmul_ogs performs when given scatter_indx (ops/fused_moe.py:224-231).
 // Requires k % 8 == 0. With `ids` given, slots whose expert id lies outside
-// [0, num_experts) were never computed and contribute nothing.
+// [0, num_experts) were never computed and contribute nothing. With
+// `weights` given each slot is scaled first: out = bf16(sum_j w_j * y_j),
+// product and sum each rounded in fp32 in slot order (no fused multiply-add),
+// which is the gammas-on-GEMM2 reduction of ops/fused_moe.py:203,224-231.
 __global__ __launch_bounds__(256) void moe_sum_kernel(
     const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int64_t m,
-    int topk, int64_t k, const int32_t* __restrict__ ids, int num_experts) {
+    int topk, int64_t k, const int32_t* __restrict__ ids, int num_experts,
+    const float* __restrict__ weights) {
   const int64_t vec_per_row = k / 8;
   const int64_t total = m * vec_per_row;
   for (int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
@@ -55,10 +59,20 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(
         if (e < 0 || e >= num_experts) continue;
       }
       const u32x4 x = *reinterpret_cast<const u32x4*>(src + j * k);
+      if (weights) {
+        const float w = weights[t * topk + j];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc[2 * q] += __uint_as_float(x[q] << 16);
-        acc[2 * q + 1] += __uint_as_float(x[q] & 0xffff0000u);
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] = __fadd_rn(acc[2 * q], __fmul_rn(w, __uint_as_float(x[q] << 16)));
+          acc[2 * q + 1] =
+              __fadd_rn(acc[2 * q + 1], __fmul_rn(w, __uint_as_float(x[q] & 0xffff0000u)));
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] += __uint_as_float(x[q] << 16);
+          acc[2 * q + 1] += __uint_as_float(x[q] & 0xffff0000u);
+        }
       }
     }
     u32x4 o;
@@ -188,17 +202,19 @@ int launch_moe_sum(const void* in, void* out, int64_t m, int topk, int64_t k,
   if (m == 0) return FGS_OK;
   hipLaunchKernelGGL(moe_sum_kernel, dim3(grid_for(m * (k / 8), 256)),
                      dim3(256), 0, stream, static_cast<const uint16_t*>(in),
-                     static_cast<uint16_t*>(out), m, topk, k, nullptr, 0);
+                     static_cast<uint16_t*>(out), m, topk, k, nullptr, 0,
+                     nullptr);
   return check_launch("moe_sum_kernel");
 }
 
 int launch_moe_sum_routed(const void* in, void* out, int64_t m, int topk,
                           int64_t k, const int32_t* ids, int num_experts,
-                          hipStream_t stream) {
+                          const float* weights, hipStream_t stream) {
   if (m == 0) return FGS_OK;
   hipLaunchKernelGGL(moe_sum_kernel, dim3(grid_for(m * (k / 8), 256)),
                      dim3(256), 0, stream, static_cast<const uint16_t*>(in),
-                     static_cast<uint16_t*>(out), m, topk, k, ids, num_experts);
+                     static_cast<uint16_t*>(out), m, topk, k, ids, num_experts,
+                     weights);
   return check_launch("moe_sum_kernel");
 }
 

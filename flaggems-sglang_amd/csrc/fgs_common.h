@@ -47,6 +47,22 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + __expf(-g)) * u;
 }
 
+// GEMM1 epilogue with the rounding points of the reference's unfused path:
+// matmul_ogs writes its output (gate and up halves, gammas applied when the
+// router weight goes on the input, ops/fused_moe.py:202-212) in bf16, then
+// _silu_and_mul_kernel computes in fp32 from those bf16 values and stores
+// bf16 (:58-63).
+__device__ __forceinline__ uint16_t gemm1_epilogue(float g, float u,
+                                                   bool scale, float gamma) {
+  if (scale) {
+    g *= gamma;
+    u *= gamma;
+  }
+  g = bf16_bits_to_f32(f32_to_bf16_bits(g));
+  u = bf16_bits_to_f32(f32_to_bf16_bits(u));
+  return f32_to_bf16_bits(silu_mul(g, u));
+}
+
 // ------------------------------------------------------------------ MFMA ---
 // v_mfma_f32_16x16x32_bf16: A 16x32, B 32x16, C 16x16 fp32.
 // Lane l holds A row (l & 15) / B column (l & 15), eight consecutive

@@ -42,7 +42,7 @@ int launch_moe_sum(const void* in, void* out, int64_t m, int topk, int64_t k,
                    hipStream_t stream);
 int launch_moe_sum_routed(const void* in, void* out, int64_t m, int topk,
                           int64_t k, const int32_t* ids, int num_experts,
-                          hipStream_t stream);
+                          const float* weights, hipStream_t stream);
 int launch_quant_fp8_group(const void* x, void* q, float* scales, int64_t rows,
                            int64_t cols, int group, hipStream_t stream);
 int launch_quant_int8_token(const void* x, int8_t* q, float* scales,

@@ -13,7 +13,7 @@
 //   GEMM1 (replaces matmul_ogs with gather + _silu_and_mul_triton,
 //          ops/fused_moe.py:205-218): a2[row, c] = bf16(silu(g) * u)
 //   GEMM2 (replaces matmul_ogs with scatter + gammas, :224-231):
-//          y[slot, c] = bf16(gamma[slot] * acc)   (top-k sum: moe_sum)
+//          y[slot, c] = bf16(acc); the gamma-weighted top-k sum is moe_sum's
 #include "fgs_moe_kernels.h"
 
 namespace fgs {
@@ -278,20 +278,12 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
         v[nb] = x;
       }
       if constexpr (GEMM1) {
-        float g = v[0], u = v[NB - 1];
-        if (p.weight_on_input && valid) {
-          const float gm = p.topk_w[sid];
-          g *= gm;
-          u *= gm;
-        }
         out[static_cast<int64_t>(r) * p.n_out + col] =
-            f32_to_bf16_bits(silu_mul(g, u));
+            gemm1_epilogue(v[0], v[NB - 1], p.weight_on_input && valid,
+                           valid ? p.topk_w[sid] : 0.f);
       } else {
-        if (valid) {
-          float y = v[0];
-          if (!p.weight_on_input) y *= p.topk_w[sid];
-          out[static_cast<int64_t>(sid) * p.n_out + col] = f32_to_bf16_bits(y);
-        }
+        if (valid)
+          out[static_cast<int64_t>(sid) * p.n_out + col] = f32_to_bf16_bits(v[0]);
       }
     }
   }

@@ -47,6 +47,7 @@ struct Plan {
   int block_m;     // alignment block = rows per GEMM row block
   int mt;          // 16-row MFMA tiles per row block (streaming kernels)
   int kw1, kw2;    // waves splitting the contraction of GEMM1 / GEMM2
+  bool tiled;      // LDS-tiled MFMA kernels (prefill) instead of streaming
   int64_t max_padded, n_blocks;
   // workspace layout (byte offsets)
   int64_t o_sorted, o_eids, o_npp, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, total;
@@ -67,8 +68,14 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
          : qmode == FGS_QMODE_INT8_CHANNEL ? kDtInt8 : kDtBf16;
   const double rows_per_expert = static_cast<double>(numel) / e;
   p.mt = rows_per_expert <= 16 ? 1 : rows_per_expert <= 32 ? 2 : 4;
-  (void)flags;
   p.block_m = 16 * p.mt;
+  // Prefill schedule: enough rows per expert that a 256-row block is mostly
+  // real rows, and shapes the tiled kernels cover.
+  const bool tiled_ok = p.dt == kDtBf16 && inter % tiled_n_align(true) == 0 &&
+                        hidden % tiled_n_align(false) == 0;
+  p.tiled = tiled_ok && !(flags & FGS_FLAG_FORCE_DECODE) &&
+            ((flags & FGS_FLAG_FORCE_PREFILL) || rows_per_expert >= 192);
+  if (p.tiled) p.block_m = tiled_block_m();
   const int step = stream_step_k(p.dt);
   p.kw1 = pick_kw(hidden, step, 4);
   p.kw2 = pick_kw(inter, step, 8);
@@ -257,8 +264,10 @@ static int run_fused(const FusedArgs& a) {
   g1.numel = numel;
   g1.topk = a.topk;
   g1.weight_on_input = on_input;
-  rc = launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
-                          static_cast<int>(p.n_blocks), a.stream);
+  rc = p.tiled ? launch_gemm_tiled(p.dt, true, g1, static_cast<int>(p.n_blocks),
+                                   a.stream)
+               : launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
+                                    static_cast<int>(p.n_blocks), a.stream);
   if (rc) return rc;
   g_prof.mark(3, a.stream);
 
@@ -290,8 +299,10 @@ static int run_fused(const FusedArgs& a) {
   g2.kdim = a.inter;
   g2.n_out = a.hidden;
   g2.nrows_w = a.hidden;
-  rc = launch_gemm_stream(p.dt, false, g2, p.mt, p.kw2,
-                          static_cast<int>(p.n_blocks), a.stream);
+  rc = p.tiled ? launch_gemm_tiled(p.dt, false, g2, static_cast<int>(p.n_blocks),
+                                   a.stream)
+               : launch_gemm_stream(p.dt, false, g2, p.mt, p.kw2,
+                                    static_cast<int>(p.n_blocks), a.stream);
   if (rc) return rc;
   g_prof.mark(5, a.stream);
 

@@ -54,4 +54,10 @@ int stream_step_k(int dt);
 int launch_gemm_stream(int dt, bool gemm1, const GemmParams& p, int mt, int kw,
                        int row_blocks, hipStream_t stream);
 
+// LDS-tiled MFMA kernels (bf16): rows per block, n_out granularity, launch.
+int tiled_block_m();
+int tiled_n_align(bool gemm1);
+int launch_gemm_tiled(int dt, bool gemm1, const GemmParams& p, int row_blocks,
+                      hipStream_t stream);
+
 }  // namespace fgs

@@ -97,10 +97,11 @@ def test_triton_kernel_fused_experts_compat(gpu, shape):
     _check(res.cpu(), res_native.cpu(), "bf16", "compat vs native")
 
 
-@pytest.mark.parametrize("sched", [_capi.FLAG_FORCE_DECODE, 0],
-                         ids=["decode", "auto"])
+@pytest.mark.parametrize("sched", [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL, 0],
+                         ids=["decode", "prefill", "auto"])
 @pytest.mark.parametrize("shape", [(1, 128, 256, 8, 2), (96, 256, 512, 16, 4),
-                                   (700, 512, 256, 8, 2)])
+                                   (700, 512, 256, 8, 2), (1000, 1024, 384, 4, 2),
+                                   (3000, 768, 640, 8, 3)])
 def test_schedules_agree(gpu, shape, sched):
     M, K, N, E, topk = shape
     x, w1, w2, w, ids = _ref_inputs(M, K, N, E, topk, gpu)

@@ -29,6 +29,7 @@ struct GemmParams {
   int64_t numel;
   int32_t topk;
   int32_t weight_on_input;
+  int32_t row_blocks;     // row blocks of the launch (tiled kernels)
 };
 
 size_t align_smem_bytes(int num_experts);

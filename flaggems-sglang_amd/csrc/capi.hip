@@ -35,7 +35,8 @@ static int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
 constexpr int kMaxExperts = 1024;
 constexpr int kKnownFlags = FGS_FLAG_ROUTER_WEIGHT_ON_INPUT |
-                            FGS_FLAG_FORCE_DECODE | FGS_FLAG_FORCE_PREFILL;
+                            FGS_FLAG_FORCE_DECODE | FGS_FLAG_FORCE_PREFILL |
+                            FGS_FLAG_TILE_MASK;
 
 static int max_padded_of(int64_t numel, int e, int block) {
   return static_cast<int>(numel + static_cast<int64_t>(e) * (block - 1));
@@ -48,7 +49,8 @@ struct Plan {
   int mt;          // 16-row MFMA tiles per row block (streaming kernels)
   int kw1, kw2;    // waves splitting the contraction of GEMM1 / GEMM2
   bool tiled;      // LDS-tiled MFMA kernels (prefill) instead of streaming
-  int64_t max_padded, n_blocks;
+  int tile_cfg;    // tiled kernel configuration
+  int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
   int64_t o_sorted, o_eids, o_npp, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, total;
 };
@@ -73,14 +75,24 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // real rows, and shapes the tiled kernels cover.
   const bool tiled_ok = p.dt == kDtBf16 && inter % tiled_n_align(true) == 0 &&
                         hidden % tiled_n_align(false) == 0;
+  const int forced_cfg = ((flags & FGS_FLAG_TILE_MASK) >> 12) - 1;
   p.tiled = tiled_ok && !(flags & FGS_FLAG_FORCE_DECODE) &&
-            ((flags & FGS_FLAG_FORCE_PREFILL) || rows_per_expert >= 192);
-  if (p.tiled) p.block_m = tiled_block_m();
+            ((flags & FGS_FLAG_FORCE_PREFILL) || forced_cfg >= 0 ||
+             rows_per_expert > 16);
+  if (p.tiled) {
+    p.tile_cfg = forced_cfg >= 0 ? forced_cfg : tiled_config_for(rows_per_expert);
+    p.block_m = tiled_block_m(p.tile_cfg);
+  }
   const int step = stream_step_k(p.dt);
   p.kw1 = pick_kw(hidden, step, 4);
   p.kw2 = pick_kw(inter, step, 8);
   p.max_padded = max_padded_of(numel, e, p.block_m);
   p.n_blocks = p.max_padded / p.block_m;
+  // Blocks that can hold rows: each touched expert pads at most one partial
+  // block, so sum_e ceil(cnt_e / B) <= numel / B + min(E, numel). The GEMMs
+  // launch only these (the rest of the expert_ids buffer is -1 anyway).
+  p.n_launch = std::min<int64_t>(p.n_blocks,
+                                 numel / p.block_m + std::min<int64_t>(e, numel));
 
   const int64_t esz = p.dt == kDtBf16 ? 2 : 1;
   int64_t o = 0;
@@ -120,8 +132,11 @@ static int validate(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
       qmode != FGS_QMODE_INT8_CHANNEL)
     return fail(FGS_EINVAL, "unknown qmode");
   if (flags & ~kKnownFlags) return fail(FGS_EINVAL, "unknown flag bits");
-  if ((flags & FGS_FLAG_FORCE_DECODE) && (flags & FGS_FLAG_FORCE_PREFILL))
-    return fail(FGS_EINVAL, "FORCE_DECODE and FORCE_PREFILL are exclusive");
+  if ((flags & FGS_FLAG_FORCE_DECODE) &&
+      (flags & (FGS_FLAG_FORCE_PREFILL | FGS_FLAG_TILE_MASK)))
+    return fail(FGS_EINVAL, "FORCE_DECODE excludes FORCE_PREFILL / TILE");
+  if (((flags & FGS_FLAG_TILE_MASK) >> 12) > kTiledConfigs)
+    return fail(FGS_EINVAL, "unknown FGS_FLAG_TILE configuration");
   const int64_t numel = m * topk;
   if (numel + static_cast<int64_t>(e) * 64 >= (int64_t(1) << 31))
     return fail(FGS_EUNSUPPORTED, "m * topk too large for int32 slot ids");
@@ -264,10 +279,10 @@ static int run_fused(const FusedArgs& a) {
   g1.numel = numel;
   g1.topk = a.topk;
   g1.weight_on_input = on_input;
-  rc = p.tiled ? launch_gemm_tiled(p.dt, true, g1, static_cast<int>(p.n_blocks),
+  rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, static_cast<int>(p.n_launch),
                                    a.stream)
                : launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
-                                    static_cast<int>(p.n_blocks), a.stream);
+                                    static_cast<int>(p.n_launch), a.stream);
   if (rc) return rc;
   g_prof.mark(3, a.stream);
 
@@ -299,10 +314,10 @@ static int run_fused(const FusedArgs& a) {
   g2.kdim = a.inter;
   g2.n_out = a.hidden;
   g2.nrows_w = a.hidden;
-  rc = p.tiled ? launch_gemm_tiled(p.dt, false, g2, static_cast<int>(p.n_blocks),
+  rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, false, g2, static_cast<int>(p.n_launch),
                                    a.stream)
                : launch_gemm_stream(p.dt, false, g2, p.mt, p.kw2,
-                                    static_cast<int>(p.n_blocks), a.stream);
+                                    static_cast<int>(p.n_launch), a.stream);
   if (rc) return rc;
   g_prof.mark(5, a.stream);
 

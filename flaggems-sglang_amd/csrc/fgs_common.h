@@ -26,14 +26,9 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// Round-to-nearest-even f32 -> bf16 bit pattern (NaN stays a quiet NaN).
+// Round-to-nearest-even f32 -> bf16 bit pattern (gfx950 v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
-    return static_cast<uint16_t>((u >> 16) | 0x40);
-  }
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -42,9 +37,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // silu(g) * u in fp32, the activation of the reference's
-// _silu_and_mul_kernel (ops/fused_moe.py:58-62): g / (1 + exp(-g)) * u.
+// _silu_and_mul_kernel (ops/fused_moe.py:58-62): g / (1 + exp(-g)) * u,
+// with the division done as a hardware reciprocal (1 ulp).
 __device__ __forceinline__ float silu_mul(float g, float u) {
-  return g / (1.0f + __expf(-g)) * u;
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
 // GEMM1 epilogue with the rounding points of the reference's unfused path:

@@ -30,6 +30,7 @@ struct GemmParams {
   int32_t topk;
   int32_t weight_on_input;
   int32_t row_blocks;     // row blocks of the launch (tiled kernels)
+  int32_t group_n;        // column tiles per rasterization group (tiled)
 };
 
 size_t align_smem_bytes(int num_experts);
@@ -55,10 +56,13 @@ int stream_step_k(int dt);
 int launch_gemm_stream(int dt, bool gemm1, const GemmParams& p, int mt, int kw,
                        int row_blocks, hipStream_t stream);
 
-// LDS-tiled MFMA kernels (bf16): rows per block, n_out granularity, launch.
-int tiled_block_m();
+// LDS-tiled MFMA kernels (bf16): configuration per rows-per-expert regime,
+// its row block, n_out granularity, launch.
+constexpr int kTiledConfigs = 4;
+int tiled_config_for(double rows_per_expert);
+int tiled_block_m(int cfg);
 int tiled_n_align(bool gemm1);
-int launch_gemm_tiled(int dt, bool gemm1, const GemmParams& p, int row_blocks,
-                      hipStream_t stream);
+int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
+                      int row_blocks, hipStream_t stream);
 
 }  // namespace fgs

@@ -5,11 +5,10 @@
 // order from moe_align_block_size) and one 16-column output tile. Its KW
 // waves split the contraction; each wave streams its share of the 16 (or,
 // for GEMM1, 16 gate + 16 up) weight rows straight from HBM into MFMA
-// operand registers, with no LDS staging: every lane reads LB contiguous
-// bytes of one weight row per step, the four lane groups of a row cover
-// 4*LB contiguous bytes. The MFMA k index is only a label, so activations
-// are read with the identical lane -> k mapping and the contraction is
-// exact. Partial sums meet in LDS; wave 0 runs the epilogue:
+// operand registers, with no LDS staging: per step the four lane groups of
+// a row cover 4*LB contiguous bytes, 64 contiguous bytes per load
+// instruction. The MFMA k index is only a label, so activations are read
+// with the identical lane -> k mapping and the contraction is exact. Partial sums meet in LDS; wave 0 runs the epilogue:
 //   GEMM1 (replaces matmul_ogs with gather + _silu_and_mul_triton,
 //          ops/fused_moe.py:205-218): a2[row, c] = bf16(silu(g) * u)
 //   GEMM2 (replaces matmul_ogs with scatter + gammas, :224-231):
@@ -46,13 +45,18 @@ struct StreamTraits<kDtInt8> {
   typedef i32x4 Acc;
 };
 
+// Lane (n, g) of a step reads 16-byte vector v at byte v*64 + g*16 of its
+// row's step segment: the four lane groups of a row read 64 contiguous
+// bytes per load instruction (whole 64-byte segments for the memory
+// pipeline), and the MFMA k order is the same permutation for weights and
+// activations.
 template <int DT, int NV>
 __device__ __forceinline__ void load_frag(u32x4 (&f)[NV], const uint8_t* p,
                                           bool valid) {
   if (valid) {
 #pragma unroll
     for (int v = 0; v < NV; ++v)
-      f[v] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + v);
+      f[v] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + v * 64));
   } else {
 #pragma unroll
     for (int v = 0; v < NV; ++v) f[v] = u32x4{0, 0, 0, 0};
@@ -64,7 +68,7 @@ __device__ __forceinline__ void load_act(u32x4 (&f)[NV], const uint8_t* p,
                                          bool valid) {
   if (valid) {
 #pragma unroll
-    for (int v = 0; v < NV; ++v) f[v] = reinterpret_cast<const u32x4*>(p)[v];
+    for (int v = 0; v < NV; ++v) f[v] = *reinterpret_cast<const u32x4*>(p + v * 64);
   } else {
 #pragma unroll
     for (int v = 0; v < NV; ++v) f[v] = u32x4{0, 0, 0, 0};
@@ -134,7 +138,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
     const int sid = p.sorted_ids[r];
     avalid[mt] = sid < p.numel;
     const int64_t src = GEMM1 ? (avalid[mt] ? sid / p.topk : 0) : r;
-    arow[mt] = p.a + (src * p.kdim) * ESZ + lg * T::kLaneBytes;
+    arow[mt] = p.a + (src * p.kdim) * ESZ + lg * 16;
   }
   // Weight rows of lane ln.
   const uint8_t* brow[NB];
@@ -142,7 +146,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int64_t n = wbase + (nb ? p.n_out : 0) + n0 + ln;
-    brow[nb] = p.w + (n * p.kdim) * ESZ + lg * T::kLaneBytes;
+    brow[nb] = p.w + (n * p.kdim) * ESZ + lg * 16;
   }
 
   // fp8 / int8 activation scales of this lane's accumulator rows.

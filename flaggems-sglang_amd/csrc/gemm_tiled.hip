@@ -3,16 +3,19 @@
 //
 // A workgroup of WM x WN waves owns a BM-row block of the expert-sorted,
 // padded row order (one expert per block, from moe_align_block_size) and
-// BNR weight rows. Each k-step stages a BM x 128-byte activation tile and a
-// BNR x 128-byte weight tile in LDS (double buffered: the next step's global
-// loads are in flight while the current step's MFMAs run), and each wave
-// multiplies its (BM/WM) x (BNR/WN) sub-tile with v_mfma_f32_32x32x16_bf16.
+// BNR weight rows. Activation and weight tiles stream into a STAGES-deep LDS
+// ring with LDS-DMA loads (global_load_lds_dwordx4: no staging registers),
+// SK bytes of k per stage. Each wave multiplies its (BM/WM) x (BNR/WN)
+// sub-tile with v_mfma_f32_32x32x16_bf16; the fragments of the next half
+// stage are read while the current MFMAs run.
 //
-// GEMM1 (fused activation): the weight tile interleaves 64 gate rows and the
-// 64 matching up rows per wave column, so every lane holds the gate and up
+// GEMM1 (fused activation): each wave's weight rows are its gate rows
+// followed by the matching up rows, so every lane holds the gate and up
 // accumulators of the same output element; the epilogue applies the
 // reference's rounding points and silu (ops/fused_moe.py:205-218).
-// GEMM2: plain y = a2 W2^T per padded row, scattered to its top-k slot.
+// GEMM2: y = a2 W2^T per padded row, stored (bf16) at its top-k slot.
+#include <stdlib.h>
+
 #include <mutex>
 #include <string>
 
@@ -20,41 +23,11 @@
 
 namespace fgs {
 
-constexpr int kStageK = 64;  // bytes of k per stage row (32 bf16)
-constexpr int kLoadRows = 16;  // rows one wave-wide 16 B/lane LDS-DMA load covers
-
-// XOR swizzle of the four 16-byte chunks of a 64-byte LDS row. The DMA
-// writes rows densely (lane l -> byte 16*l of a 1 KiB block), so rows are not
-// padded; instead row r keeps logical chunk c at chunk c ^ swz(r), which puts
-// the 8 rows any 8 consecutive lanes read in distinct 16-byte bank groups.
-__device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
-
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Tile order. The grid is 1-D and padded to a multiple of the 8 XCDs.
-// Workgroup `pid` runs on XCD pid % 8, so logical tile
-// (pid % 8) * (grid / 8) + pid / 8 gives every XCD a contiguous range of
-// tiles, walked in groups of kGroupN column tiles: the ~32 workgroups an
-// XCD runs at once cover a few row blocks x kGroupN column tiles and share
-// their activation and weight tiles through that XCD's L2.
-constexpr int kGroupN = 8;
-
-__device__ __forceinline__ bool tile_of(int pid, int grid, int n_rb, int n_ct,
-                                        int* rb, int* ct) {
-  const int logical = (pid % 8) * (grid / 8) + pid / 8;
-  if (logical >= n_rb * n_ct) return false;
-  const int span = n_rb * kGroupN;
-  const int group = logical / span;
-  const int idx = logical - group * span;
-  const int gsize = min(kGroupN, n_ct - group * kGroupN);
-  *rb = idx / gsize;
-  *ct = group * kGroupN + idx % gsize;
-  return true;
 }
 
 // One wave-wide LDS-DMA load: lane l copies 16 bytes from `src` (its own
@@ -66,32 +39,78 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
 
 __device__ __forceinline__ void wave_barrier_all() { __builtin_amdgcn_s_barrier(); }
 
-template <int BM, int BNR, int WM, int WN, int STAGES, bool GEMM1>
-__global__ __launch_bounds__(WM * WN * 64, 1) void moe_gemm_tiled_bf16_kernel(
+// Tile order. The grid is 1-D and padded to a multiple of the 8 XCDs.
+// Workgroup `pid` runs on XCD pid % 8, so logical tile
+// (pid % 8) * (grid / 8) + pid / 8 gives every XCD a contiguous range of
+// tiles, walked in groups of group_n column tiles: the workgroups an XCD runs
+// at once cover a few row blocks x group_n column tiles and share their
+// activation and weight tiles through that XCD's L2.
+__device__ __forceinline__ bool tile_of(int pid, int grid, int n_rb, int n_ct,
+                                        int group_n, int* rb, int* ct) {
+  const int logical = (pid % 8) * (grid / 8) + pid / 8;
+  if (logical >= n_rb * n_ct) return false;
+  const int span = n_rb * group_n;
+  const int group = logical / span;
+  const int idx = logical - group * span;
+  const int gsize = min(group_n, n_ct - group * group_n);
+  *rb = idx / gsize;
+  *ct = group * group_n + idx % gsize;
+  return true;
+}
+
+template <int BM_, int BNR_, int WM_, int WN_, int SK_, int STAGES_>
+struct TileCfg {
+  static constexpr int BM = BM_;        // rows (alignment block size)
+  static constexpr int BNR = BNR_;      // weight rows per tile
+  static constexpr int WM = WM_, WN = WN_;
+  static constexpr int SK = SK_;        // k bytes per LDS stage row
+  static constexpr int STAGES = STAGES_;
+  static constexpr int NW = WM * WN;
+  static constexpr int CPR = SK / 16;   // 16-byte chunks per stage row
+  static constexpr int LR = 64 / CPR;   // rows one LDS-DMA wave load covers
+  static constexpr int RPL = 256 / SK;  // stage rows per 256-byte bank line
+  static constexpr int LDS_BYTES = STAGES * (BM + BNR) * SK;
+  static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KiB");
+};
+
+// Swizzled position of logical 16-byte chunk c of stage row r. The DMA
+// writes rows densely (lane l -> byte 16*l of a 1 KiB block), so rows are
+// not padded; gfx950's LDS serves a 16-byte-per-lane read 16 lanes (256
+// bytes, all 64 banks) at a time, and the XOR with (r / RPL) % CPR gives
+// the 16 consecutive rows such a group reads 16 distinct bank positions.
+template <class C>
+__device__ __forceinline__ int chunk_pos(int r, int c) {
+  return c ^ ((r / C::RPL) % C::CPR);
+}
+
+template <class C, bool GEMM1>
+__global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
     const GemmParams p) {
-  constexpr int NW = WM * WN;
-  constexpr int A_BYTES = BM * kStageK;
-  constexpr int B_BYTES = BNR * kStageK;
+  constexpr int BM = C::BM, BNR = C::BNR, SK = C::SK, STAGES = C::STAGES;
+  constexpr int NW = C::NW, WN = C::WN;
+  constexpr int A_BYTES = BM * SK;
+  constexpr int B_BYTES = BNR * SK;
   constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int NLA = BM / (kLoadRows * NW);   // A loads per wave per stage
-  constexpr int NLB = BNR / (kLoadRows * NW);  // B loads per wave per stage
+  constexpr int NLA = BM / (C::LR * NW);   // A loads per wave per stage
+  constexpr int NLB = BNR / (C::LR * NW);  // B loads per wave per stage
   constexpr int NL = NLA + NLB;
-  constexpr int WROWS = BM / WM;               // rows per wave
-  constexpr int WCOLS = BNR / WN;              // weight rows per wave
-  constexpr int RB = WROWS / 32;               // 32-row MFMA blocks
-  constexpr int CB = WCOLS / 32;               // 32-col MFMA blocks
-  static_assert(NLA * kLoadRows * NW == BM, "A tile / waves");
-  static_assert(NLB * kLoadRows * NW == BNR, "B tile / waves");
-  static_assert(STAGES >= 3 && STAGES <= 5, "stages");
+  constexpr int WROWS = BM / C::WM;        // rows per wave
+  constexpr int WCOLS = BNR / WN;          // weight rows per wave
+  constexpr int RB = WROWS / 32;           // 32-row MFMA blocks
+  constexpr int CB = WCOLS / 32;           // 32-col MFMA blocks
+  constexpr int KK = SK / 32;              // 16-element k steps per stage
+  static_assert(NLA * C::LR * NW == BM, "A tile / waves");
+  static_assert(NLB * C::LR * NW == BNR, "B tile / waves");
+  static_assert(STAGES >= 3 && (STAGES - 2) * NL < 64, "stages");
   static_assert(RB >= 1 && CB >= 1, "wave tile");
-  static_assert(!GEMM1 || (WCOLS % 64 == 0 && CB % 2 == 0), "gate/up pairing");
+  static_assert(!GEMM1 || CB % 2 == 0, "gate/up pairing");
 
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
   constexpr int N_PER_TILE = GEMM1 ? BNR / 2 : BNR;
   int rb_id, tile_n;
   if (!tile_of(blockIdx.x, gridDim.x, p.row_blocks,
-               static_cast<int>(p.n_out / N_PER_TILE), &rb_id, &tile_n))
+               static_cast<int>(p.n_out / N_PER_TILE), p.group_n, &rb_id, &tile_n))
     return;
   if (rb_id * BM >= p.num_post_pad[0]) return;
   const int e = p.expert_ids[rb_id];
@@ -103,36 +122,40 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void moe_gemm_tiled_bf16_kernel(
   const int wn = wave % WN;
   const int row0 = rb_id * BM;
 
-  // ---- this lane's source of each LDS-DMA load (row lane/4, chunk lane%4)
-  const int lrow = lane >> 2;
-  const int lchunk = lane & 3;
+  // ---- this lane's source of each LDS-DMA load: row lane/CPR, chunk lane%CPR
+  const int lrow = lane / C::CPR;
+  const int lchunk = lane % C::CPR;
   const uint8_t* a_src[NLA];
 #pragma unroll
   for (int i = 0; i < NLA; ++i) {
-    const int r = (wave * NLA + i) * kLoadRows + lrow;
+    const int r = (wave * NLA + i) * C::LR + lrow;
     const int sid = p.sorted_ids[row0 + r];
     // pad rows read token 0 / their own row: finite values, never stored
     const int64_t src = GEMM1 ? (sid < p.numel ? sid / p.topk : 0) : row0 + r;
-    a_src[i] = p.a + src * p.kdim * 2 + ((lchunk ^ swz(r)) * 16);
+    a_src[i] = p.a + src * p.kdim * 2 + chunk_pos<C>(r, lchunk) * 16;
   }
   const uint8_t* b_src[NLB];
   const int64_t wbase = static_cast<int64_t>(e) * p.nrows_w;
 #pragma unroll
   for (int i = 0; i < NLB; ++i) {
-    const int j = (wave * NLB + i) * kLoadRows + lrow;  // tile row
+    const int j = (wave * NLB + i) * C::LR + lrow;  // tile row
     int64_t wrow;
     if constexpr (GEMM1) {
-      // rows [64q, 64q+64): q even -> gate, q odd -> up, column block q/2
-      const int q = j / 64;
-      wrow = (q & 1 ? p.n_out : 0) + tile_n * (BNR / 2) + (q / 2) * 64 + j % 64;
+      // tile rows of wave column wc: WCOLS/2 gate rows, then the same
+      // output columns' up rows
+      constexpr int HALF = WCOLS / 2;
+      const int wc = j / WCOLS;
+      const int in = j % WCOLS;
+      const int ncol = tile_n * (BNR / 2) + wc * HALF + in % HALF;
+      wrow = (in >= HALF ? p.n_out : 0) + ncol;
     } else {
       wrow = static_cast<int64_t>(tile_n) * BNR + j;
     }
-    b_src[i] = p.w + (wbase + wrow) * p.kdim * 2 + ((lchunk ^ swz(j)) * 16);
+    b_src[i] = p.w + (wbase + wrow) * p.kdim * 2 + chunk_pos<C>(j, lchunk) * 16;
   }
 
   auto issue = [&](int kt, int slot) {
-    const int64_t koff = static_cast<int64_t>(kt) * kStageK;
+    const int64_t koff = static_cast<int64_t>(kt) * SK;
     uint8_t* base = lds + slot * STAGE;
 #pragma unroll
     for (int i = 0; i < NLA; ++i)
@@ -153,21 +176,23 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void moe_gemm_tiled_bf16_kernel(
   // Fragment reads: lane reads row (lane & 31) of a 32-row block, logical
   // chunk 2*kk + (lane >> 5) (16 bf16 of k per kk step).
   const int fr = lane & 31;
-  int frag_off[2];
+  int frag_off[KK];
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-    frag_off[kk] = fr * kStageK + (((2 * kk + (lane >> 5)) ^ swz(fr)) * 16);
-  const int a_base = wm * WROWS * kStageK;
-  const int b_base = A_BYTES + wn * WCOLS * kStageK;
+  for (int kk = 0; kk < KK; ++kk)
+    frag_off[kk] = fr * SK + chunk_pos<C>(fr, 2 * kk + (lane >> 5)) * 16;
+  const int a_base = wm * WROWS * SK;
+  const int b_base = A_BYTES + wn * WCOLS * SK;
 
-  const int KT = static_cast<int>(p.kdim * 2 / kStageK);
+  const int KT = static_cast<int>(p.kdim * 2 / SK);
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < KT) issue(s, s);
 
   // Waits until at most `n` of this wave's later stages are in flight.
   auto wait_stages = [&](int n) {
-    if (n >= 3) wait_vmcnt<3 * NL>();
+    if (n >= 5) wait_vmcnt<(5 * NL < 64 ? 5 * NL : 0)>();
+    else if (n == 4) wait_vmcnt<(4 * NL < 64 ? 4 * NL : 0)>();
+    else if (n == 3) wait_vmcnt<(3 * NL < 64 ? 3 * NL : 0)>();
     else if (n == 2) wait_vmcnt<2 * NL>();
     else if (n == 1) wait_vmcnt<NL>();
     else wait_vmcnt<0>();
@@ -176,73 +201,104 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void moe_gemm_tiled_bf16_kernel(
     const uint8_t* st = lds + (kt % STAGES) * STAGE;
 #pragma unroll
     for (int i = 0; i < RB; ++i)
-      fa[i] = *reinterpret_cast<const bf16x8*>(st + a_base + i * 32 * kStageK +
+      fa[i] = *reinterpret_cast<const bf16x8*>(st + a_base + i * 32 * SK +
                                                frag_off[kk]);
 #pragma unroll
     for (int j = 0; j < CB; ++j)
-      fb[j] = *reinterpret_cast<const bf16x8*>(st + b_base + j * 32 * kStageK +
+      fb[j] = *reinterpret_cast<const bf16x8*>(st + b_base + j * 32 * SK +
                                                frag_off[kk]);
   };
+  // Weights are the MFMA's A operand and activations its B operand, so the
+  // 32x32 accumulator is transposed: lane l holds token (l & 31) and four
+  // runs of 4 consecutive output columns -> 8-byte stores in the epilogue.
   auto mma = [&](const bf16x8 (&fa)[RB], const bf16x8 (&fb)[CB]) {
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
-      for (int j = 0; j < CB; ++j) acc[i][j] = mfma32_bf16(fa[i], fb[j], acc[i][j]);
+      for (int j = 0; j < CB; ++j) acc[i][j] = mfma32_bf16(fb[j], fa[i], acc[i][j]);
   };
 
-  // Software pipeline: the fragments of the next half-stage are read from
-  // LDS while the MFMAs of the current one run; the barrier that publishes
-  // stage kt+1 (and frees slot kt-1 for the next DMA) sits between the two
-  // halves of stage kt.
-  bf16x8 fa0[RB], fb0[CB], fa1[RB], fb1[CB];
+  // Software pipeline over half-stage fragment sets: the fragments of the
+  // next k step are read from LDS while the MFMAs of the current one run;
+  // the barrier that publishes stage kt+1 (and frees slot kt-1 for the next
+  // DMA) sits before the last k step of stage kt. The last stage is peeled
+  // so the loop body has no branch around LDS reads.
+  bf16x8 fa[2][RB], fb[2][CB];
   wait_stages(min(STAGES - 2, KT - 1));
   wave_barrier_all();
-  read_frags(0, 0, fa0, fb0);
-  // (the last stage is peeled so the loop body has no branch around LDS
-  // reads, which lets the compiler wait for exactly the fragments it needs)
+  read_frags(0, 0, fa[0], fb[0]);
   for (int kt = 0; kt + 1 < KT; ++kt) {
-    read_frags(kt, 1, fa1, fb1);
-    mma(fa0, fb0);
+#pragma unroll
+    for (int kk = 0; kk + 1 < KK; ++kk) {
+      read_frags(kt, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+      mma(fa[kk & 1], fb[kk & 1]);
+    }
     wait_stages(min(STAGES - 3, KT - 2 - kt));
     wave_barrier_all();
     if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-    read_frags(kt + 1, 0, fa0, fb0);
-    mma(fa1, fb1);
+    read_frags(kt + 1, 0, fa[KK & 1], fb[KK & 1]);
+    mma(fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
+    if constexpr (KK & 1) {
+      // odd KK: the next stage's first fragments landed in set 1; move them
+      // to set 0 where the next iteration expects them
+#pragma unroll
+      for (int i = 0; i < RB; ++i) fa[0][i] = fa[1][i];
+#pragma unroll
+      for (int j = 0; j < CB; ++j) fb[0][j] = fb[1][j];
+    }
   }
-  read_frags(KT - 1, 1, fa1, fb1);
-  mma(fa0, fb0);
-  mma(fa1, fb1);
+#pragma unroll
+  for (int kk = 0; kk + 1 < KK; ++kk) {
+    read_frags(KT - 1, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+    mma(fa[kk & 1], fb[kk & 1]);
+  }
+  mma(fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
 
-  // ---- epilogue: lane owns column (lane & 31) of each 32x32 block and rows
-  // 8*(v>>2) + 4*(lane>>5) + (v&3).
+  // ---- epilogue: lane owns token row (lane & 31) of each 32-row block and,
+  // in each 32-column block, columns 8*q + 4*(lane>>5) + {0..3}, q = 0..3
+  // (accumulator registers 4q..4q+3).
   uint16_t* out = static_cast<uint16_t*>(p.out);
-  const int ccol = lane & 31;
+  const int csub = 4 * (lane >> 5);
 #pragma unroll
   for (int i = 0; i < RB; ++i) {
+    const int r = row0 + wm * WROWS + i * 32 + (lane & 31);
+    const int sid = p.sorted_ids[r];
+    const bool valid = sid < p.numel;
+    if constexpr (GEMM1) {
+      const bool scale = p.weight_on_input && valid;
+      const float gamma = scale ? p.topk_w[sid] : 0.f;
+      uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int r = row0 + wm * WROWS + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-      const int sid = p.sorted_ids[r];
-      const bool valid = sid < p.numel;
-      if constexpr (GEMM1) {
-        const float gamma = (p.weight_on_input && valid) ? p.topk_w[sid] : 0.f;
+      for (int jb = 0; jb < CB / 2; ++jb) {
+        const int col0 = tile_n * (BNR / 2) + wn * (WCOLS / 2) + jb * 32 + csub;
 #pragma unroll
-        for (int jb = 0; jb < CB / 2; ++jb) {
-          // wave columns: [gate 64 | up 64] per 64-column group
-          const int q = jb / 2;
-          const int h = jb % 2;
-          const float g = acc[i][q * 4 + h][v];
-          const float u = acc[i][q * 4 + 2 + h][v];
-          const int col = tile_n * (BNR / 2) + wn * (WCOLS / 2) + q * 64 + h * 32 + ccol;
-          out[static_cast<int64_t>(r) * p.n_out + col] =
-              gemm1_epilogue(g, u, p.weight_on_input && valid, gamma);
+        for (int g4 = 0; g4 < 4; ++g4) {
+          uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t b = gemm1_epilogue(acc[i][jb][4 * g4 + t],
+                                              acc[i][jb + CB / 2][4 * g4 + t], scale, gamma);
+            if (t < 2) w0 |= b << (16 * t);
+            else w1 |= b << (16 * (t - 2));
+          }
+          uint2 v2;
+          v2.x = w0;
+          v2.y = w1;
+          *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
         }
-      } else {
-        if (valid) {
+      }
+    } else {
+      if (valid) {
+        uint16_t* orow = out + static_cast<int64_t>(sid) * p.n_out;
 #pragma unroll
-          for (int j = 0; j < CB; ++j) {
-            const int col = tile_n * BNR + wn * WCOLS + j * 32 + ccol;
-            out[static_cast<int64_t>(sid) * p.n_out + col] = f32_to_bf16_bits(acc[i][j][v]);
+        for (int j = 0; j < CB; ++j) {
+          const int col0 = tile_n * BNR + wn * WCOLS + j * 32 + csub;
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            uint2 v2;
+            v2.x = pack_bf16x2(acc[i][j][4 * g4], acc[i][j][4 * g4 + 1]);
+            v2.y = pack_bf16x2(acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3]);
+            *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
           }
         }
       }
@@ -250,39 +306,91 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void moe_gemm_tiled_bf16_kernel(
   }
 }
 
-template <int BM, int BNR, int WM, int WN, int STAGES, bool GEMM1>
+// Column tiles per rasterization group (FGS_MOE_GROUPN overrides; a tuning
+// aid read once).
+static int group_n_choice() {
+  static const int g = [] {
+    const char* s = getenv("FGS_MOE_GROUPN");
+    const int v = s ? atoi(s) : 2;
+    return (v >= 1 && v <= 64) ? v : 2;
+  }();
+  return g;
+}
+
+template <class C, bool GEMM1>
 static int launch_tiled(const GemmParams& p, int row_blocks, hipStream_t stream) {
-  constexpr int kLds = STAGES * (BM + BNR) * kStageK;
-  auto kern = moe_gemm_tiled_bf16_kernel<BM, BNR, WM, WN, STAGES, GEMM1>;
+  auto kern = moe_gemm_tiled_bf16_kernel<C, GEMM1>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&] {
     attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               C::LDS_BYTES);
   });
   if (attr != hipSuccess)
     return fail(FGS_ELAUNCH, std::string("tiled GEMM LDS opt-in: ") +
                                  hipGetErrorString(attr));
-  const int tiles_n = static_cast<int>(GEMM1 ? p.n_out / (BNR / 2) : p.n_out / BNR);
+  const int tiles_n = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   GemmParams q = p;
   q.row_blocks = row_blocks;
+  q.group_n = group_n_choice();
   const int tiles = (row_blocks * tiles_n + 7) / 8 * 8;
-  hipLaunchKernelGGL(kern, dim3(tiles), dim3(WM * WN * 64), kLds, stream, q);
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(C::NW * 64), C::LDS_BYTES, stream, q);
   return check_launch("moe_gemm_tiled_bf16_kernel");
 }
 
-int tiled_block_m() { return 256; }
+// Tile configurations (BM, BNR, WM, WN, SK, STAGES), one per rows-per-expert
+// regime. Small row blocks keep padding low and still read every weight
+// tile once per block; the 256-row tile has the highest MFMA intensity.
+using Cfg256 = TileCfg<256, 256, 4, 2, 64, 4>;  // 8 waves of 64x128
+using Cfg128 = TileCfg<128, 256, 2, 4, 64, 6>;  // 8 waves of 64x64
+using Cfg64 = TileCfg<64, 256, 1, 4, 128, 4>;   // 4 waves of 64x64
+using Cfg32 = TileCfg<32, 256, 1, 4, 128, 4>;   // 4 waves of 32x64
 
-// n_out granularity the tiled kernels need (GEMM1 output cols per tile,
-// GEMM2 output cols per tile).
+static const int kTileRows[kTiledConfigs] = {Cfg256::BM, Cfg128::BM, Cfg64::BM,
+                                             Cfg32::BM};
+
+// FGS_MOE_TILE (0..3) forces one configuration (a tuning aid; read once).
+static int forced_tile() {
+  static const int forced = [] {
+    const char* s = getenv("FGS_MOE_TILE");
+    if (!s) return -1;
+    const int v = atoi(s);
+    return (v >= 0 && v < kTiledConfigs) ? v : -1;
+  }();
+  return forced;
+}
+
+int tiled_config_for(double rows_per_expert) {
+  if (forced_tile() >= 0) return forced_tile();
+  if (rows_per_expert >= 192) return 0;
+  if (rows_per_expert >= 96) return 1;
+  if (rows_per_expert >= 40) return 2;
+  return 3;
+}
+
+int tiled_block_m(int cfg) { return kTileRows[cfg]; }
+
+// n_out granularity the tiled kernels need: GEMM1 output cols per tile,
+// GEMM2 output cols per tile (every configuration uses BNR = 256).
 int tiled_n_align(bool gemm1) { return gemm1 ? 128 : 256; }
 
-int launch_gemm_tiled(int dt, bool gemm1, const GemmParams& p, int row_blocks,
-                      hipStream_t stream) {
+int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
+                      int row_blocks, hipStream_t stream) {
   if (dt != kDtBf16) return fail(FGS_EUNSUPPORTED, "tiled GEMM: bf16 only");
   if (row_blocks <= 0) return FGS_OK;
-  if (gemm1) return launch_tiled<256, 256, 4, 2, 4, true>(p, row_blocks, stream);
-  return launch_tiled<256, 256, 4, 2, 4, false>(p, row_blocks, stream);
+#define FGS_TILE_CASE(I, CFG)                                          \
+  case I:                                                              \
+    return gemm1 ? launch_tiled<CFG, true>(p, row_blocks, stream)      \
+                 : launch_tiled<CFG, false>(p, row_blocks, stream);
+  switch (cfg) {
+    FGS_TILE_CASE(0, Cfg256)
+    FGS_TILE_CASE(1, Cfg128)
+    FGS_TILE_CASE(2, Cfg64)
+    FGS_TILE_CASE(3, Cfg32)
+  }
+#undef FGS_TILE_CASE
+  return fail(FGS_EINVAL, "tiled GEMM: unknown configuration");
 }
 
 }  // namespace fgs

@@ -23,6 +23,12 @@ QMODE_INT8_CHANNEL = 2
 FLAG_ROUTER_WEIGHT_ON_INPUT = 0x1
 FLAG_FORCE_DECODE = 0x100
 FLAG_FORCE_PREFILL = 0x200
+TILED_CONFIGS = 4  # row blocks 256, 128, 64, 32
+
+
+def flag_tile(cfg: int) -> int:
+    """Schedule flag forcing tiled configuration ``cfg`` (FGS_FLAG_TILE)."""
+    return ((cfg + 1) & 0x7) << 12
 
 LIB_NAME = "libfgs_moe.so"
 

@@ -48,6 +48,10 @@ extern "C" {
 #define FGS_FLAG_ROUTER_WEIGHT_ON_INPUT 0x1 /* gammas on GEMM1 output rows */
 #define FGS_FLAG_FORCE_DECODE 0x100         /* schedule: streaming kernels  */
 #define FGS_FLAG_FORCE_PREFILL 0x200        /* schedule: LDS-tiled kernels  */
+/* schedule: LDS-tiled kernels with row-block configuration c (0: 256 rows,
+ * 1: 128, 2: 64, 3: 32) instead of the rows-per-expert choice */
+#define FGS_FLAG_TILE(c) ((((c) + 1) & 0x7) << 12)
+#define FGS_FLAG_TILE_MASK 0x7000
 
 /* Library version string, e.g. "fgs_moe 0.1.0 gfx950". */
 const char* fgs_moe_version(void);

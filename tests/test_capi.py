@@ -55,7 +55,10 @@ def test_align_max_padded():
         ((1, 4096, 14336, 8, 9, 0, 0), _capi.FGS_EINVAL, "topk"),
         ((1, 4096, 14336, 8, 2, 7, 0), _capi.FGS_EINVAL, "qmode"),
         ((1, 4096, 14336, 8, 2, 0, 0x40), _capi.FGS_EINVAL, "flag"),
-        ((1, 4096, 14336, 8, 2, 0, 0x300), _capi.FGS_EINVAL, "exclusive"),
+        ((1, 4096, 14336, 8, 2, 0, 0x300), _capi.FGS_EINVAL, "excludes"),
+        ((1, 4096, 14336, 8, 2, 0, 0x100 | 0x1000), _capi.FGS_EINVAL, "excludes"),
+        ((1, 4096, 14336, 8, 2, 0, 0x5000), _capi.FGS_EINVAL, "TILE"),
+        ((1, 4096, 14336, 8, 2, 0, 0x4000), 0, ""),
         ((1, 4000, 14336, 8, 2, 0, 0), _capi.FGS_EUNSUPPORTED, "multiples"),
         ((1, 3584, 2560, 64, 8, 2, 0), 0, ""),
         ((1, 3584 - 128, 2560, 64, 8, 2, 0), _capi.FGS_EUNSUPPORTED, "multiples"),

@@ -110,6 +110,20 @@ def test_schedules_agree(gpu, shape, sched):
     _check(res.cpu()[_sample(M, 64)], ref, "bf16", f"sched {sched} {shape}")
 
 
+@pytest.mark.parametrize("cfg", range(_capi.TILED_CONFIGS))
+@pytest.mark.parametrize("shape", [(40, 256, 256, 4, 2), (300, 512, 384, 8, 3),
+                                   (1500, 1024, 1024, 8, 2)])
+def test_tiled_configs(gpu, shape, cfg):
+    """Every LDS-tiled configuration, forced, on shapes that leave partial
+    and empty row blocks."""
+    M, K, N, E, topk = shape
+    x, w1, w2, w, ids = _ref_inputs(M, K, N, E, topk, gpu)
+    res = fm.fused_moe(x, w1, w2, w, ids, _flags=_capi.flag_tile(cfg))
+    toks = _sample(M, 64)
+    ref = moe_ref.fused_moe(x, w1, w2, w, ids, tokens=toks, return_mag=True)
+    _check(res.cpu()[toks], ref, "bf16", f"tile {cfg} {shape}")
+
+
 def test_dropped_slots_and_routed_scaling(gpu):
     x, w1, w2, w, ids = _ref_inputs(16, 256, 128, 4, 2, gpu)
     ids2 = ids.clone()

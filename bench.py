@@ -52,7 +52,26 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep-steps", type=int, default=10)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy (the reference "
+                         "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def calibrate_copy():
+    """A plain device-to-device copy of known size: its FETCH_SIZE and
+    WRITE_SIZE readings give the counter-to-byte factor for the traffic
+    figures (read 1 GiB, write 1 GiB per launch)."""
+    import torch
+
+    n = 1 << 30
+    src = torch.ones(n // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "torch copy_", "bytes_read": n,
+                      "bytes_written": n, "launches": 3}), flush=True)
 
 
 class Layer:
@@ -123,6 +142,20 @@ def time_layer(layer, steps, warmup, flush):
     return ms, stages
 
 
+def measured_traffic(cfg_name, M, stage):
+    """HBM bytes per launch of a stage's kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/traffic_<cfg>.json,
+    copy-calibrated), or None when that configuration was not profiled."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        entry = json.load(f).get("by_stage", {}).get(f"{cfg_name}:{M}:{stage}")
+    if not entry:
+        return None
+    return entry
+
+
 def dominant(layer, stages):
     """Roofline object for the slowest stage (a GEMM in every config)."""
     cfg = layer.cfg
@@ -142,17 +175,24 @@ def dominant(layer, stages):
     gbs = (wbytes + io) / t / 1e9
     frac_mfma = tflops / PEAK_TFLOPS[cfg.mode]
     frac_hbm = gbs / PEAK_HBM_GBS
+    meas = measured_traffic(cfg.name, M, name)
+    traffic = None if meas is None else round(meas["fetch_bytes"] + meas["write_bytes"])
+    extra = {"algorithmic_bytes": round(wbytes + io),
+             "traffic_source": None if meas is None else
+             "profiles/traffic_%s.json: rocprofv3 FETCH_SIZE + WRITE_SIZE per "
+             "dispatch, scaled by a 1 GiB copy (profiled avg %.4f ms)"
+             % (cfg.name, meas["avg_ns"] / 1e6)}
     if frac_mfma >= frac_hbm:
         return {"kernel": f"moe_gemm ({name})", "bound": "mfma",
                 "achieved": round(tflops, 2), "peak": PEAK_TFLOPS[cfg.mode],
-                "unit": "TFLOP/s", "frac": round(frac_mfma, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(frac_mfma, 4), "traffic": traffic,
                 "per_unit": f"{'4' if name == 'gemm1' else '2'}*M*topk*K*N flops",
-                "avg_ms": round(stages[name], 4)}
+                "avg_ms": round(stages[name], 4), **extra}
     return {"kernel": f"moe_gemm ({name})", "bound": "hbm",
             "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(frac_hbm, 4), "traffic": None,
+            "frac": round(frac_hbm, 4), "traffic": traffic,
             "per_unit": "touched_experts * weight bytes + activations",
-            "avg_ms": round(stages[name], 4)}
+            "avg_ms": round(stages[name], 4), **extra}
 
 
 def row(layer, ms, stages):
@@ -214,6 +254,9 @@ def main():
               f"multi-GPU part here); --gpus {args.gpus} is not supported",
               file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     import torch
 
     from flaggems_sglang import _capi, testing

@@ -4,6 +4,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <array>
 #include <mutex>
 #include <string>
@@ -50,10 +51,39 @@ struct Plan {
   int kw1, kw2;    // waves splitting the contraction of GEMM1 / GEMM2
   bool tiled;      // LDS-tiled MFMA kernels (prefill) instead of streaming
   int tile_cfg;    // tiled kernel configuration
+  int ksplit2;     // GEMM2 k splits (tiled only; > 1 -> fp32 partials)
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
   int64_t o_sorted, o_eids, o_npp, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, total;
 };
+
+// k splits for the tiled GEMM2: its grid (row blocks x hidden/256 column
+// tiles) is often a few waves of 256 workgroups, and a partial last wave
+// idles most CUs for a whole tile. Pick the smallest split (<= 4, keeping
+// >= 8 stages of 64 k per split) whose expected grid fills >= 90 % of its
+// last wave, else the best one. Row blocks are estimated for balanced
+// routing: numel / B plus half a padded block per touched expert.
+constexpr int kNumCUs = 256;  // MI355X
+
+static int pick_ksplit(int64_t numel, int e, int bm, int64_t hidden,
+                       int64_t inter) {
+  const double blocks = static_cast<double>(numel) / bm +
+                        0.5 * static_cast<double>(std::min<int64_t>(e, numel));
+  const double wgs = blocks * static_cast<double>(hidden / 256);
+  int best = 1;
+  double best_eff = 0.0;
+  for (int s = 1; s <= 4; ++s) {
+    if (inter / 32 < 8 * s) break;
+    const double waves = wgs * s / kNumCUs;
+    const double eff = waves / std::ceil(waves);
+    if (eff >= 0.9) return s;
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
+      best = s;
+    }
+  }
+  return best;
+}
 
 static int pick_kw(int64_t kdim, int step, int cap) {
   const int64_t steps = kdim / step;
@@ -79,9 +109,11 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   p.tiled = tiled_ok && !(flags & FGS_FLAG_FORCE_DECODE) &&
             ((flags & FGS_FLAG_FORCE_PREFILL) || forced_cfg >= 0 ||
              rows_per_expert > 16);
+  p.ksplit2 = 1;
   if (p.tiled) {
     p.tile_cfg = forced_cfg >= 0 ? forced_cfg : tiled_config_for(rows_per_expert);
     p.block_m = tiled_block_m(p.tile_cfg);
+    p.ksplit2 = pick_ksplit(numel, e, p.block_m, hidden, inter);
   }
   const int step = stream_step_k(p.dt);
   p.kw1 = pick_kw(hidden, step, 4);
@@ -113,7 +145,7 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
     p.o_a2s = take(p.dt == kDtFp8 ? p.max_padded * (inter / 128) * 4
                                   : p.max_padded * 4);
   }
-  p.o_y = take(numel * hidden * 2);
+  p.o_y = take(p.ksplit2 > 1 ? p.ksplit2 * numel * hidden * 4 : numel * hidden * 2);
   p.total = o;
   *pl = p;
   return FGS_OK;
@@ -314,6 +346,7 @@ static int run_fused(const FusedArgs& a) {
   g2.kdim = a.inter;
   g2.n_out = a.hidden;
   g2.nrows_w = a.hidden;
+  g2.ksplit = p.ksplit2;
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, false, g2, static_cast<int>(p.n_launch),
                                    a.stream)
                : launch_gemm_stream(p.dt, false, g2, p.mt, p.kw2,
@@ -321,9 +354,14 @@ static int run_fused(const FusedArgs& a) {
   if (rc) return rc;
   g_prof.mark(5, a.stream);
 
-  rc = launch_moe_sum_routed(y, a.out, a.m, a.topk, a.hidden, a.topk_ids,
-                             a.e, on_input ? nullptr : a.topk_weights,
-                             a.stream);
+  if (p.ksplit2 > 1)
+    rc = launch_moe_sum_partials(reinterpret_cast<const float*>(y), p.ksplit2,
+                                 a.out, a.m, a.topk, a.hidden, a.topk_ids, a.e,
+                                 on_input ? nullptr : a.topk_weights, a.stream);
+  else
+    rc = launch_moe_sum_routed(y, a.out, a.m, a.topk, a.hidden, a.topk_ids,
+                               a.e, on_input ? nullptr : a.topk_weights,
+                               a.stream);
   g_prof.mark(6, a.stream);
   return rc;
 }

@@ -82,6 +82,40 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(
   }
 }
 
+// moe_sum over fp32 split-K partials: 4 columns per thread.
+__global__ __launch_bounds__(256) void moe_sum_partials_kernel(
+    const float* __restrict__ part, int nsplit, uint16_t* __restrict__ out,
+    int64_t m, int topk, int64_t k, const int32_t* __restrict__ ids,
+    int num_experts, const float* __restrict__ weights) {
+  const int64_t vec_per_row = k / 4;
+  const int64_t total = m * vec_per_row;
+  const int64_t split_stride = m * topk * k;
+  for (int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+       v < total; v += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t t = v / vec_per_row;
+    const int64_t c = (v - t * vec_per_row) * 4;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < topk; ++j) {
+      const int64_t slot = t * topk + j;
+      const int e = ids[slot];
+      if (e < 0 || e >= num_experts) continue;
+      f32x4 y = *reinterpret_cast<const f32x4*>(part + slot * k + c);
+      for (int s = 1; s < nsplit; ++s)
+        y += *reinterpret_cast<const f32x4*>(part + s * split_stride + slot * k + c);
+      const float w = weights ? weights[slot] : 1.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float yb = bf16_bits_to_f32(f32_to_bf16_bits(y[q]));
+        acc[q] = weights ? __fadd_rn(acc[q], __fmul_rn(w, yb)) : acc[q] + yb;
+      }
+    }
+    uint2 o;
+    o.x = pack_bf16x2(acc[0], acc[1]);
+    o.y = pack_bf16x2(acc[2], acc[3]);
+    *reinterpret_cast<uint2*>(out + t * k + c) = o;
+  }
+}
+
 // ------------------------------------------------------ fp8 group quant ---
 // One wave per (row, group of `group` columns); group % 8 == 0, group <= 512.
 // scale = max(amax, 1e-10) / 448; q = e4m3fn(clamp(x / scale, +-448)).
@@ -216,6 +250,18 @@ int launch_moe_sum_routed(const void* in, void* out, int64_t m, int topk,
                      static_cast<uint16_t*>(out), m, topk, k, ids, num_experts,
                      weights);
   return check_launch("moe_sum_kernel");
+}
+
+int launch_moe_sum_partials(const float* part, int nsplit, void* out, int64_t m,
+                            int topk, int64_t k, const int32_t* ids,
+                            int num_experts, const float* weights,
+                            hipStream_t stream) {
+  if (m == 0) return FGS_OK;
+  hipLaunchKernelGGL(moe_sum_partials_kernel, dim3(grid_for(m * (k / 4), 256)),
+                     dim3(256), 0, stream, part, nsplit,
+                     static_cast<uint16_t*>(out), m, topk, k, ids, num_experts,
+                     weights);
+  return check_launch("moe_sum_partials_kernel");
 }
 
 int launch_quant_fp8_group(const void* x, void* q, float* scales,

@@ -31,6 +31,7 @@ struct GemmParams {
   int32_t weight_on_input;
   int32_t row_blocks;     // row blocks of the launch (tiled kernels)
   int32_t group_n;        // column tiles per rasterization group (tiled)
+  int32_t ksplit;         // GEMM2 k splits; > 1: out is fp32 [ksplit][numel][n_out]
 };
 
 size_t align_smem_bytes(int num_experts);
@@ -45,6 +46,12 @@ int launch_moe_sum(const void* in, void* out, int64_t m, int topk, int64_t k,
 int launch_moe_sum_routed(const void* in, void* out, int64_t m, int topk,
                           int64_t k, const int32_t* ids, int num_experts,
                           const float* weights, hipStream_t stream);
+// Same reduction over fp32 split-K partials [nsplit][m*topk][k]: each slot's
+// y = bf16(sum_s part[s]) (splits in order), then the weighted top-k sum.
+int launch_moe_sum_partials(const float* part, int nsplit, void* out, int64_t m,
+                            int topk, int64_t k, const int32_t* ids,
+                            int num_experts, const float* weights,
+                            hipStream_t stream);
 int launch_quant_fp8_group(const void* x, void* q, float* scales, int64_t rows,
                            int64_t cols, int group, hipStream_t stream);
 int launch_quant_int8_token(const void* x, int8_t* q, float* scales,

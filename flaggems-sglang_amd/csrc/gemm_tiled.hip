@@ -13,11 +13,14 @@
 // followed by the matching up rows, so every lane holds the gate and up
 // accumulators of the same output element; the epilogue applies the
 // reference's rounding points and silu (ops/fused_moe.py:205-218).
-// GEMM2: y = a2 W2^T per padded row, stored (bf16) at its top-k slot.
+// GEMM2: y = a2 W2^T per padded row, stored (bf16) at its top-k slot, or,
+// split over k (ksplit > 1, to fill the chip when there are few tiles), as
+// fp32 partial sums per split that moe_sum adds in a fixed order.
 #include <stdlib.h>
 
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "fgs_moe_kernels.h"
 
@@ -56,6 +59,18 @@ __device__ __forceinline__ bool tile_of(int pid, int grid, int n_rb, int n_ct,
   *rb = idx / gsize;
   *ct = group * group_n + idx % gsize;
   return true;
+}
+
+// Calls f(std::integral_constant<int, n>) for a runtime n in [0, N].
+template <int N, class F>
+__device__ __forceinline__ void dispatch_count(int n, F&& f) {
+  if constexpr (N >= 0) {
+    if (n == N) {
+      f(std::integral_constant<int, N>{});
+      return;
+    }
+    dispatch_count<N - 1>(n, f);
+  }
 }
 
 template <int BM_, int BNR_, int WM_, int WN_, int SK_, int STAGES_>
@@ -108,10 +123,14 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
   constexpr int N_PER_TILE = GEMM1 ? BNR / 2 : BNR;
+  const int n_ct = static_cast<int>(p.n_out / N_PER_TILE);
   int rb_id, tile_n;
-  if (!tile_of(blockIdx.x, gridDim.x, p.row_blocks,
-               static_cast<int>(p.n_out / N_PER_TILE), p.group_n, &rb_id, &tile_n))
+  if (!tile_of(blockIdx.x, gridDim.x, p.row_blocks * p.ksplit, n_ct, p.group_n,
+               &rb_id, &tile_n))
     return;
+  // split-K (GEMM2 only): the row-block index space repeats once per split
+  const int ks = rb_id / p.row_blocks;
+  rb_id -= ks * p.row_blocks;
   if (rb_id * BM >= p.num_post_pad[0]) return;
   const int e = p.expert_ids[rb_id];
   if (e < 0) return;
@@ -130,8 +149,11 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
   for (int i = 0; i < NLA; ++i) {
     const int r = (wave * NLA + i) * C::LR + lrow;
     const int sid = p.sorted_ids[row0 + r];
-    // pad rows read token 0 / their own row: finite values, never stored
-    const int64_t src = GEMM1 ? (sid < p.numel ? sid / p.topk : 0) : row0 + r;
+    // Pad rows (always a suffix of the block: one expert per block) read a
+    // row every pad shares -- token 0, or the block's first row -- so they
+    // cost L1/L2 hits only; their results are never stored.
+    const bool ok = sid < p.numel;
+    const int64_t src = GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? r : 0);
     a_src[i] = p.a + src * p.kdim * 2 + chunk_pos<C>(r, lchunk) * 16;
   }
   const uint8_t* b_src[NLB];
@@ -183,7 +205,13 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
   const int a_base = wm * WROWS * SK;
   const int b_base = A_BYTES + wn * WCOLS * SK;
 
-  const int KT = static_cast<int>(p.kdim * 2 / SK);
+  const int KT_all = static_cast<int>(p.kdim * 2 / SK);
+  const int kt0 = ks * KT_all / p.ksplit;
+  const int KT = (ks + 1) * KT_all / p.ksplit - kt0;
+#pragma unroll
+  for (int i = 0; i < NLA; ++i) a_src[i] += static_cast<int64_t>(kt0) * SK;
+#pragma unroll
+  for (int i = 0; i < NLB; ++i) b_src[i] += static_cast<int64_t>(kt0) * SK;
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s)
     if (s < KT) issue(s, s);
@@ -211,48 +239,60 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
   // Weights are the MFMA's A operand and activations its B operand, so the
   // 32x32 accumulator is transposed: lane l holds token (l & 31) and four
   // runs of 4 consecutive output columns -> 8-byte stores in the epilogue.
-  auto mma = [&](const bf16x8 (&fa)[RB], const bf16x8 (&fb)[CB]) {
+  // 32-row blocks of this wave that hold at least one real row. Pad rows are
+  // a suffix of the block, so the live blocks are a prefix; the main loop is
+  // instantiated per live count so all-pad blocks (the tail of an expert's
+  // last block) skip their MFMAs without branches inside the MFMA stream.
+  int nlive = 0;
 #pragma unroll
-    for (int i = 0; i < RB; ++i)
-#pragma unroll
-      for (int j = 0; j < CB; ++j) acc[i][j] = mfma32_bf16(fb[j], fa[i], acc[i][j]);
-  };
+  for (int i = 0; i < RB; ++i)
+    nlive += p.sorted_ids[row0 + wm * WROWS + i * 32] < p.numel ? 1 : 0;
 
-  // Software pipeline over half-stage fragment sets: the fragments of the
-  // next k step are read from LDS while the MFMAs of the current one run;
-  // the barrier that publishes stage kt+1 (and frees slot kt-1 for the next
-  // DMA) sits before the last k step of stage kt. The last stage is peeled
-  // so the loop body has no branch around LDS reads.
   bf16x8 fa[2][RB], fb[2][CB];
-  wait_stages(min(STAGES - 2, KT - 1));
-  wave_barrier_all();
-  read_frags(0, 0, fa[0], fb[0]);
-  for (int kt = 0; kt + 1 < KT; ++kt) {
+  auto main_loop = [&](auto nlive_c) {
+    constexpr int NLIVE = decltype(nlive_c)::value;
+    auto mma = [&](const bf16x8 (&a)[RB], const bf16x8 (&b)[CB]) {
+#pragma unroll
+      for (int i = 0; i < NLIVE; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j) acc[i][j] = mfma32_bf16(b[j], a[i], acc[i][j]);
+    };
+    // Software pipeline over half-stage fragment sets: the fragments of the
+    // next k step are read from LDS while the MFMAs of the current one run;
+    // the barrier that publishes stage kt+1 (and frees slot kt-1 for the
+    // next DMA) sits before the last k step of stage kt. The last stage is
+    // peeled so the loop body has no branch around LDS reads.
+    wait_stages(min(STAGES - 2, KT - 1));
+    wave_barrier_all();
+    read_frags(0, 0, fa[0], fb[0]);
+    for (int kt = 0; kt + 1 < KT; ++kt) {
+#pragma unroll
+      for (int kk = 0; kk + 1 < KK; ++kk) {
+        read_frags(kt, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+        mma(fa[kk & 1], fb[kk & 1]);
+      }
+      wait_stages(min(STAGES - 3, KT - 2 - kt));
+      wave_barrier_all();
+      if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+      read_frags(kt + 1, 0, fa[KK & 1], fb[KK & 1]);
+      mma(fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
+      if constexpr (KK & 1) {
+        // odd KK: the next stage's first fragments landed in set 1; move
+        // them to set 0 where the next iteration expects them
+#pragma unroll
+        for (int i = 0; i < RB; ++i) fa[0][i] = fa[1][i];
+#pragma unroll
+        for (int j = 0; j < CB; ++j) fb[0][j] = fb[1][j];
+      }
+    }
 #pragma unroll
     for (int kk = 0; kk + 1 < KK; ++kk) {
-      read_frags(kt, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+      read_frags(KT - 1, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
       mma(fa[kk & 1], fb[kk & 1]);
     }
-    wait_stages(min(STAGES - 3, KT - 2 - kt));
-    wave_barrier_all();
-    if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-    read_frags(kt + 1, 0, fa[KK & 1], fb[KK & 1]);
     mma(fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
-    if constexpr (KK & 1) {
-      // odd KK: the next stage's first fragments landed in set 1; move them
-      // to set 0 where the next iteration expects them
-#pragma unroll
-      for (int i = 0; i < RB; ++i) fa[0][i] = fa[1][i];
-#pragma unroll
-      for (int j = 0; j < CB; ++j) fb[0][j] = fb[1][j];
-    }
-  }
-#pragma unroll
-  for (int kk = 0; kk + 1 < KK; ++kk) {
-    read_frags(KT - 1, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-    mma(fa[kk & 1], fb[kk & 1]);
-  }
-  mma(fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
+  };
+  dispatch_count<RB>(nlive, main_loop);
 
   // ---- epilogue: lane owns token row (lane & 31) of each 32-row block and,
   // in each 32-column block, columns 8*q + 4*(lane>>5) + {0..3}, q = 0..3
@@ -265,6 +305,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
     const int sid = p.sorted_ids[r];
     const bool valid = sid < p.numel;
     if constexpr (GEMM1) {
+      if (!valid) continue;  // pad rows: never read by GEMM2's real rows
       const bool scale = p.weight_on_input && valid;
       const float gamma = scale ? p.topk_w[sid] : 0.f;
       uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
@@ -287,19 +328,30 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
           *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
         }
       }
-    } else {
-      if (valid) {
-        uint16_t* orow = out + static_cast<int64_t>(sid) * p.n_out;
+    } else if (valid && p.ksplit > 1) {
+      // fp32 partial sums of split ks, reduced in fixed order by moe_sum
+      float* orow = static_cast<float*>(p.out) +
+                    (static_cast<int64_t>(ks) * p.numel + sid) * p.n_out;
 #pragma unroll
-        for (int j = 0; j < CB; ++j) {
-          const int col0 = tile_n * BNR + wn * WCOLS + j * 32 + csub;
+      for (int j = 0; j < CB; ++j) {
+        const int col0 = tile_n * BNR + wn * WCOLS + j * 32 + csub;
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            uint2 v2;
-            v2.x = pack_bf16x2(acc[i][j][4 * g4], acc[i][j][4 * g4 + 1]);
-            v2.y = pack_bf16x2(acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3]);
-            *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
-          }
+        for (int g4 = 0; g4 < 4; ++g4)
+          *reinterpret_cast<f32x4*>(orow + col0 + 8 * g4) =
+              f32x4{acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2],
+                    acc[i][j][4 * g4 + 3]};
+      }
+    } else if (valid) {
+      uint16_t* orow = out + static_cast<int64_t>(sid) * p.n_out;
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        const int col0 = tile_n * BNR + wn * WCOLS + j * 32 + csub;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          uint2 v2;
+          v2.x = pack_bf16x2(acc[i][j][4 * g4], acc[i][j][4 * g4 + 1]);
+          v2.y = pack_bf16x2(acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3]);
+          *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
         }
       }
     }
@@ -334,7 +386,8 @@ static int launch_tiled(const GemmParams& p, int row_blocks, hipStream_t stream)
   GemmParams q = p;
   q.row_blocks = row_blocks;
   q.group_n = group_n_choice();
-  const int tiles = (row_blocks * tiles_n + 7) / 8 * 8;
+  if (GEMM1 || q.ksplit < 1) q.ksplit = 1;
+  const int tiles = (row_blocks * q.ksplit * tiles_n + 7) / 8 * 8;
   hipLaunchKernelGGL(kern, dim3(tiles), dim3(C::NW * 64), C::LDS_BYTES, stream, q);
   return check_launch("moe_gemm_tiled_bf16_kernel");
 }

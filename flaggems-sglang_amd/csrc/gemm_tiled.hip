@@ -363,8 +363,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
 static int group_n_choice() {
   static const int g = [] {
     const char* s = getenv("FGS_MOE_GROUPN");
-    const int v = s ? atoi(s) : 2;
-    return (v >= 1 && v <= 64) ? v : 2;
+    const int v = s ? atoi(s) : 4;
+    return (v >= 1 && v <= 64) ? v : 4;
   }();
   return g;
 }

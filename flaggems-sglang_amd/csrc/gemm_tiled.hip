@@ -42,6 +42,11 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
 
 __device__ __forceinline__ void wave_barrier_all() { __builtin_amdgcn_s_barrier(); }
 
+// s_waitcnt lgkmcnt(0): this wave's LDS reads have completed.
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt((63 & 15) | (7 << 4) | (0 << 8) | ((63 >> 4) << 14));
+}
+
 // Tile order. The grid is 1-D and padded to a multiple of the 8 XCDs.
 // Workgroup `pid` runs on XCD pid % 8, so logical tile
 // (pid % 8) * (grid / 8) + pid / 8 gives every XCD a contiguous range of
@@ -116,7 +121,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
   constexpr int KK = SK / 32;              // 16-element k steps per stage
   static_assert(NLA * C::LR * NW == BM, "A tile / waves");
   static_assert(NLB * C::LR * NW == BNR, "B tile / waves");
-  static_assert(STAGES >= 3 && (STAGES - 2) * NL < 64, "stages");
+  static_assert(STAGES >= 2 && (STAGES - 1) * NL < 64, "stages");
   static_assert(RB >= 1 && CB >= 1, "wave tile");
   static_assert(!GEMM1 || CB % 2 == 0, "gate/up pairing");
 
@@ -213,12 +218,13 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
 #pragma unroll
   for (int i = 0; i < NLB; ++i) b_src[i] += static_cast<int64_t>(kt0) * SK;
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
+  for (int s = 0; s < STAGES; ++s)
     if (s < KT) issue(s, s);
 
   // Waits until at most `n` of this wave's later stages are in flight.
   auto wait_stages = [&](int n) {
-    if (n >= 5) wait_vmcnt<(5 * NL < 64 ? 5 * NL : 0)>();
+    if (n >= 6) wait_vmcnt<(6 * NL < 64 ? 6 * NL : 0)>();
+    else if (n == 5) wait_vmcnt<(5 * NL < 64 ? 5 * NL : 0)>();
     else if (n == 4) wait_vmcnt<(4 * NL < 64 ? 4 * NL : 0)>();
     else if (n == 3) wait_vmcnt<(3 * NL < 64 ? 3 * NL : 0)>();
     else if (n == 2) wait_vmcnt<2 * NL>();
@@ -257,12 +263,15 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
 #pragma unroll
         for (int j = 0; j < CB; ++j) acc[i][j] = mfma32_bf16(b[j], a[i], acc[i][j]);
     };
-    // Software pipeline over half-stage fragment sets: the fragments of the
-    // next k step are read from LDS while the MFMAs of the current one run;
-    // the barrier that publishes stage kt+1 (and frees slot kt-1 for the
-    // next DMA) sits before the last k step of stage kt. The last stage is
-    // peeled so the loop body has no branch around LDS reads.
-    wait_stages(min(STAGES - 2, KT - 1));
+    // Software pipeline over k-step fragment sets: the fragments of the
+    // next k step are read from LDS while the MFMAs of the current one run.
+    // The barrier sits before the last k step of stage kt, once this wave's
+    // reads of stage kt have all completed (its last fragments are in
+    // registers): it publishes stage kt+1 and frees stage kt's slot, which
+    // the DMA of stage kt+STAGES then refills, STAGES-1 stages ahead of its
+    // use. The last stage is peeled so the loop body has no branch around
+    // LDS reads.
+    wait_stages(min(STAGES - 1, KT - 1));
     wave_barrier_all();
     read_frags(0, 0, fa[0], fb[0]);
     for (int kt = 0; kt + 1 < KT; ++kt) {
@@ -271,9 +280,10 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
         read_frags(kt, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
         mma(fa[kk & 1], fb[kk & 1]);
       }
-      wait_stages(min(STAGES - 3, KT - 2 - kt));
+      wait_lgkm0();
+      wait_stages(min(STAGES - 2, KT - 2 - kt));
       wave_barrier_all();
-      if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+      if (kt + STAGES < KT) issue(kt + STAGES, kt % STAGES);
       read_frags(kt + 1, 0, fa[KK & 1], fb[KK & 1]);
       mma(fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
       if constexpr (KK & 1) {
@@ -395,8 +405,8 @@ static int launch_tiled(const GemmParams& p, int row_blocks, hipStream_t stream)
 // Tile configurations (BM, BNR, WM, WN, SK, STAGES), one per rows-per-expert
 // regime. Small row blocks keep padding low and still read every weight
 // tile once per block; the 256-row tile has the highest MFMA intensity.
-using Cfg256 = TileCfg<256, 256, 4, 2, 64, 4>;  // 8 waves of 64x128
-using Cfg128 = TileCfg<128, 256, 2, 4, 64, 6>;  // 8 waves of 64x64
+using Cfg256 = TileCfg<256, 256, 4, 2, 128, 2>;  // 8 waves of 64x128
+using Cfg128 = TileCfg<128, 256, 2, 4, 128, 3>;  // 8 waves of 64x64
 using Cfg64 = TileCfg<64, 256, 1, 4, 128, 4>;   // 4 waves of 64x64
 using Cfg32 = TileCfg<32, 256, 1, 4, 128, 4>;   // 4 waves of 32x64
 

@@ -103,7 +103,7 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   p.block_m = 16 * p.mt;
   // Prefill schedule: enough rows per expert that a 256-row block is mostly
   // real rows, and shapes the tiled kernels cover.
-  const bool tiled_ok = p.dt == kDtBf16 && inter % tiled_n_align(true) == 0 &&
+  const bool tiled_ok = inter % tiled_n_align(true) == 0 &&
                         hidden % tiled_n_align(false) == 0;
   const int forced_cfg = ((flags & FGS_FLAG_TILE_MASK) >> 12) - 1;
   p.tiled = tiled_ok && !(flags & FGS_FLAG_FORCE_DECODE) &&
@@ -111,7 +111,7 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
              rows_per_expert > 16);
   p.ksplit2 = 1;
   if (p.tiled) {
-    p.tile_cfg = forced_cfg >= 0 ? forced_cfg : tiled_config_for(rows_per_expert);
+    p.tile_cfg = forced_cfg >= 0 ? forced_cfg : tiled_config_for(p.dt, rows_per_expert);
     p.block_m = tiled_block_m(p.tile_cfg);
     p.ksplit2 = pick_ksplit(numel, e, p.block_m, hidden, inter);
   }
@@ -174,6 +174,11 @@ static int validate(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
     return fail(FGS_EUNSUPPORTED, "m * topk too large for int32 slot ids");
   const int dt = qmode == FGS_QMODE_FP8_BLOCK ? kDtFp8
                  : qmode == FGS_QMODE_INT8_CHANNEL ? kDtInt8 : kDtBf16;
+  const int forced_cfg = ((flags & FGS_FLAG_TILE_MASK) >> 12) - 1;
+  if (forced_cfg >= 0 && !tiled_config_supported(dt, forced_cfg))
+    return fail(FGS_EUNSUPPORTED, "FGS_FLAG_TILE configuration " +
+                                      std::to_string(forced_cfg) +
+                                      " is not available for this qmode");
   const int step = stream_step_k(dt);
   if (hidden % step != 0 || inter % step != 0)
     return fail(FGS_EUNSUPPORTED, "hidden and inter must be multiples of " +

@@ -63,10 +63,11 @@ int stream_step_k(int dt);
 int launch_gemm_stream(int dt, bool gemm1, const GemmParams& p, int mt, int kw,
                        int row_blocks, hipStream_t stream);
 
-// LDS-tiled MFMA kernels (bf16): configuration per rows-per-expert regime,
-// its row block, n_out granularity, launch.
+// LDS-tiled MFMA kernels (bf16, fp8, int8): configuration per element type
+// and rows-per-expert regime, its row block, n_out granularity, launch.
 constexpr int kTiledConfigs = 4;
-int tiled_config_for(double rows_per_expert);
+int tiled_config_supported(int dt, int cfg);
+int tiled_config_for(int dt, double rows_per_expert);
 int tiled_block_m(int cfg);
 int tiled_n_align(bool gemm1);
 int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,

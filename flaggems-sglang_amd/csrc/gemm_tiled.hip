@@ -103,27 +103,94 @@ __device__ __forceinline__ int chunk_pos(int r, int c) {
   return c ^ ((r / C::RPL) % C::CPR);
 }
 
-template <class C, bool GEMM1>
-__global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
+// Element types of the tiled kernels. A 32x32 MFMA k step reads 16 bytes
+// per lane of each operand (bf16: 8 elements, int8: 16) -- one LDS chunk --
+// except fp8, whose 32x32x64 MFMA reads 32 bytes per lane (two chunks).
+template <int DT>
+struct TiledType;
+template <>
+struct TiledType<kDtBf16> {
+  static constexpr int ESZ = 2, FC = 1;
+  using Frag = bf16x8;
+  using Acc = f32x16;
+  static __device__ __forceinline__ Acc mma(Frag w, Frag x, Acc c) {
+    return mfma32_bf16(w, x, c);
+  }
+};
+template <>
+struct TiledType<kDtInt8> {
+  static constexpr int ESZ = 1, FC = 1;
+  using Frag = i32x4;
+  using Acc = i32x16;
+  // v_mfma_i32_32x32x32_i8: same lane layout as the bf16 32x32x16 form
+  // with 16 int8 of k per lane.
+  static __device__ __forceinline__ Acc mma(Frag w, Frag x, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(w, x, c, 0, 0, 0);
+  }
+};
+template <>
+struct TiledType<kDtFp8> {
+  static constexpr int ESZ = 1, FC = 2;
+  using Frag = i32x8;
+  using Acc = f32x16;
+  // v_mfma_scale_f32_32x32x64_f8f6f4, both operands OCP e4m3 (format 0),
+  // unit e8m0 block scales (127): 32 fp8 of k per lane.
+  static __device__ __forceinline__ Acc mma(Frag w, Frag x, Acc c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, x, c, 0, 0, 0, 127,
+                                                           0, 127);
+  }
+};
+
+// Bytes of the per-stage scale area (fp8 only): one float slot per lane of
+// the workgroup, filled by one 4-byte LDS-DMA load per wave per stage.
+template <int DT, class C>
+constexpr int tiled_scale_bytes() {
+  return DT == kDtFp8 ? C::NW * 256 : 0;
+}
+template <int DT, class C>
+constexpr int tiled_lds_bytes() {
+  return C::STAGES * ((C::BM + C::BNR) * C::SK + tiled_scale_bytes<DT, C>());
+}
+
+// 4-byte LDS-DMA load: lane l copies 4 bytes from `src` to byte 4*l of the
+// 256-byte block at `lds_dst`.
+__device__ __forceinline__ void lds_dma4(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(
+      src, (__attribute__((address_space(3))) void*)(lds_dst), 4, 0, 0);
+}
+
+template <int DT, class C, bool GEMM1>
+__global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
     const GemmParams p) {
+  using T = TiledType<DT>;
+  using Frag = typename T::Frag;
+  using Acc = typename T::Acc;
+  constexpr bool FP8 = DT == kDtFp8;
+  constexpr bool INT8 = DT == kDtInt8;
+  constexpr int ESZ = T::ESZ, FC = T::FC;
   constexpr int BM = C::BM, BNR = C::BNR, SK = C::SK, STAGES = C::STAGES;
   constexpr int NW = C::NW, WN = C::WN;
   constexpr int A_BYTES = BM * SK;
   constexpr int B_BYTES = BNR * SK;
-  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int SC_OFF = A_BYTES + B_BYTES;
+  constexpr int STAGE = SC_OFF + tiled_scale_bytes<DT, C>();
   constexpr int NLA = BM / (C::LR * NW);   // A loads per wave per stage
   constexpr int NLB = BNR / (C::LR * NW);  // B loads per wave per stage
-  constexpr int NL = NLA + NLB;
+  constexpr int NL = NLA + NLB + (FP8 ? 1 : 0);
   constexpr int WROWS = BM / C::WM;        // rows per wave
   constexpr int WCOLS = BNR / WN;          // weight rows per wave
   constexpr int RB = WROWS / 32;           // 32-row MFMA blocks
   constexpr int CB = WCOLS / 32;           // 32-col MFMA blocks
-  constexpr int KK = SK / 32;              // 16-element k steps per stage
+  constexpr int KK = SK / (32 * FC);       // MFMA k steps per stage
   static_assert(NLA * C::LR * NW == BM, "A tile / waves");
   static_assert(NLB * C::LR * NW == BNR, "B tile / waves");
   static_assert(STAGES >= 2 && (STAGES - 1) * NL < 64, "stages");
-  static_assert(RB >= 1 && CB >= 1, "wave tile");
+  static_assert(RB >= 1 && CB >= 1 && KK >= 1, "wave tile");
   static_assert(!GEMM1 || CB % 2 == 0, "gate/up pairing");
+  static_assert(tiled_lds_bytes<DT, C>() <= 160 * 1024, "gfx950 LDS is 160 KiB");
+  // fp8: one stage is one 128-wide k block of the block scales, and a tile's
+  // weight rows span whole 128-row scale blocks
+  static_assert(!FP8 || (SK == 128 && BNR % 256 == 0 && BM + 4 <= NW * 64), "fp8 tile");
 
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
@@ -145,6 +212,17 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
   const int wm = wave / WN;
   const int wn = wave % WN;
   const int row0 = rb_id * BM;
+  const int64_t row_bytes = p.kdim * ESZ;
+
+  // Activation row feeding padded row r of the block. Pad rows (always a
+  // suffix of the block: one expert per block) read a row every pad shares
+  // -- token 0, or the block's first row -- so they cost L1/L2 hits only;
+  // their results are never stored.
+  auto act_row = [&](int r) -> int64_t {
+    const int sid = p.sorted_ids[row0 + r];
+    const bool ok = sid < p.numel;
+    return GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? r : 0);
+  };
 
   // ---- this lane's source of each LDS-DMA load: row lane/CPR, chunk lane%CPR
   const int lrow = lane / C::CPR;
@@ -153,13 +231,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
 #pragma unroll
   for (int i = 0; i < NLA; ++i) {
     const int r = (wave * NLA + i) * C::LR + lrow;
-    const int sid = p.sorted_ids[row0 + r];
-    // Pad rows (always a suffix of the block: one expert per block) read a
-    // row every pad shares -- token 0, or the block's first row -- so they
-    // cost L1/L2 hits only; their results are never stored.
-    const bool ok = sid < p.numel;
-    const int64_t src = GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? r : 0);
-    a_src[i] = p.a + src * p.kdim * 2 + chunk_pos<C>(r, lchunk) * 16;
+    a_src[i] = p.a + act_row(r) * row_bytes + chunk_pos<C>(r, lchunk) * 16;
   }
   const uint8_t* b_src[NLB];
   const int64_t wbase = static_cast<int64_t>(e) * p.nrows_w;
@@ -178,7 +250,28 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
     } else {
       wrow = static_cast<int64_t>(tile_n) * BNR + j;
     }
-    b_src[i] = p.w + (wbase + wrow) * p.kdim * 2 + chunk_pos<C>(j, lchunk) * 16;
+    b_src[i] = p.w + (wbase + wrow) * row_bytes + chunk_pos<C>(j, lchunk) * 16;
+  }
+
+  // fp8 block scales of one k block, staged with the tiles: slot s < BM is
+  // padded row s's activation scale, slot BM + b the tile's b-th 128-row
+  // weight scale block (GEMM1: b = 0 gate, 1 up); other slots are unused.
+  const int kblocks = static_cast<int>(p.kdim / 128);
+  const float* sc_src = nullptr;
+  if constexpr (FP8) {
+    const int slot = wave * 64 + lane;
+    const int64_t wblk0 = static_cast<int64_t>(e) * (p.nrows_w / 128);
+    if (slot < BM) {
+      sc_src = p.a_scale + act_row(slot) * kblocks;
+    } else {
+      int64_t wb = 0;
+      if (slot < BM + (GEMM1 ? 2 : BNR / 128)) {
+        const int b = slot - BM;
+        wb = GEMM1 ? (b ? p.n_out / 128 : 0) + tile_n * (BNR / 2) / 128
+                   : static_cast<int64_t>(tile_n) * (BNR / 128) + b;
+      }
+      sc_src = p.w_scale + (wblk0 + wb) * kblocks;
+    }
   }
 
   auto issue = [&](int kt, int slot) {
@@ -190,33 +283,37 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
 #pragma unroll
     for (int i = 0; i < NLB; ++i)
       lds_dma16(b_src[i] + koff, base + A_BYTES + (wave * NLB + i) * 1024);
+    if constexpr (FP8) lds_dma4(sc_src + kt, base + SC_OFF + wave * 256);
   };
 
-  f32x16 acc[RB][CB];
+  Acc acc[RB][CB];
 #pragma unroll
   for (int i = 0; i < RB; ++i)
 #pragma unroll
     for (int j = 0; j < CB; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
   // Fragment reads: lane reads row (lane & 31) of a 32-row block, logical
-  // chunk 2*kk + (lane >> 5) (16 bf16 of k per kk step).
+  // chunks FC*(2*kk + (lane >> 5)) + c, c < FC.
   const int fr = lane & 31;
-  int frag_off[KK];
+  int frag_off[KK][FC];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
-    frag_off[kk] = fr * SK + chunk_pos<C>(fr, 2 * kk + (lane >> 5)) * 16;
+#pragma unroll
+    for (int c = 0; c < FC; ++c)
+      frag_off[kk][c] = fr * SK + chunk_pos<C>(fr, FC * (2 * kk + (lane >> 5)) + c) * 16;
   const int a_base = wm * WROWS * SK;
   const int b_base = A_BYTES + wn * WCOLS * SK;
 
-  const int KT_all = static_cast<int>(p.kdim * 2 / SK);
+  const int KT_all = static_cast<int>(row_bytes / SK);
   const int kt0 = ks * KT_all / p.ksplit;
   const int KT = (ks + 1) * KT_all / p.ksplit - kt0;
 #pragma unroll
   for (int i = 0; i < NLA; ++i) a_src[i] += static_cast<int64_t>(kt0) * SK;
 #pragma unroll
   for (int i = 0; i < NLB; ++i) b_src[i] += static_cast<int64_t>(kt0) * SK;
+  if constexpr (FP8) sc_src += kt0;
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < KT) issue(s, s);
@@ -231,16 +328,33 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
     else if (n == 1) wait_vmcnt<NL>();
     else wait_vmcnt<0>();
   };
-  auto read_frags = [&](int kt, int kk, bf16x8 (&fa)[RB], bf16x8 (&fb)[CB]) {
+  auto load_frag = [&](const uint8_t* p0, int kk) -> Frag {
+    if constexpr (FC == 1) {
+      return *reinterpret_cast<const Frag*>(p0 + frag_off[kk][0]);
+    } else {
+      const i32x4 lo = *reinterpret_cast<const i32x4*>(p0 + frag_off[kk][0]);
+      const i32x4 hi = *reinterpret_cast<const i32x4*>(p0 + frag_off[kk][FC - 1]);
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+  auto read_frags = [&](int kt, int kk, Frag (&fa)[RB], Frag (&fb)[CB]) {
     const uint8_t* st = lds + (kt % STAGES) * STAGE;
 #pragma unroll
-    for (int i = 0; i < RB; ++i)
-      fa[i] = *reinterpret_cast<const bf16x8*>(st + a_base + i * 32 * SK +
-                                               frag_off[kk]);
+    for (int i = 0; i < RB; ++i) fa[i] = load_frag(st + a_base + i * 32 * SK, kk);
 #pragma unroll
-    for (int j = 0; j < CB; ++j)
-      fb[j] = *reinterpret_cast<const bf16x8*>(st + b_base + j * 32 * SK +
-                                               frag_off[kk]);
+    for (int j = 0; j < CB; ++j) fb[j] = load_frag(st + b_base + j * 32 * SK, kk);
+  };
+  // fp8: this lane's activation scale per 32-row block and the wave's weight
+  // scale per 32-col block, for stage kt.
+  auto read_scales = [&](int kt, float (&sa)[RB], float (&sw)[CB]) {
+    const float* sc = reinterpret_cast<const float*>(lds + (kt % STAGES) * STAGE + SC_OFF);
+#pragma unroll
+    for (int i = 0; i < RB; ++i) sa[i] = sc[wm * WROWS + i * 32 + fr];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const int b = GEMM1 ? (j >= CB / 2 ? 1 : 0) : (wn * WCOLS + j * 32) / 128;
+      sw[j] = sc[BM + b];
+    }
   };
   // Weights are the MFMA's A operand and activations its B operand, so the
   // 32x32 accumulator is transposed: lane l holds token (l & 31) and four
@@ -254,14 +368,37 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
   for (int i = 0; i < RB; ++i)
     nlive += p.sorted_ids[row0 + wm * WROWS + i * 32] < p.numel ? 1 : 0;
 
-  bf16x8 fa[2][RB], fb[2][CB];
+  Frag fa[2][RB], fb[2][CB];
   auto main_loop = [&](auto nlive_c) {
     constexpr int NLIVE = decltype(nlive_c)::value;
-    auto mma = [&](const bf16x8 (&a)[RB], const bf16x8 (&b)[CB]) {
+    // fp8: each stage (one k block) accumulates into tmp, which is then
+    // added to acc times the block's activation x weight scale.
+    Acc tmp[FP8 ? RB : 1][FP8 ? CB : 1];
+    float sa_c[RB], sw_c[CB], sa_n[RB], sw_n[CB];
+    auto mma = [&](int kk, const Frag (&a)[RB], const Frag (&b)[CB]) {
 #pragma unroll
       for (int i = 0; i < NLIVE; ++i)
 #pragma unroll
-        for (int j = 0; j < CB; ++j) acc[i][j] = mfma32_bf16(b[j], a[i], acc[i][j]);
+        for (int j = 0; j < CB; ++j) {
+          if constexpr (FP8) {
+            const Acc zero = {};
+            tmp[i][j] = T::mma(b[j], a[i], kk == 0 ? zero : tmp[i][j]);
+          } else {
+            acc[i][j] = T::mma(b[j], a[i], acc[i][j]);
+          }
+        }
+    };
+    auto fold = [&]() {
+      if constexpr (FP8) {
+#pragma unroll
+        for (int i = 0; i < NLIVE; ++i)
+#pragma unroll
+          for (int j = 0; j < CB; ++j) {
+            const float s = sa_c[i] * sw_c[j];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] += tmp[i][j][v] * s;
+          }
+      }
     };
     // Software pipeline over k-step fragment sets: the fragments of the
     // next k step are read from LDS while the MFMAs of the current one run.
@@ -274,18 +411,27 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
     wait_stages(min(STAGES - 1, KT - 1));
     wave_barrier_all();
     read_frags(0, 0, fa[0], fb[0]);
+    if constexpr (FP8) read_scales(0, sa_c, sw_c);
     for (int kt = 0; kt + 1 < KT; ++kt) {
 #pragma unroll
       for (int kk = 0; kk + 1 < KK; ++kk) {
         read_frags(kt, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-        mma(fa[kk & 1], fb[kk & 1]);
+        mma(kk, fa[kk & 1], fb[kk & 1]);
       }
       wait_lgkm0();
       wait_stages(min(STAGES - 2, KT - 2 - kt));
       wave_barrier_all();
       if (kt + STAGES < KT) issue(kt + STAGES, kt % STAGES);
       read_frags(kt + 1, 0, fa[KK & 1], fb[KK & 1]);
-      mma(fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
+      if constexpr (FP8) read_scales(kt + 1, sa_n, sw_n);
+      mma(KK - 1, fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
+      if constexpr (FP8) {
+        fold();
+#pragma unroll
+        for (int i = 0; i < RB; ++i) sa_c[i] = sa_n[i];
+#pragma unroll
+        for (int j = 0; j < CB; ++j) sw_c[j] = sw_n[j];
+      }
       if constexpr (KK & 1) {
         // odd KK: the next stage's first fragments landed in set 1; move
         // them to set 0 where the next iteration expects them
@@ -298,25 +444,38 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
 #pragma unroll
     for (int kk = 0; kk + 1 < KK; ++kk) {
       read_frags(KT - 1, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-      mma(fa[kk & 1], fb[kk & 1]);
+      mma(kk, fa[kk & 1], fb[kk & 1]);
     }
-    mma(fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
+    mma(KK - 1, fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
+    fold();
   };
   dispatch_count<RB>(nlive, main_loop);
 
   // ---- epilogue: lane owns token row (lane & 31) of each 32-row block and,
   // in each 32-column block, columns 8*q + 4*(lane>>5) + {0..3}, q = 0..3
-  // (accumulator registers 4q..4q+3).
+  // (accumulator registers 4q..4q+3). int8 dequantises here:
+  // float(acc) * a_scale[row] * w_scale[channel].
   uint16_t* out = static_cast<uint16_t*>(p.out);
   const int csub = 4 * (lane >> 5);
+  const float* wsc = INT8 ? p.w_scale + wbase : nullptr;
+  auto wscale4 = [&](int64_t wrow) -> f32x4 {
+    if constexpr (INT8) return *reinterpret_cast<const f32x4*>(wsc + wrow);
+    else return f32x4{1.f, 1.f, 1.f, 1.f};
+  };
+  auto value = [&](const Acc& a, int v, float sa, float sw) -> float {
+    if constexpr (INT8) return static_cast<float>(a[v]) * sa * sw;
+    else return a[v];
+  };
 #pragma unroll
   for (int i = 0; i < RB; ++i) {
-    const int r = row0 + wm * WROWS + i * 32 + (lane & 31);
+    const int rr = wm * WROWS + i * 32 + (lane & 31);
+    const int r = row0 + rr;
     const int sid = p.sorted_ids[r];
     const bool valid = sid < p.numel;
+    if (!valid) continue;  // pad rows: never stored
+    const float sa = INT8 ? p.a_scale[act_row(rr)] : 1.f;
     if constexpr (GEMM1) {
-      if (!valid) continue;  // pad rows: never read by GEMM2's real rows
-      const bool scale = p.weight_on_input && valid;
+      const bool scale = p.weight_on_input != 0;
       const float gamma = scale ? p.topk_w[sid] : 0.f;
       uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
 #pragma unroll
@@ -324,11 +483,14 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
         const int col0 = tile_n * (BNR / 2) + wn * (WCOLS / 2) + jb * 32 + csub;
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
+          const f32x4 swg = wscale4(col0 + 8 * g4);
+          const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
           uint32_t w0 = 0, w1 = 0;
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const uint32_t b = gemm1_epilogue(acc[i][jb][4 * g4 + t],
-                                              acc[i][jb + CB / 2][4 * g4 + t], scale, gamma);
+            const uint32_t b = gemm1_epilogue(value(acc[i][jb], 4 * g4 + t, sa, swg[t]),
+                                              value(acc[i][jb + CB / 2], 4 * g4 + t, sa, swu[t]),
+                                              scale, gamma);
             if (t < 2) w0 |= b << (16 * t);
             else w1 |= b << (16 * (t - 2));
           }
@@ -338,7 +500,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
           *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
         }
       }
-    } else if (valid && p.ksplit > 1) {
+    } else if (p.ksplit > 1) {
       // fp32 partial sums of split ks, reduced in fixed order by moe_sum
       float* orow = static_cast<float*>(p.out) +
                     (static_cast<int64_t>(ks) * p.numel + sid) * p.n_out;
@@ -346,21 +508,27 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_bf16_kernel(
       for (int j = 0; j < CB; ++j) {
         const int col0 = tile_n * BNR + wn * WCOLS + j * 32 + csub;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4)
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const f32x4 sw = wscale4(col0 + 8 * g4);
+          const int v = 4 * g4;
           *reinterpret_cast<f32x4*>(orow + col0 + 8 * g4) =
-              f32x4{acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2],
-                    acc[i][j][4 * g4 + 3]};
+              f32x4{value(acc[i][j], v, sa, sw[0]), value(acc[i][j], v + 1, sa, sw[1]),
+                    value(acc[i][j], v + 2, sa, sw[2]), value(acc[i][j], v + 3, sa, sw[3])};
+        }
       }
-    } else if (valid) {
+    } else {
       uint16_t* orow = out + static_cast<int64_t>(sid) * p.n_out;
 #pragma unroll
       for (int j = 0; j < CB; ++j) {
         const int col0 = tile_n * BNR + wn * WCOLS + j * 32 + csub;
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
+          const f32x4 sw = wscale4(col0 + 8 * g4);
+          const int v = 4 * g4;
           uint2 v2;
-          v2.x = pack_bf16x2(acc[i][j][4 * g4], acc[i][j][4 * g4 + 1]);
-          v2.y = pack_bf16x2(acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3]);
+          v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]), value(acc[i][j], v + 1, sa, sw[1]));
+          v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]),
+                             value(acc[i][j], v + 3, sa, sw[3]));
           *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
         }
       }
@@ -379,15 +547,15 @@ static int group_n_choice() {
   return g;
 }
 
-template <class C, bool GEMM1>
+template <int DT, class C, bool GEMM1>
 static int launch_tiled(const GemmParams& p, int row_blocks, hipStream_t stream) {
-  auto kern = moe_gemm_tiled_bf16_kernel<C, GEMM1>;
+  auto kern = moe_gemm_tiled_kernel<DT, C, GEMM1>;
+  constexpr int lds_bytes = tiled_lds_bytes<DT, C>();
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&] {
     attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                               C::LDS_BYTES);
+                               hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
   });
   if (attr != hipSuccess)
     return fail(FGS_ELAUNCH, std::string("tiled GEMM LDS opt-in: ") +
@@ -398,8 +566,8 @@ static int launch_tiled(const GemmParams& p, int row_blocks, hipStream_t stream)
   q.group_n = group_n_choice();
   if (GEMM1 || q.ksplit < 1) q.ksplit = 1;
   const int tiles = (row_blocks * q.ksplit * tiles_n + 7) / 8 * 8;
-  hipLaunchKernelGGL(kern, dim3(tiles), dim3(C::NW * 64), C::LDS_BYTES, stream, q);
-  return check_launch("moe_gemm_tiled_bf16_kernel");
+  hipLaunchKernelGGL(kern, dim3(tiles), dim3(C::NW * 64), lds_bytes, stream, q);
+  return check_launch("moe_gemm_tiled_kernel");
 }
 
 // Tile configurations (BM, BNR, WM, WN, SK, STAGES), one per rows-per-expert
@@ -409,6 +577,11 @@ using Cfg256 = TileCfg<256, 256, 4, 2, 128, 2>;  // 8 waves of 64x128
 using Cfg128 = TileCfg<128, 256, 2, 4, 128, 3>;  // 8 waves of 64x64
 using Cfg64 = TileCfg<64, 256, 1, 4, 128, 4>;   // 4 waves of 64x64
 using Cfg32 = TileCfg<32, 256, 1, 4, 128, 4>;   // 4 waves of 32x64
+// fp8 keeps a second accumulator set per k block (the block-scale fold), so
+// it has no 256-row configuration, and the stage scale area costs a stage
+// at 64 and 32 rows.
+using Fp8Cfg64 = TileCfg<64, 256, 1, 4, 128, 3>;
+using Fp8Cfg32 = TileCfg<32, 256, 1, 4, 128, 3>;
 
 static const int kTileRows[kTiledConfigs] = {Cfg256::BM, Cfg128::BM, Cfg64::BM,
                                              Cfg32::BM};
@@ -424,12 +597,17 @@ static int forced_tile() {
   return forced;
 }
 
-int tiled_config_for(double rows_per_expert) {
-  if (forced_tile() >= 0) return forced_tile();
-  if (rows_per_expert >= 192) return 0;
-  if (rows_per_expert >= 96) return 1;
-  if (rows_per_expert >= 40) return 2;
-  return 3;
+int tiled_config_supported(int dt, int cfg) {
+  return cfg >= 0 && cfg < kTiledConfigs && !(dt == kDtFp8 && cfg == 0);
+}
+
+int tiled_config_for(int dt, double rows_per_expert) {
+  int c = 3;
+  if (rows_per_expert >= 192) c = 0;
+  else if (rows_per_expert >= 96) c = 1;
+  else if (rows_per_expert >= 40) c = 2;
+  if (forced_tile() >= 0) c = forced_tile();
+  return (dt == kDtFp8 && c == 0) ? 1 : c;
 }
 
 int tiled_block_m(int cfg) { return kTileRows[cfg]; }
@@ -438,22 +616,42 @@ int tiled_block_m(int cfg) { return kTileRows[cfg]; }
 // GEMM2 output cols per tile (every configuration uses BNR = 256).
 int tiled_n_align(bool gemm1) { return gemm1 ? 128 : 256; }
 
+template <int DT, class C>
+static int launch_cfg(bool gemm1, const GemmParams& p, int row_blocks,
+                      hipStream_t stream) {
+  return gemm1 ? launch_tiled<DT, C, true>(p, row_blocks, stream)
+               : launch_tiled<DT, C, false>(p, row_blocks, stream);
+}
+
 int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
                       int row_blocks, hipStream_t stream) {
-  if (dt != kDtBf16) return fail(FGS_EUNSUPPORTED, "tiled GEMM: bf16 only");
+  if (!tiled_config_supported(dt, cfg))
+    return fail(FGS_EINVAL, "tiled GEMM: configuration " + std::to_string(cfg) +
+                                " not available for this element type");
   if (row_blocks <= 0) return FGS_OK;
-#define FGS_TILE_CASE(I, CFG)                                          \
-  case I:                                                              \
-    return gemm1 ? launch_tiled<CFG, true>(p, row_blocks, stream)      \
-                 : launch_tiled<CFG, false>(p, row_blocks, stream);
-  switch (cfg) {
-    FGS_TILE_CASE(0, Cfg256)
-    FGS_TILE_CASE(1, Cfg128)
-    FGS_TILE_CASE(2, Cfg64)
-    FGS_TILE_CASE(3, Cfg32)
+  switch (dt) {
+    case kDtBf16:
+      switch (cfg) {
+        case 0: return launch_cfg<kDtBf16, Cfg256>(gemm1, p, row_blocks, stream);
+        case 1: return launch_cfg<kDtBf16, Cfg128>(gemm1, p, row_blocks, stream);
+        case 2: return launch_cfg<kDtBf16, Cfg64>(gemm1, p, row_blocks, stream);
+        default: return launch_cfg<kDtBf16, Cfg32>(gemm1, p, row_blocks, stream);
+      }
+    case kDtInt8:
+      switch (cfg) {
+        case 0: return launch_cfg<kDtInt8, Cfg256>(gemm1, p, row_blocks, stream);
+        case 1: return launch_cfg<kDtInt8, Cfg128>(gemm1, p, row_blocks, stream);
+        case 2: return launch_cfg<kDtInt8, Cfg64>(gemm1, p, row_blocks, stream);
+        default: return launch_cfg<kDtInt8, Cfg32>(gemm1, p, row_blocks, stream);
+      }
+    case kDtFp8:
+      switch (cfg) {
+        case 1: return launch_cfg<kDtFp8, Cfg128>(gemm1, p, row_blocks, stream);
+        case 2: return launch_cfg<kDtFp8, Fp8Cfg64>(gemm1, p, row_blocks, stream);
+        default: return launch_cfg<kDtFp8, Fp8Cfg32>(gemm1, p, row_blocks, stream);
+      }
   }
-#undef FGS_TILE_CASE
-  return fail(FGS_EINVAL, "tiled GEMM: unknown configuration");
+  return fail(FGS_EINVAL, "tiled GEMM: unknown element type");
 }
 
 }  // namespace fgs

@@ -59,6 +59,8 @@ def test_align_max_padded():
         ((1, 4096, 14336, 8, 2, 0, 0x100 | 0x1000), _capi.FGS_EINVAL, "excludes"),
         ((1, 4096, 14336, 8, 2, 0, 0x5000), _capi.FGS_EINVAL, "TILE"),
         ((1, 4096, 14336, 8, 2, 0, 0x4000), 0, ""),
+        ((1, 7168, 2048, 256, 8, 1, 0x1000), _capi.FGS_EUNSUPPORTED, "not available"),
+        ((1, 7168, 2048, 256, 8, 1, 0x2000), 0, ""),
         ((1, 4000, 14336, 8, 2, 0, 0), _capi.FGS_EUNSUPPORTED, "multiples"),
         ((1, 3584, 2560, 64, 8, 2, 0), 0, ""),
         ((1, 3584 - 128, 2560, 64, 8, 2, 0), _capi.FGS_EUNSUPPORTED, "multiples"),

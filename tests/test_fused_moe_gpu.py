@@ -9,7 +9,9 @@ experts are copied to the host).
 
 Tolerance: |res - ref| <= atol + rtol*s elementwise, where s is the
 magnitude sum_j |w_j * y_j| of the top-k terms an output sums (outputs that
-cancel towards 0 keep the rounding error of their terms), and
+cancel towards 0 keep the rounding error of their terms; fp8 / int8 add a
+sixteenth of the absolute GEMM2 dot product, the scale on which the
+re-quantised intermediate's grid-point flips move y), and
 sum|res - ref| / sum|ref| <= mean_rel, with (atol, rtol, mean_rel) =
 (2e-2, 1e-2, 1e-2) for bf16 and (5e-2, 2e-2, 5e-2) for fp8 / int8 against
 the dequantising oracle.
@@ -124,6 +126,46 @@ def test_tiled_configs(gpu, shape, cfg):
     _check(res.cpu()[toks], ref, "bf16", f"tile {cfg} {shape}")
 
 
+_QUANT_TILES = [("fp8", c) for c in range(1, _capi.TILED_CONFIGS)] + \
+               [("int8", c) for c in range(_capi.TILED_CONFIGS)]
+
+
+@pytest.mark.parametrize("mode,cfg", _QUANT_TILES, ids=[f"{m}-{c}" for m, c in _QUANT_TILES])
+@pytest.mark.parametrize("shape", [(300, 512, 512, 8, 3), (1500, 1024, 768, 8, 2)])
+def test_tiled_configs_quantised(gpu, shape, mode, cfg):
+    """fp8 (128x128 block scales) and int8 (per-channel) tiled kernels, each
+    configuration forced, against the dequantising oracle."""
+    M, K, N, E, topk = shape
+    seed = M + K + N + E + topk
+    wts = testing.make_weights(K, N, E, mode, 0.1, device=gpu, seed=seed)
+    x, tw, ti = testing.make_tokens(M, K, E, topk, device=gpu, seed=seed)
+    res = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, _flags=_capi.flag_tile(cfg),
+                       **wts.kwargs(mode))
+    toks = _sample(M, 32)
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=mode,
+                            w1_scale=wts.w1_scale, w2_scale=wts.w2_scale,
+                            tokens=toks, return_mag=True)
+    _check(res.cpu()[toks], ref, mode, f"{mode} tile {cfg} {shape}")
+
+
+@pytest.mark.parametrize("mode", ["fp8", "int8"])
+def test_quantised_schedules_agree(gpu, mode):
+    """Streaming and tiled kernels of a quantised mode on the same inputs."""
+    M, K, N, E, topk = 700, 1024, 512, 8, 2
+    wts = testing.make_weights(K, N, E, mode, 0.1, device=gpu, seed=7)
+    x, tw, ti = testing.make_tokens(M, K, E, topk, device=gpu, seed=7)
+    dec = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, _flags=_capi.FLAG_FORCE_DECODE,
+                       **wts.kwargs(mode))
+    pre = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, _flags=_capi.FLAG_FORCE_PREFILL,
+                       **wts.kwargs(mode))
+    toks = _sample(M, 32)
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=mode,
+                            w1_scale=wts.w1_scale, w2_scale=wts.w2_scale,
+                            tokens=toks, return_mag=True)
+    _check(dec.cpu()[toks], ref, mode, f"{mode} decode")
+    _check(pre.cpu()[toks], ref, mode, f"{mode} prefill")
+
+
 def test_dropped_slots_and_routed_scaling(gpu):
     x, w1, w2, w, ids = _ref_inputs(16, 256, 128, 4, 2, gpu)
     ids2 = ids.clone()
@@ -165,8 +207,9 @@ CONFIG_CASES = [
     ("small", 64), ("mixtral", 1), ("mixtral", 32), ("mixtral", 512),
     ("mixtral", 4096), ("qwen3", 1), ("qwen3", 256), ("qwen3", 2048),
     ("qwen3_skewed", 16), ("qwen3_skewed", 2048), ("qwen3_skewed", 8192),
-    ("qwen2_int8", 1), ("qwen2_int8", 64), ("qwen2_int8", 1024),
+    ("qwen2_int8", 1), ("qwen2_int8", 64), ("qwen2_int8", 1024), ("qwen2_int8", 8192),
     ("deepseek_fp8", 1), ("deepseek_fp8", 32), ("deepseek_fp8", 512),
+    ("deepseek_fp8", 4096),
 ]
 
 

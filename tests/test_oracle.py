@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+from flaggems_sglang import testing
 from oracle import moe_ref
 
 
@@ -298,6 +299,37 @@ def test_moe_quantised_modes_track_bf16():
     for q in (fp8, int8):
         rel = (q - base).abs().sum() / base.abs().sum()
         assert rel < 0.08, rel
+
+
+@pytest.mark.parametrize("mode", ["fp8", "int8"])
+def test_quantised_tolerance_model(mode):
+    """The fp8 / int8 elementwise bound absorbs GEMM1 results perturbed at
+    the fp8 MFMA's accumulation precision (W13 scales times 1 + 2^-14: about
+    2 % of the bf16 intermediate moves by an ulp and its re-quantisation
+    flips grid points), and still rejects a 10 % error planted in one
+    128-column weight-scale block of W2."""
+    x, w1, w2, w, ids = _inputs(64, 512, 256, 4, 2, seed=9, scale=0.1)
+    qf = moe_ref.quant_weight_fp8_block if mode == "fp8" else moe_ref.quant_weight_int8_channel
+    q1 = [qf(w1[e]) for e in range(4)]
+    q2 = [qf(w2[e]) for e in range(4)]
+    W1, S1 = torch.stack([a for a, _ in q1]), torch.stack([b for _, b in q1])
+    W2, S2 = torch.stack([a for a, _ in q2]), torch.stack([b for _, b in q2])
+    tol = testing.TOL[mode]
+    ref, mag = moe_ref.fused_moe(x, W1, W2, w, ids, mode=mode, w1_scale=S1,
+                                 w2_scale=S2, return_mag=True)
+    out2 = moe_ref.fused_moe(x, W1, W2, w, ids, mode=mode, w1_scale=S1 * (1 + 2.0 ** -14),
+                             w2_scale=S2)
+    assert not torch.equal(out2, ref)
+    ok, _, mean_rel = moe_ref.compare(out2, ref, tol["atol"], tol["rtol"], mag)
+    assert ok and mean_rel < tol["mean_rel"]
+    S2bad = S2.clone()
+    if mode == "fp8":
+        S2bad[:, 0, :] *= 1.1   # output columns 0..127
+    else:
+        S2bad[:, :128] *= 1.1
+    bad = moe_ref.fused_moe(x, W1, W2, w, ids, mode=mode, w1_scale=S1, w2_scale=S2bad)
+    ok, _, _ = moe_ref.compare(bad, ref, tol["atol"], tol["rtol"], mag)
+    assert not ok
 
 
 def test_compare_helper():

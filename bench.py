@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep-steps", type=int, default=10)
+    ap.add_argument("--flags", type=lambda v: int(v, 0), default=0,
+                    help="schedule flags passed to the op (FGS_FLAG_* of "
+                         "include/fgs_moe.h; a tuning aid)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (the reference "
                          "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -77,10 +80,10 @@ def calibrate_copy():
 class Layer:
     """One configuration's weights plus a token batch, ready to call."""
 
-    def __init__(self, cfg, weights, M, device):
+    def __init__(self, cfg, weights, M, device, flags=0):
         from flaggems_sglang import testing
 
-        self.cfg, self.w, self.M = cfg, weights, M
+        self.cfg, self.w, self.M, self.flags = cfg, weights, M, flags
         self.x, self.tw, self.ti = testing.make_tokens(
             M, cfg.K, cfg.E, cfg.topk, cfg.scoring, cfg.hot_experts,
             cfg.hot_bias, device=device, seed=M + cfg.K + cfg.N + cfg.E + cfg.topk)
@@ -94,11 +97,16 @@ class Layer:
         import flaggems_sglang
 
         return flaggems_sglang.fused_moe(self.x, self.w.w1, self.w.w2, self.tw,
-                                         self.ti, **self.kw)
+                                         self.ti, _flags=self.flags, **self.kw)
 
 
 def time_layer(layer, steps, warmup, flush):
-    """Times `steps` calls (after `warmup`), returns (ms/call, stage ms)."""
+    """Times `steps` calls (after `warmup`), returns (ms/call, stage ms).
+
+    The timed calls run with the library's stage profiler off (its events
+    cost a few microseconds each on the GPU timeline); a second, untimed
+    pass of the same calls with the profiler on gives the per-stage split.
+    """
     import ctypes
 
     import torch
@@ -110,33 +118,36 @@ def time_layer(layer, steps, warmup, flush):
     for _ in range(warmup):
         layer()
     torch.cuda.synchronize()
+
+    def run(n, profile):
+        total = 0.0
+        lib.fgs_moe_profile_enable(1 if profile else 0)
+        if flush:
+            # cold weights each step: a 512 MiB write evicts L2 and MALL;
+            # only the layer call itself is inside the events.
+            for _ in range(n):
+                scratch.fill_(1)
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record()
+                layer()
+                b.record()
+                torch.cuda.synchronize()
+                total += a.elapsed_time(b)
+        else:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(n):
+                layer()
+            torch.cuda.synchronize()
+            total = (time.perf_counter() - t0) * 1e3
+        lib.fgs_moe_profile_enable(0)
+        return total / n
+
+    ms = run(steps, False)
     stage = (ctypes.c_float * 6)()
     lib.fgs_moe_profile_read(stage, 6)  # drop anything recorded before
-    total = 0.0
-    if flush:
-        # cold weights each step: a 512 MiB write evicts L2 and MALL; only
-        # the layer call itself is inside the events.
-        for _ in range(steps):
-            scratch.fill_(1)
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            lib.fgs_moe_profile_enable(1)
-            a.record()
-            layer()
-            b.record()
-            lib.fgs_moe_profile_enable(0)
-            torch.cuda.synchronize()
-            total += a.elapsed_time(b)
-        ms = total / steps
-    else:
-        lib.fgs_moe_profile_enable(1)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            layer()
-        torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / steps
-        lib.fgs_moe_profile_enable(0)
+    run(max(3, min(steps, 10)), True)
     n = lib.fgs_moe_profile_read(stage, 6)
     stages = dict(zip(_capi.PROFILE_STAGES, [float(v) for v in stage])) if n > 0 else {}
     return ms, stages
@@ -274,7 +285,7 @@ def main():
     torch.cuda.synchronize()
     log(f"weights {weights.nbytes() / 1e9:.2f} GB in {time.perf_counter() - t0:.1f}s")
 
-    head = Layer(cfg, weights, M, dev)
+    head = Layer(cfg, weights, M, dev, args.flags)
     small_ws = head.bytes < FLUSH_BYTES
     ms, stages = time_layer(head, args.steps, args.warmup, flush=small_ws)
     log(f"headline {cfg.name} M={M}: {ms:.4f} ms/layer stages={stages}")
@@ -282,7 +293,7 @@ def main():
     sweep = []
     if not args.no_sweep:
         for m in cfg.Ms:
-            lay = head if m == M else Layer(cfg, weights, m, dev)
+            lay = head if m == M else Layer(cfg, weights, m, dev, args.flags)
             flush = lay.bytes < FLUSH_BYTES
             sms, sst = time_layer(lay, args.sweep_steps, 3, flush)
             r = row(lay, sms, sst)
@@ -312,7 +323,7 @@ def main():
                 "softmax/sigmoid top-k routing)",
         "config": {"workload": f"{cfg.name} fused-MoE layer, M={M}",
                    "M": M, "K": cfg.K, "N": cfg.N, "E": cfg.E,
-                   "topk": cfg.topk, "mode": cfg.mode,
+                   "topk": cfg.topk, "mode": cfg.mode, "flags": args.flags,
                    "experts_touched": head.touched,
                    "layer_flops": head.flops, "layer_bytes": head.bytes,
                    "gb_s": round(head.bytes / (ms * 1e-3) / 1e9, 1),

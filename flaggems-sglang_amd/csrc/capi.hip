@@ -60,20 +60,20 @@ struct Plan {
 // k splits for the tiled GEMM2: its grid (row blocks x hidden/256 column
 // tiles) is often a few waves of 256 workgroups, and a partial last wave
 // idles most CUs for a whole tile. Pick the smallest split (<= 4, keeping
-// >= 8 stages of 64 k per split) whose expected grid fills >= 90 % of its
-// last wave, else the best one. Row blocks are estimated for balanced
-// routing: numel / B plus half a padded block per touched expert.
+// >= 8 LDS stages of 128 bytes of k per split) whose expected grid fills
+// >= 90 % of its last wave, else the best one. Row blocks are estimated for
+// balanced routing: numel / B plus half a padded block per touched expert.
 constexpr int kNumCUs = 256;  // MI355X
 
 static int pick_ksplit(int64_t numel, int e, int bm, int64_t hidden,
-                       int64_t inter) {
+                       int64_t k_bytes) {
   const double blocks = static_cast<double>(numel) / bm +
                         0.5 * static_cast<double>(std::min<int64_t>(e, numel));
   const double wgs = blocks * static_cast<double>(hidden / 256);
   int best = 1;
   double best_eff = 0.0;
   for (int s = 1; s <= 4; ++s) {
-    if (inter / 32 < 8 * s) break;
+    if (k_bytes / 128 < 8 * s) break;
     const double waves = wgs * s / kNumCUs;
     const double eff = waves / std::ceil(waves);
     if (eff >= 0.9) return s;
@@ -101,19 +101,23 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   const double rows_per_expert = static_cast<double>(numel) / e;
   p.mt = rows_per_expert <= 16 ? 1 : rows_per_expert <= 32 ? 2 : 4;
   p.block_m = 16 * p.mt;
-  // Prefill schedule: enough rows per expert that a 256-row block is mostly
-  // real rows, and shapes the tiled kernels cover.
+  // LDS-tiled kernels (deep DMA pipeline) from two rows per expert, or from
+  // one where GEMM2's k (inter) holds >= 16 LDS stages to amortise each
+  // tile's pipeline fill; the streaming kernels below that (single-token
+  // decode). Shapes the tiled kernels do not cover always stream.
+  const int64_t esz = p.dt == kDtBf16 ? 2 : 1;
   const bool tiled_ok = inter % tiled_n_align(true) == 0 &&
                         hidden % tiled_n_align(false) == 0;
   const int forced_cfg = ((flags & FGS_FLAG_TILE_MASK) >> 12) - 1;
+  const bool many_rows = rows_per_expert >= 2.0 ||
+                         (rows_per_expert >= 1.0 && inter * esz >= 16 * 128);
   p.tiled = tiled_ok && !(flags & FGS_FLAG_FORCE_DECODE) &&
-            ((flags & FGS_FLAG_FORCE_PREFILL) || forced_cfg >= 0 ||
-             rows_per_expert > 16);
+            ((flags & FGS_FLAG_FORCE_PREFILL) || forced_cfg >= 0 || many_rows);
   p.ksplit2 = 1;
   if (p.tiled) {
     p.tile_cfg = forced_cfg >= 0 ? forced_cfg : tiled_config_for(p.dt, rows_per_expert);
     p.block_m = tiled_block_m(p.tile_cfg);
-    p.ksplit2 = pick_ksplit(numel, e, p.block_m, hidden, inter);
+    p.ksplit2 = pick_ksplit(numel, e, p.block_m, hidden, inter * esz);
   }
   const int step = stream_step_k(p.dt);
   p.kw1 = pick_kw(hidden, step, 4);
@@ -126,7 +130,6 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   p.n_launch = std::min<int64_t>(p.n_blocks,
                                  numel / p.block_m + std::min<int64_t>(e, numel));
 
-  const int64_t esz = p.dt == kDtBf16 ? 2 : 1;
   int64_t o = 0;
   auto take = [&](int64_t bytes) {
     const int64_t at = o;
@@ -326,16 +329,17 @@ static int run_fused(const FusedArgs& a) {
   const uint8_t* act2 = reinterpret_cast<const uint8_t*>(a2);
   const float* act2_scale = nullptr;
   if (p.dt == kDtFp8) {
+    // only the padded rows in use (num_tokens_post_padded, on the device)
     rc = launch_quant_fp8_group(a2, ws + p.o_a2q,
                                 reinterpret_cast<float*>(ws + p.o_a2s),
-                                p.max_padded, a.inter, 128, a.stream);
+                                p.max_padded, a.inter, 128, a.stream, npp);
     if (rc) return rc;
     act2 = ws + p.o_a2q;
     act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
   } else if (p.dt == kDtInt8) {
     rc = launch_quant_int8_token(a2, reinterpret_cast<int8_t*>(ws + p.o_a2q),
                                  reinterpret_cast<float*>(ws + p.o_a2s),
-                                 p.max_padded, a.inter, a.stream);
+                                 p.max_padded, a.inter, a.stream, npp);
     if (rc) return rc;
     act2 = ws + p.o_a2q;
     act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
@@ -434,9 +438,9 @@ int32_t fgs_moe_quant_fp8_group(const void* x, void* q, float* scales,
                                 int64_t rows, int64_t cols, int32_t group,
                                 void* stream) {
   if (rows < 0 || cols <= 0) return fail(FGS_EINVAL, "rows >= 0 and cols > 0 required");
-  if (group < 8 || group > 512 || group % 8 || cols % group)
+  if (group < 8 || group > 512 || (group & (group - 1)) || cols % group)
     return fail(FGS_EUNSUPPORTED,
-                "group must be a multiple of 8 in [8, 512] dividing cols");
+                "group must be a power of two in [8, 512] dividing cols");
   if (rows > 0 && (!x || !q || !scales))
     return fail(FGS_EINVAL, "null pointer argument");
   if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(q) % 8)

@@ -117,64 +117,67 @@ __global__ __launch_bounds__(256) void moe_sum_partials_kernel(
 }
 
 // ------------------------------------------------------ fp8 group quant ---
-// One wave per (row, group of `group` columns); group % 8 == 0, group <= 512.
+// Each lane quantises 8 consecutive columns; the group/8 lanes of a group
+// (a power of two <= 64, aligned within the wave) reduce its amax with
+// butterfly shuffles, so a wave covers 512 columns.
 // scale = max(amax, 1e-10) / 448; q = e4m3fn(clamp(x / scale, +-448)).
+// With `rows_dev` given, rows >= *rows_dev are skipped (padded-row buffers
+// whose live prefix is only known on the device).
 __global__ __launch_bounds__(256) void quant_fp8_group_kernel(
     const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
-    float* __restrict__ scales, int64_t rows, int64_t cols, int group) {
+    float* __restrict__ scales, int64_t rows, int64_t cols, int group,
+    const int32_t* __restrict__ rows_dev) {
   const int lane = threadIdx.x & 63;
-  const int64_t groups_per_row = cols / group;
-  const int64_t n_items = rows * groups_per_row;
-  const int64_t item = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) / 64;
-  if (item >= n_items) return;
-  const int64_t r = item / groups_per_row;
-  const int64_t g = item - r * groups_per_row;
-  const uint16_t* src = x + r * cols + g * group;
-  uint8_t* dst = q + r * cols + g * group;
-  // Each lane holds up to 8 columns.
-  const bool active = lane * 8 < group;
-  float v[8];
+  const int lanes_per_group = group / 8;
+  const int64_t vec_per_row = cols / 8;
+  const int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  const int64_t r = v / vec_per_row;
+  const int64_t live_rows = rows_dev ? min(rows, static_cast<int64_t>(*rows_dev)) : rows;
+  const bool active = r < live_rows;
+  const int64_t c = (v - r * vec_per_row) * 8;
+  float f[8];
   float amax = 0.f;
   if (active) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(src + lane * 8);
+    const u32x4 w = *reinterpret_cast<const u32x4*>(x + r * cols + c);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      v[2 * j] = __uint_as_float(w[j] << 16);
-      v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      f[2 * j] = __uint_as_float(w[j] << 16);
+      f[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  for (int d = lanes_per_group / 2; d >= 1; d >>= 1)
+    amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  if (!active) return;
   const float scale = fmaxf(amax, 1e-10f) / 448.0f;
-  if (active) {
-    uint32_t lo = 0, hi = 0;
+  uint32_t lo = 0, hi = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float a = fminf(fmaxf(v[2 * j] / scale, -448.f), 448.f);
-      const float b = fminf(fmaxf(v[2 * j + 1] / scale, -448.f), 448.f);
-      const uint32_t p = cvt_pk_fp8(a, b);
-      if (j < 2)
-        lo |= p << (16 * j);
-      else
-        hi |= p << (16 * (j - 2));
-    }
-    uint2 o;
-    o.x = lo;
-    o.y = hi;
-    *reinterpret_cast<uint2*>(dst + lane * 8) = o;
+  for (int j = 0; j < 4; ++j) {
+    const float a = fminf(fmaxf(f[2 * j] / scale, -448.f), 448.f);
+    const float b = fminf(fmaxf(f[2 * j + 1] / scale, -448.f), 448.f);
+    const uint32_t pk = cvt_pk_fp8(a, b);
+    if (j < 2)
+      lo |= pk << (16 * j);
+    else
+      hi |= pk << (16 * (j - 2));
   }
-  if (lane == 0) scales[r * groups_per_row + g] = scale;
+  uint2 o;
+  o.x = lo;
+  o.y = hi;
+  *reinterpret_cast<uint2*>(q + r * cols + c) = o;
+  if ((lane & (lanes_per_group - 1)) == 0) scales[r * (cols / group) + c / group] = scale;
 }
 
 // ----------------------------------------------------- int8 token quant ---
-// One workgroup (256 threads) per row; cols % 8 == 0.
+// One workgroup (256 threads) per row; cols % 8 == 0. With `rows_dev`
+// given, rows >= *rows_dev are skipped.
 // scale = max(amax, 1e-10) / 127; q = clamp(rne(x / scale), -127, 127).
 __global__ __launch_bounds__(256) void quant_int8_token_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q,
-    float* __restrict__ scales, int64_t cols) {
+    float* __restrict__ scales, int64_t cols, const int32_t* __restrict__ rows_dev) {
   const int64_t r = blockIdx.x;
+  if (rows_dev && r >= *rows_dev) return;
   const uint16_t* src = x + r * cols;
   int8_t* dst = q + r * cols;
   float amax = 0.f;
@@ -266,22 +269,22 @@ int launch_moe_sum_partials(const float* part, int nsplit, void* out, int64_t m,
 
 int launch_quant_fp8_group(const void* x, void* q, float* scales,
                            int64_t rows, int64_t cols, int group,
-                           hipStream_t stream) {
-  const int64_t items = rows * (cols / group);
-  if (items == 0) return FGS_OK;
-  const int64_t blocks = (items * 64 + 255) / 256;
-  hipLaunchKernelGGL(quant_fp8_group_kernel, dim3(static_cast<unsigned>(blocks)),
+                           hipStream_t stream, const int32_t* rows_dev) {
+  const int64_t vecs = rows * (cols / 8);
+  if (vecs == 0) return FGS_OK;
+  hipLaunchKernelGGL(quant_fp8_group_kernel, dim3(static_cast<unsigned>((vecs + 255) / 256)),
                      dim3(256), 0, stream, static_cast<const uint16_t*>(x),
-                     static_cast<uint8_t*>(q), scales, rows, cols, group);
+                     static_cast<uint8_t*>(q), scales, rows, cols, group, rows_dev);
   return check_launch("quant_fp8_group_kernel");
 }
 
 int launch_quant_int8_token(const void* x, int8_t* q, float* scales,
-                            int64_t rows, int64_t cols, hipStream_t stream) {
+                            int64_t rows, int64_t cols, hipStream_t stream,
+                            const int32_t* rows_dev) {
   if (rows == 0) return FGS_OK;
   hipLaunchKernelGGL(quant_int8_token_kernel, dim3(static_cast<unsigned>(rows)),
                      dim3(256), 0, stream, static_cast<const uint16_t*>(x), q,
-                     scales, cols);
+                     scales, cols, rows_dev);
   return check_launch("quant_int8_token_kernel");
 }
 

@@ -30,6 +30,7 @@ struct GemmParams {
   int32_t topk;
   int32_t weight_on_input;
   int32_t row_blocks;     // row blocks of the launch (tiled kernels)
+  int32_t group_m;        // row blocks per rasterization band (tiled; 0: off)
   int32_t group_n;        // column tiles per rasterization group (tiled)
   int32_t ksplit;         // GEMM2 k splits; > 1: out is fp32 [ksplit][numel][n_out]
 };
@@ -52,10 +53,14 @@ int launch_moe_sum_partials(const float* part, int nsplit, void* out, int64_t m,
                             int topk, int64_t k, const int32_t* ids,
                             int num_experts, const float* weights,
                             hipStream_t stream);
+// Activation quantisers; with `rows_dev` given only rows < *rows_dev (a
+// device-side count such as num_tokens_post_padded) are processed.
 int launch_quant_fp8_group(const void* x, void* q, float* scales, int64_t rows,
-                           int64_t cols, int group, hipStream_t stream);
+                           int64_t cols, int group, hipStream_t stream,
+                           const int32_t* rows_dev = nullptr);
 int launch_quant_int8_token(const void* x, int8_t* q, float* scales,
-                            int64_t rows, int64_t cols, hipStream_t stream);
+                            int64_t rows, int64_t cols, hipStream_t stream,
+                            const int32_t* rows_dev = nullptr);
 
 // k elements per pipeline step of the streaming kernels (kdim must be a
 // multiple of it).

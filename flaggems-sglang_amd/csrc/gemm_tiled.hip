@@ -50,13 +50,24 @@ __device__ __forceinline__ void wait_lgkm0() {
 // Tile order. The grid is 1-D and padded to a multiple of the 8 XCDs.
 // Workgroup `pid` runs on XCD pid % 8, so logical tile
 // (pid % 8) * (grid / 8) + pid / 8 gives every XCD a contiguous range of
-// tiles, walked in groups of group_n column tiles: the workgroups an XCD runs
-// at once cover a few row blocks x group_n column tiles and share their
-// activation and weight tiles through that XCD's L2.
+// tiles. group_m > 0: bands of group_m row blocks, walked column by column
+// (row block fastest), so the row blocks of one expert -- adjacent in the
+// sorted order -- read each weight tile back to back, and a band's
+// activation tiles are reused across its columns. group_m == 0: all row
+// blocks walked per group of group_n column tiles (column fastest).
 __device__ __forceinline__ bool tile_of(int pid, int grid, int n_rb, int n_ct,
-                                        int group_n, int* rb, int* ct) {
+                                        int group_m, int group_n, int* rb, int* ct) {
   const int logical = (pid % 8) * (grid / 8) + pid / 8;
   if (logical >= n_rb * n_ct) return false;
+  if (group_m > 0) {
+    const int band_tiles = group_m * n_ct;
+    const int band = logical / band_tiles;
+    const int rem = logical - band * band_tiles;
+    const int rows = min(group_m, n_rb - band * group_m);
+    *ct = rem / rows;
+    *rb = band * group_m + rem % rows;
+    return true;
+  }
   const int span = n_rb * group_n;
   const int group = logical / span;
   const int idx = logical - group * span;
@@ -197,8 +208,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   constexpr int N_PER_TILE = GEMM1 ? BNR / 2 : BNR;
   const int n_ct = static_cast<int>(p.n_out / N_PER_TILE);
   int rb_id, tile_n;
-  if (!tile_of(blockIdx.x, gridDim.x, p.row_blocks * p.ksplit, n_ct, p.group_n,
-               &rb_id, &tile_n))
+  if (!tile_of(blockIdx.x, gridDim.x, p.row_blocks * p.ksplit, n_ct, p.group_m,
+               p.group_n, &rb_id, &tile_n))
     return;
   // split-K (GEMM2 only): the row-block index space repeats once per split
   const int ks = rb_id / p.row_blocks;
@@ -536,14 +547,19 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   }
 }
 
-// Column tiles per rasterization group (FGS_MOE_GROUPN overrides; a tuning
-// aid read once).
+// Rasterization (FGS_MOE_GROUPM / FGS_MOE_GROUPN override; tuning aids read
+// once): row blocks per band, or, with bands off (0), column tiles per group.
+static int env_choice(const char* name, int dflt, int lo, int hi) {
+  const char* s = getenv(name);
+  const int v = s ? atoi(s) : dflt;
+  return (v >= lo && v <= hi) ? v : dflt;
+}
+static int group_m_choice() {
+  static const int g = env_choice("FGS_MOE_GROUPM", 0, 0, 64);
+  return g;
+}
 static int group_n_choice() {
-  static const int g = [] {
-    const char* s = getenv("FGS_MOE_GROUPN");
-    const int v = s ? atoi(s) : 4;
-    return (v >= 1 && v <= 64) ? v : 4;
-  }();
+  static const int g = env_choice("FGS_MOE_GROUPN", 4, 1, 64);
   return g;
 }
 
@@ -563,6 +579,7 @@ static int launch_tiled(const GemmParams& p, int row_blocks, hipStream_t stream)
   const int tiles_n = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   GemmParams q = p;
   q.row_blocks = row_blocks;
+  q.group_m = group_m_choice();
   q.group_n = group_n_choice();
   if (GEMM1 || q.ksplit < 1) q.ksplit = 1;
   const int tiles = (row_blocks * q.ksplit * tiles_n + 7) / 8 * 8;
@@ -605,7 +622,7 @@ int tiled_config_for(int dt, double rows_per_expert) {
   int c = 3;
   if (rows_per_expert >= 192) c = 0;
   else if (rows_per_expert >= 96) c = 1;
-  else if (rows_per_expert >= 40) c = 2;
+  else if (rows_per_expert >= 24) c = 2;
   if (forced_tile() >= 0) c = forced_tile();
   return (dt == kDtFp8 && c == 0) ? 1 : c;
 }

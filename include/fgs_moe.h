@@ -99,6 +99,7 @@ int32_t fgs_moe_sum(const void* in, void* out, int64_t m, int32_t topk,
 /* Dynamic per-(row, group) fp8 quantisation: x bf16 [rows, cols],
  * q e4m3fn [rows, cols], scales f32 [rows, cols / group] with
  * scale = max(amax, 1e-10) / 448 and q = e4m3fn(clamp(x / scale, +-448)).
+ * group: a power of two in [8, 512] dividing cols.
  * No reference counterpart (the reference asserts fp8 off,
  * ops/fused_moe.py:170-172); needed by the fp8 w8a8 path. */
 int32_t fgs_moe_quant_fp8_group(const void* x, void* q, float* scales,

@@ -108,15 +108,16 @@ def test_moe_sum(gpu, m, k, K):
     assert _ulp_diff_bf16(out, ref).max() <= 1
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 128), (37, 7168), (512, 2048)])
-def test_quant_fp8_group_bit_exact(gpu, rows, cols):
+@pytest.mark.parametrize("rows,cols,group", [(1, 128, 128), (37, 7168, 128), (512, 2048, 128),
+                                            (5, 1024, 512), (9, 256, 32), (3, 64, 8)])
+def test_quant_fp8_group_bit_exact(gpu, rows, cols, group):
     g = torch.Generator().manual_seed(rows + cols)
     x = (torch.randn(rows, cols, generator=g) * 2).to(torch.bfloat16)
     x[0, :5] = 0.0
     if rows > 1:
-        x[1, :128] = 0.0  # all-zero group: scale = 1e-10/448
-    q, s = fm.per_token_group_quant_fp8(x.to(gpu), 128)
-    rq, rsc = moe_ref.quant_fp8_group(x, 128)
+        x[1, :group] = 0.0  # all-zero group: scale = 1e-10/448
+    q, s = fm.per_token_group_quant_fp8(x.to(gpu), group)
+    rq, rsc = moe_ref.quant_fp8_group(x, group)
     assert torch.equal(s.cpu(), rsc)
     assert torch.equal(q.cpu().view(torch.uint8), rq.view(torch.uint8))
 

@@ -100,12 +100,14 @@ class Layer:
                                          self.ti, _flags=self.flags, **self.kw)
 
 
-def time_layer(layer, steps, warmup, flush):
+def time_layer(layer, steps, warmup, flush, profile_timed=False):
     """Times `steps` calls (after `warmup`), returns (ms/call, stage ms).
 
-    The timed calls run with the library's stage profiler off (its events
-    cost a few microseconds each on the GPU timeline); a second, untimed
-    pass of the same calls with the profiler on gives the per-stage split.
+    With `profile_timed` the library's stage events are recorded during the
+    timed calls themselves (the headline: its roofline comes from the same
+    launches it times; the events cost a few microseconds per call).
+    Otherwise the timed calls run with the profiler off and a second pass of
+    the same calls with it on gives the per-stage split (the sweep).
     """
     import ctypes
 
@@ -144,10 +146,11 @@ def time_layer(layer, steps, warmup, flush):
         lib.fgs_moe_profile_enable(0)
         return total / n
 
-    ms = run(steps, False)
     stage = (ctypes.c_float * 6)()
     lib.fgs_moe_profile_read(stage, 6)  # drop anything recorded before
-    run(max(3, min(steps, 10)), True)
+    ms = run(steps, profile_timed)
+    if not profile_timed:
+        run(max(3, min(steps, 10)), True)
     n = lib.fgs_moe_profile_read(stage, 6)
     stages = dict(zip(_capi.PROFILE_STAGES, [float(v) for v in stage])) if n > 0 else {}
     return ms, stages
@@ -287,7 +290,8 @@ def main():
 
     head = Layer(cfg, weights, M, dev, args.flags)
     small_ws = head.bytes < FLUSH_BYTES
-    ms, stages = time_layer(head, args.steps, args.warmup, flush=small_ws)
+    ms, stages = time_layer(head, args.steps, args.warmup, flush=small_ws,
+                            profile_timed=True)
     log(f"headline {cfg.name} M={M}: {ms:.4f} ms/layer stages={stages}")
 
     sweep = []

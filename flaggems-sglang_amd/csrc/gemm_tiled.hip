@@ -219,7 +219,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   if (e < 0) return;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave index in an SGPR: LDS-DMA destinations (M0) then stay scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN;
   const int wn = wave % WN;
   const int row0 = rb_id * BM;
@@ -399,6 +400,14 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
           }
         }
     };
+    // Region schedule: one MFMA, then all of the next step's fragment
+    // reads, then the remaining MFMAs (reads get the MFMAs' time to land).
+    auto sched_step = [&]() {
+      constexpr int NR = (RB + CB) * FC;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - 1, 0);
+    };
     auto fold = [&]() {
       if constexpr (FP8) {
 #pragma unroll
@@ -428,6 +437,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
       for (int kk = 0; kk + 1 < KK; ++kk) {
         read_frags(kt, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
         mma(kk, fa[kk & 1], fb[kk & 1]);
+        sched_step();
+        __builtin_amdgcn_sched_barrier(0);
       }
       wait_lgkm0();
       wait_stages(min(STAGES - 2, KT - 2 - kt));

@@ -35,7 +35,7 @@ static hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 static int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
 constexpr int kMaxExperts = 1024;
-constexpr int kKnownFlags = FGS_FLAG_ROUTER_WEIGHT_ON_INPUT |
+constexpr int kKnownFlags = FGS_FLAG_ROUTER_WEIGHT_ON_INPUT | FGS_FLAG_ACT_GELU |
                             FGS_FLAG_FORCE_DECODE | FGS_FLAG_FORCE_PREFILL |
                             FGS_FLAG_TILE_MASK;
 
@@ -249,6 +249,11 @@ struct FusedArgs {
   int64_t ws_bytes;
   void* out;
   hipStream_t stream;
+  // bias variant: fp32 biases, swiglu(alpha, limit) activation
+  const float* b13 = nullptr;
+  const float* b2 = nullptr;
+  bool swiglu = false;
+  float alpha = 1.f, limit = 0.f;
 };
 
 static int run_fused(const FusedArgs& a) {
@@ -263,6 +268,7 @@ static int run_fused(const FusedArgs& a) {
     return fail(FGS_EINVAL, "quantised mode needs w13_scale and w2_scale");
   if (reinterpret_cast<uintptr_t>(a.x) % 16 || reinterpret_cast<uintptr_t>(a.w13) % 16 ||
       reinterpret_cast<uintptr_t>(a.w2) % 16 || reinterpret_cast<uintptr_t>(a.out) % 16 ||
+      reinterpret_cast<uintptr_t>(a.b13) % 16 || reinterpret_cast<uintptr_t>(a.b2) % 16 ||
       reinterpret_cast<uintptr_t>(a.ws) % 256)
     return fail(FGS_EINVAL, "tensors must be 16-byte aligned (workspace 256)");
 
@@ -319,6 +325,10 @@ static int run_fused(const FusedArgs& a) {
   g1.numel = numel;
   g1.topk = a.topk;
   g1.weight_on_input = on_input;
+  g1.act = a.swiglu ? kActSwiglu : (a.flags & FGS_FLAG_ACT_GELU) ? kActGelu : kActSilu;
+  g1.alpha = a.alpha;
+  g1.limit = a.limit;
+  g1.bias = a.b13;
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, static_cast<int>(p.n_launch),
                                    a.stream)
                : launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
@@ -351,6 +361,7 @@ static int run_fused(const FusedArgs& a) {
   g2.a_scale = act2_scale;
   g2.w = static_cast<const uint8_t*>(a.w2);
   g2.w_scale = a.w2_scale;
+  g2.bias = a.b2;
   g2.out = y;
   g2.kdim = a.inter;
   g2.n_out = a.hidden;
@@ -514,6 +525,31 @@ int32_t fgs_moe_fused_bf16(const void* x, const void* w13, const void* w2,
               nullptr,        topk_weights, topk_ids, m,      hidden,
               inter,          num_experts,  topk,     flags,  workspace,
               ws_bytes,       out,          as_stream(stream)};
+  return run_fused(a);
+}
+
+int32_t fgs_moe_fused_bf16_bias(const void* x, const void* w13, const float* b13,
+                                const void* w2, const float* b2,
+                                const float* topk_weights, const int32_t* topk_ids,
+                                int64_t m, int64_t hidden, int64_t inter,
+                                int32_t num_experts, int32_t topk, int32_t flags,
+                                float alpha, float limit, void* workspace,
+                                int64_t ws_bytes, void* out, void* stream) {
+  if (flags & FGS_FLAG_ACT_GELU)
+    return fail(FGS_EUNSUPPORTED, "the bias variant's activation is swiglu only");
+  if (m > 0 && (!b13 || !b2))
+    return fail(FGS_EINVAL, "bias variant needs both b13 and b2");
+  if (!(alpha == alpha) || !(limit == limit))
+    return fail(FGS_EINVAL, "alpha and limit must not be NaN");
+  FusedArgs a{FGS_QMODE_BF16, x,      w13,    w2,          nullptr,
+              nullptr,        topk_weights, topk_ids, m,      hidden,
+              inter,          num_experts,  topk,     flags,  workspace,
+              ws_bytes,       out,          as_stream(stream)};
+  a.b13 = b13;
+  a.b2 = b2;
+  a.swiglu = true;
+  a.alpha = alpha;
+  a.limit = limit;
   return run_fused(a);
 }
 

@@ -44,20 +44,43 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
-// GEMM1 epilogue with the rounding points of the reference's unfused path:
+// GEMM1 activations.
+enum { kActSilu = 0, kActGelu = 1, kActSwiglu = 2 };
+
+// gelu(g) * u with the exact (erf) gelu: the activation sgl_kernel's
+// gelu_and_mul applies (ops/fused_moe.py:219-220).
+__device__ __forceinline__ float gelu_mul(float g, float u) {
+  return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f)) * u;
+}
+
+// GEMM1 epilogue.
+// silu / gelu keep the rounding points of the reference's unfused path:
 // matmul_ogs writes its output (gate and up halves, gammas applied when the
 // router weight goes on the input, ops/fused_moe.py:202-212) in bf16, then
-// _silu_and_mul_kernel computes in fp32 from those bf16 values and stores
-// bf16 (:58-63).
-__device__ __forceinline__ uint16_t gemm1_epilogue(float g, float u,
-                                                   bool scale, float gamma) {
+// the activation kernel computes in fp32 from those bf16 values and stores
+// bf16 (:58-63, :219-220).
+// swiglu is the activation fused into matmul_ogs by the bias variant
+// (:274-314): gate g and linear u stay fp32 (biases already added);
+// with limit > 0, g = min(g, limit) and u = clamp(u, -limit, limit); out =
+// bf16(g * sigmoid(alpha * g) * (u + 1)).
+__device__ __forceinline__ uint16_t gemm1_epilogue(float g, float u, bool scale,
+                                                   float gamma, int act = kActSilu,
+                                                   float alpha = 1.f, float limit = 0.f) {
   if (scale) {
     g *= gamma;
     u *= gamma;
   }
+  if (act == kActSwiglu) {
+    if (limit > 0.f) {
+      g = fminf(g, limit);
+      u = fminf(fmaxf(u, -limit), limit);
+    }
+    const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-alpha * g));
+    return f32_to_bf16_bits(g * sg * (u + 1.0f));
+  }
   g = bf16_bits_to_f32(f32_to_bf16_bits(g));
   u = bf16_bits_to_f32(f32_to_bf16_bits(u));
-  return f32_to_bf16_bits(silu_mul(g, u));
+  return f32_to_bf16_bits(act == kActGelu ? gelu_mul(g, u) : silu_mul(g, u));
 }
 
 // ------------------------------------------------------------------ MFMA ---

@@ -33,6 +33,9 @@ struct GemmParams {
   int32_t group_m;        // row blocks per rasterization band (tiled; 0: off)
   int32_t group_n;        // column tiles per rasterization group (tiled)
   int32_t ksplit;         // GEMM2 k splits; > 1: out is fp32 [ksplit][numel][n_out]
+  int32_t act;            // GEMM1 activation (kActSilu / kActGelu / kActSwiglu)
+  float alpha, limit;     // swiglu parameters
+  const float* bias;      // fp32 per expert: GEMM1 [E, 2N] (gate | up), GEMM2 [E, K]; or null
 };
 
 size_t align_smem_bytes(int num_experts);

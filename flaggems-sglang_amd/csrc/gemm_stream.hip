@@ -279,12 +279,14 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
         } else {
           x = acc[nb][mt][i];
         }
+        if (p.bias)  // per-expert fp32 bias (the bias variant)
+          x += p.bias[static_cast<int64_t>(e) * p.nrows_w + (nb ? p.n_out : 0) + col];
         v[nb] = x;
       }
       if constexpr (GEMM1) {
         out[static_cast<int64_t>(r) * p.n_out + col] =
             gemm1_epilogue(v[0], v[NB - 1], p.weight_on_input && valid,
-                           valid ? p.topk_w[sid] : 0.f);
+                           valid ? p.topk_w[sid] : 0.f, p.act, p.alpha, p.limit);
       } else {
         if (valid)
           out[static_cast<int64_t>(sid) * p.n_out + col] = f32_to_bf16_bits(v[0]);

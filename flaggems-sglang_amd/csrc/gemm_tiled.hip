@@ -488,6 +488,11 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
     if constexpr (INT8) return static_cast<float>(a[v]) * sa * sw;
     else return a[v];
   };
+  // per-expert fp32 bias (the bias variant); GEMM2 split-K adds it once
+  const float* bias = p.bias && (GEMM1 || ks == 0) ? p.bias + wbase : nullptr;
+  auto bias4 = [&](int64_t col) -> f32x4 {
+    return bias ? *reinterpret_cast<const f32x4*>(bias + col) : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
 #pragma unroll
   for (int i = 0; i < RB; ++i) {
     const int rr = wm * WROWS + i * 32 + (lane & 31);
@@ -507,12 +512,15 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
         for (int g4 = 0; g4 < 4; ++g4) {
           const f32x4 swg = wscale4(col0 + 8 * g4);
           const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
+          const f32x4 bg = bias4(col0 + 8 * g4);
+          const f32x4 bu = bias4(p.n_out + col0 + 8 * g4);
           uint32_t w0 = 0, w1 = 0;
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const uint32_t b = gemm1_epilogue(value(acc[i][jb], 4 * g4 + t, sa, swg[t]),
-                                              value(acc[i][jb + CB / 2], 4 * g4 + t, sa, swu[t]),
-                                              scale, gamma);
+            const uint32_t b = gemm1_epilogue(
+                value(acc[i][jb], 4 * g4 + t, sa, swg[t]) + bg[t],
+                value(acc[i][jb + CB / 2], 4 * g4 + t, sa, swu[t]) + bu[t], scale, gamma,
+                p.act, p.alpha, p.limit);
             if (t < 2) w0 |= b << (16 * t);
             else w1 |= b << (16 * (t - 2));
           }
@@ -532,10 +540,12 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const f32x4 sw = wscale4(col0 + 8 * g4);
+          const f32x4 bb = bias4(col0 + 8 * g4);
           const int v = 4 * g4;
           *reinterpret_cast<f32x4*>(orow + col0 + 8 * g4) =
-              f32x4{value(acc[i][j], v, sa, sw[0]), value(acc[i][j], v + 1, sa, sw[1]),
-                    value(acc[i][j], v + 2, sa, sw[2]), value(acc[i][j], v + 3, sa, sw[3])};
+              f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0], value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
+                    value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                    value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
         }
       }
     } else {
@@ -546,11 +556,13 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const f32x4 sw = wscale4(col0 + 8 * g4);
+          const f32x4 bb = bias4(col0 + 8 * g4);
           const int v = 4 * g4;
           uint2 v2;
-          v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]), value(acc[i][j], v + 1, sa, sw[1]));
-          v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]),
-                             value(acc[i][j], v + 3, sa, sw[3]));
+          v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
+                             value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
+          v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                             value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
           *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
         }
       }

@@ -21,6 +21,7 @@ QMODE_FP8_BLOCK = 1
 QMODE_INT8_CHANNEL = 2
 
 FLAG_ROUTER_WEIGHT_ON_INPUT = 0x1
+FLAG_ACT_GELU = 0x2
 FLAG_FORCE_DECODE = 0x100
 FLAG_FORCE_PREFILL = 0x200
 TILED_CONFIGS = 4  # row blocks 256, 128, 64, 32
@@ -60,6 +61,12 @@ SIGNATURES = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
          _i64, _i32, _i32, _i32, _c_void_p, _i64, _c_void_p, _c_void_p],
+    ),
+    "fgs_moe_fused_bf16_bias": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _i64, _i64, _i64, _i32, _i32, _i32, ctypes.c_float,
+         ctypes.c_float, _c_void_p, _i64, _c_void_p, _c_void_p],
     ),
     "fgs_moe_fused_fp8_block": (
         _i32,

@@ -41,6 +41,22 @@ def _require_gpu(name: str, t: torch.Tensor) -> None:
         )
 
 
+_DEINTERLEAVE_CACHE: dict = {}
+
+
+def _cached(cache: dict, w: torch.Tensor, fn):
+    """``fn(w)`` cached per weight version (a model's weights are converted
+    once, not on every call)."""
+    key = (w.data_ptr(), w._version, tuple(w.shape), tuple(w.stride()), w.dtype)
+    hit = cache.get(key)
+    if hit is None:
+        if len(cache) > 64:
+            cache.clear()
+        hit = fn(w)
+        cache[key] = hit
+    return hit
+
+
 # --------------------------------------------------------------- routing ---
 @dataclass
 class RoutingData:
@@ -251,7 +267,10 @@ def fused_moe(
     up rows); ``w2`` ``[E, K, N]``; ``topk_weights`` ``[M, topk]``;
     ``topk_ids`` ``[M, topk]``. Returns bf16 ``[M, K]``::
 
-        out[t] = sum_j w[t,j] * (silu(x_t W1g[e]^T) * (x_t W1u[e]^T)) W2[e]^T
+        out[t] = sum_j w[t,j] * (act(x_t W1g[e]^T) * (x_t W1u[e]^T)) W2[e]^T
+
+    with ``act`` silu, or the exact (erf) gelu for ``activation="gelu"``
+    (sgl_kernel's ``gelu_and_mul``, ops/fused_moe.py:219-220).
 
     Modes: bf16; ``use_fp8_w8a8`` with ``block_shape=[128, 128]`` (e4m3fn
     weights, fp32 block scales ``w1_scale [E, 2N/128, K/128]``,
@@ -266,9 +285,7 @@ def fused_moe(
     _check_unsupported(expert_map=expert_map, a1_scale=a1_scale,
                        a2_scale=a2_scale)
     assert inplace is False, "Inplace is not supported"
-    if activation != "silu":
-        if activation == "gelu":
-            raise NotImplementedError("activation='gelu' is not implemented")
+    if activation not in ("silu", "gelu"):
         raise ValueError(f"Unsupported FusedMoe activation: {activation}")
     assert not (use_fp8_w8a8 and use_int8_w8a8), (
         "use_fp8_w8a8 and use_int8_w8a8 are exclusive")
@@ -322,6 +339,8 @@ def fused_moe(
     flags = int(_flags)
     if apply_router_weight_on_input:
         flags |= _capi.FLAG_ROUTER_WEIGHT_ON_INPUT
+    if activation == "gelu":
+        flags |= _capi.FLAG_ACT_GELU
     x = hidden_states.contiguous()
     w1 = w1.contiguous()
     w2 = w2.contiguous()
@@ -360,20 +379,14 @@ def fused_moe(
 
 
 _TRANSPOSE_CACHE: dict = {}
+_TRANSPOSE_DEINTERLEAVE_CACHE: dict = {}
 
 
 def _native_layout(w: torch.Tensor) -> torch.Tensor:
     """``[E, A, B] -> [E, B, A]`` contiguous, cached per weight version so a
     model's weights are transposed once, not on every call (the reference
     plugin transposes on every call, ops/fused_moe.py:342-343)."""
-    key = (w.data_ptr(), w._version, tuple(w.shape), tuple(w.stride()), w.dtype)
-    hit = _TRANSPOSE_CACHE.get(key)
-    if hit is None:
-        if len(_TRANSPOSE_CACHE) > 64:
-            _TRANSPOSE_CACHE.clear()
-        hit = w.transpose(-1, -2).contiguous()
-        _TRANSPOSE_CACHE[key] = hit
-    return hit
+    return _cached(_TRANSPOSE_CACHE, w, lambda t: t.transpose(-1, -2).contiguous())
 
 
 def triton_kernel_fused_experts(
@@ -434,17 +447,252 @@ def triton_kernel_fused_experts(
                         apply_router_weight_on_input=apply_router_weight_on_input)
         return out.view(num_tokens, hidden)
     # No combine: one row per (token, slot) in the gate (row-sorted) order.
+    return _uncombined(
+        lambda x, tw, ti: fused_moe(
+            x, w13n, w2n, tw, ti, activation=activation,
+            apply_router_weight_on_input=apply_router_weight_on_input),
+        hidden_states, topk_weights, topk_ids)
+
+
+def _deinterleave_rows(w: torch.Tensor) -> torch.Tensor:
+    """Rows ``[g0, u0, g1, u1, ...]`` (dim -2 of ``[E, 2N, K]``, or the last
+    dim of a bias ``[E, 2N]``) -> ``[g0..g(N-1), u0..u(N-1)]``."""
+    if w.ndim == 2:
+        return torch.cat([w[:, 0::2], w[:, 1::2]], dim=1).contiguous()
+    return torch.cat([w[:, 0::2, :], w[:, 1::2, :]], dim=1).contiguous()
+
+
+def fused_moe_with_bias(
+    hidden_states: torch.Tensor,
+    w1: torch.Tensor,
+    b1: torch.Tensor,
+    w2: torch.Tensor,
+    b2: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    apply_router_weight_on_input: bool = False,
+    gemm1_alpha: Optional[float] = None,
+    gemm1_clamp_limit: Optional[float] = None,
+    interleaved: bool = True,
+    routed_scaling_factor: Optional[float] = None,
+    _flags: int = 0,
+) -> torch.Tensor:
+    """Fused MoE with biases and the swiglu activation on SGLang-layout
+    weights (the computation of ``triton_kernel_fused_experts_with_bias``,
+    ops/fused_moe.py:235-325).
+
+    ``w1`` bf16 ``[E, 2N, K]`` with gate and linear rows interleaved
+    (``interleaved=True``, the layout matmul_ogs's fused swiglu reads) or
+    gate rows then linear rows; ``b1`` ``[E, 2N]`` in the same order;
+    ``w2`` ``[E, K, N]``; ``b2`` ``[E, K]``. Per slot::
+
+        g = x W1g^T + b1g;  u = x W1u^T + b1u
+        g = min(g, limit);  u = clamp(u, -limit, limit)   (when limit given)
+        a = bf16(g * sigmoid(alpha * g) * (u + 1))
+        y = bf16(a W2^T + b2);  out = bf16(sum_j w_j * y_j)
+
+    ``gemm1_alpha`` defaults to 1.0 and no clamp is applied without
+    ``gemm1_clamp_limit``. The router weight multiplies g and u before the
+    activation when ``apply_router_weight_on_input``.
+    """
+    logger.debug("FLAGGEMS_SGLANG FUSED_MOE_WITH_BIAS (gfx950)")
+    assert hidden_states.ndim == 2, "hidden_states must be 2D"
+    assert hidden_states.dtype == torch.bfloat16, "hidden_states must be bfloat16"
+    for name, t in (("hidden_states", hidden_states), ("w1", w1), ("b1", b1),
+                    ("w2", w2), ("b2", b2), ("topk_weights", topk_weights),
+                    ("topk_ids", topk_ids)):
+        _require_gpu(name, t)
+    assert w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16, (
+        "w1 and w2 must be bfloat16")
+    E, two_n, K = w1.shape
+    N = two_n // 2
+    assert hidden_states.shape[1] == K, "hidden size mismatch"
+    assert tuple(w2.shape) == (E, K, N), "intermediate size mismatch"
+    assert tuple(b1.shape) == (E, two_n) and tuple(b2.shape) == (E, K), (
+        "b1 must be [E, 2N] and b2 [E, K]")
+    M = hidden_states.shape[0]
+    assert topk_ids.shape == topk_weights.shape and topk_ids.shape[0] == M, (
+        "topk_ids / topk_weights must be [M, topk]")
+    topk = topk_ids.shape[1]
+    if interleaved:
+        w1 = _cached(_DEINTERLEAVE_CACHE, w1, _deinterleave_rows)
+        b1 = _deinterleave_rows(b1)
+    alpha = 1.0 if gemm1_alpha is None else float(gemm1_alpha)
+    limit = 0.0 if gemm1_clamp_limit is None else float(gemm1_clamp_limit)
+
+    lib = _capi.load()
+    flags = int(_flags)
+    if apply_router_weight_on_input:
+        flags |= _capi.FLAG_ROUTER_WEIGHT_ON_INPUT
+    x = hidden_states.contiguous()
+    w1 = w1.contiguous()
+    w2 = w2.contiguous()
+    b1f = b1.to(torch.float32).contiguous()
+    b2f = b2.to(torch.float32).contiguous()
+    ids = topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights.to(torch.float32).contiguous()
+    ws_bytes = lib.fgs_moe_workspace_bytes(M, K, N, E, topk, _capi.QMODE_BF16, flags)
+    if ws_bytes < 0:
+        _capi.check(lib.fgs_moe_validate(M, K, N, E, topk, _capi.QMODE_BF16,
+                                         flags, 0), "fused_moe_with_bias")
+    out = torch.empty((M, K), dtype=torch.bfloat16, device=x.device)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=x.device)
+    rc = lib.fgs_moe_fused_bf16_bias(
+        x.data_ptr(), w1.data_ptr(), b1f.data_ptr(), w2.data_ptr(),
+        b2f.data_ptr(), wts.data_ptr(), ids.data_ptr(), M, K, N, E, topk, flags,
+        alpha, limit, ws.data_ptr(), ws_bytes, out.data_ptr(), _stream_ptr(x))
+    _capi.check(rc, "fused_moe_with_bias")
+    if routed_scaling_factor is not None and routed_scaling_factor != 1.0:
+        out.mul_(routed_scaling_factor)
+    return out
+
+
+def _uncombined(fn, hidden_states, topk_weights, topk_ids, **kw):
+    """One output row per (token, slot), token-major, slots in the routing
+    order: the op on each token repeated topk times with one slot each."""
     top_k = topk_ids.shape[1]
     rep_x = hidden_states.repeat_interleave(top_k, dim=0)
-    flat_ids = topk_ids.reshape(-1, 1)
-    flat_w = topk_weights.reshape(-1, 1)
-    return fused_moe(rep_x, w13n, w2n, flat_w, flat_ids, activation=activation,
-                     apply_router_weight_on_input=apply_router_weight_on_input)
+    return fn(rep_x, topk_weights.reshape(-1, 1), topk_ids.reshape(-1, 1), **kw)
+
+
+def triton_kernel_fused_experts_with_bias(
+    hidden_states: torch.Tensor,
+    w1: torch.Tensor,
+    w1_pcg,
+    b1: torch.Tensor,
+    w2: torch.Tensor,
+    w2_pcg,
+    b2: torch.Tensor,
+    routing_data,
+    gather_indx,
+    scatter_indx,
+    inplace: bool = False,
+    activation: str = "silu",
+    apply_router_weight_on_input: bool = False,
+    global_num_experts: int = -1,
+    gemm1_alpha: Optional[float] = None,
+    gemm1_clamp_limit: Optional[float] = None,
+) -> torch.Tensor:
+    """Drop-in for the reference's ``triton_kernel_fused_experts_with_bias``
+    (ops/fused_moe.py:235-325): same signature and checks, reference layout
+    ``w1 [E, K, 2N]`` with interleaved gate/linear columns, ``b1 [E, 2N]``,
+    ``w2 [E, N, K]``, ``b2 [E, K]``, reference routing format. bf16 weights
+    only: a precision config (``w1_pcg`` / ``w2_pcg``) is accepted and
+    ignored for bf16 weights. ``scatter_indx=None`` returns un-combined rows.
+    """
+    logger.debug("FLAGGEMS_SGLANG FUSED_MOE_WITH_BIAS (gfx950)")
+    assert inplace is False, "Inplace is not supported"
+    assert hidden_states.dtype == torch.bfloat16, "hidden_states must be bfloat16"
+    if activation != "silu":
+        raise ValueError(f"Unsupported FusedMoe activation: {activation}")
+    assert w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16, (
+        "w1 and w2 must be bfloat16")
+    num_tokens, hidden = hidden_states.shape
+    topk_weights, topk_ids = _routing_to_topk(routing_data, gather_indx,
+                                              num_tokens)
+    w13n = _cached(_TRANSPOSE_DEINTERLEAVE_CACHE, w1,
+                   lambda w: _deinterleave_rows(w.transpose(-1, -2)))
+    b1n = _deinterleave_rows(b1)
+    w2n = _native_layout(w2)
+    kw = dict(apply_router_weight_on_input=apply_router_weight_on_input,
+              gemm1_alpha=gemm1_alpha, gemm1_clamp_limit=gemm1_clamp_limit,
+              interleaved=False)
+
+    def call(x, tw, ti, **k):
+        return fused_moe_with_bias(x, w13n, b1n, w2n, b2, tw, ti, **k)
+
+    if scatter_indx is not None:
+        return call(hidden_states, topk_weights, topk_ids, **kw).view(num_tokens, hidden)
+    return _uncombined(call, hidden_states, topk_weights, topk_ids, **kw)
+
+
+@dataclass
+class StandardCombineInput:
+    """Stand-in for SGLang's ``StandardCombineInput`` (the adapter's return
+    type, ops/fused_moe.py:422) when SGLang is not installed."""
+
+    hidden_states: torch.Tensor
+
+
+def _combine_input_cls():
+    try:
+        from sglang.srt.layers.moe.token_dispatcher.standard import (
+            StandardCombineInput as cls,
+        )
+        return cls
+    except Exception:
+        return StandardCombineInput
+
+
+def fused_moe_flagos(obj, layer, dispatch_output):
+    """SGLang runner adapter (the reference's ``fused_moe_flagos``,
+    ops/fused_moe.py:328-422) on native-layout weights: ``layer.w13_weight``
+    ``[E, 2N, K]`` and ``layer.w2_weight`` ``[E, K, N]`` are used as they are
+    (the reference transposes both on every call, :342-343).
+
+    Reads ``obj.runner.config`` (``num_experts``, ``activation``,
+    ``apply_router_weight_on_input``, ``no_combine``,
+    ``routed_scaling_factor``, ``gemm1_alpha``, ``gemm1_clamp_limit``),
+    optional ``layer.w13_weight_bias`` / ``layer.w2_weight_bias`` (both or
+    neither: the bias variant with interleaved gate/linear rows), and
+    ``dispatch_output.hidden_states`` / ``.topk_output`` (standard
+    ``topk_weights`` / ``topk_ids`` or the triton-kernels routing tuple).
+    ``no_combine`` returns ``[tokens, topk, hidden]``; the routed scaling
+    factor applies to combined outputs only (:408-420).
+    """
+    cfg = obj.runner.config
+    hidden_states = dispatch_output.hidden_states
+    topk_output = dispatch_output.topk_output
+    if isinstance(topk_output, (tuple, list)) and len(topk_output) == 3 and \
+            hasattr(topk_output[0], "gate_scal"):
+        routing_data, gather_indx, _ = topk_output
+        topk_weights, topk_ids = _routing_to_topk(routing_data, gather_indx,
+                                                  hidden_states.shape[0])
+    else:
+        topk_weights, topk_ids = topk_output.topk_weights, topk_output.topk_ids
+    no_combine = bool(getattr(cfg, "no_combine", False))
+    on_input = bool(getattr(cfg, "apply_router_weight_on_input", False))
+    activation = getattr(cfg, "activation", "silu")
+    b13 = getattr(layer, "w13_weight_bias", None)
+    b2 = getattr(layer, "w2_weight_bias", None)
+    if b13 is not None or b2 is not None:
+        assert b13 is not None and b2 is not None, (
+            "Bias execution requires both w13_bias and w2_bias")
+        if activation != "silu":
+            raise ValueError(f"Unsupported FusedMoe activation: {activation}")
+        w13 = _cached(_DEINTERLEAVE_CACHE, layer.w13_weight, _deinterleave_rows)
+        b13n = _deinterleave_rows(b13)
+
+        def call(x, tw, ti):
+            return fused_moe_with_bias(
+                x, w13, b13n, layer.w2_weight, b2, tw, ti,
+                apply_router_weight_on_input=on_input,
+                gemm1_alpha=getattr(cfg, "gemm1_alpha", None),
+                gemm1_clamp_limit=getattr(cfg, "gemm1_clamp_limit", None),
+                interleaved=False)
+    else:
+        def call(x, tw, ti):
+            return fused_moe(x, layer.w13_weight, layer.w2_weight, tw, ti,
+                             activation=activation,
+                             apply_router_weight_on_input=on_input)
+    if no_combine:
+        rows = _uncombined(call, hidden_states, topk_weights, topk_ids)
+        output = rows.view(hidden_states.shape[0], topk_ids.shape[1],
+                           hidden_states.shape[-1])
+    else:
+        output = call(hidden_states, topk_weights, topk_ids)
+        scale = getattr(cfg, "routed_scaling_factor", None)
+        if scale is not None and scale != 1.0:
+            output.mul_(scale)
+    return _combine_input_cls()(hidden_states=output)
 
 
 __all__ = [
     "fused_moe",
+    "fused_moe_with_bias",
+    "fused_moe_flagos",
     "triton_kernel_fused_experts",
+    "triton_kernel_fused_experts_with_bias",
     "moe_align_block_size",
     "silu_and_mul",
     "moe_sum",

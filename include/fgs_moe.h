@@ -46,6 +46,9 @@ extern "C" {
 
 /* `flags` bits of the fused entry points. */
 #define FGS_FLAG_ROUTER_WEIGHT_ON_INPUT 0x1 /* gammas on GEMM1 output rows */
+/* GEMM1 activation gelu(gate) * up (exact erf gelu, sgl_kernel's
+ * gelu_and_mul, ops/fused_moe.py:219-220) instead of silu(gate) * up */
+#define FGS_FLAG_ACT_GELU 0x2
 #define FGS_FLAG_FORCE_DECODE 0x100         /* schedule: streaming kernels  */
 #define FGS_FLAG_FORCE_PREFILL 0x200        /* schedule: LDS-tiled kernels  */
 /* schedule: LDS-tiled kernels with row-block configuration c (0: 256 rows,
@@ -146,6 +149,27 @@ int32_t fgs_moe_fused_bf16(const void* x, const void* w13, const void* w2,
                            int32_t num_experts, int32_t topk, int32_t flags,
                            void* workspace, int64_t ws_bytes, void* out,
                            void* stream);
+
+/* Fused MoE with biases and the swiglu activation, bf16. Replaces
+ * triton_kernel_fused_experts_with_bias (ops/fused_moe.py:235-325):
+ * GEMM1 with bias b1 and swiglu fused (matmul_ogs(..., bias=b1,
+ * fused_activation=swiglu, :303-313)), GEMM2 with bias b2 (:315-323), top-k
+ * gammas and sum.
+ *   w13 bf16 [E, 2*inter, hidden] (gate rows 0..inter-1, then linear rows:
+ *       the reference's interleaved columns de-interleaved once by the caller)
+ *   b13 f32 [E, 2*inter] (same row order), b2 f32 [E, hidden]
+ *   a = bf16(g * sigmoid(alpha*g) * (u + 1)) with g = x W13g^T + b13g,
+ *   u = x W13u^T + b13u and, for limit > 0, g = min(g, limit),
+ *   u = clamp(u, -limit, limit); y = bf16(a W2^T + b2); out = bf16(sum_j w_j y_j).
+ * FGS_FLAG_ACT_GELU is rejected (the reference raises for non-silu,
+ * :280-283). */
+int32_t fgs_moe_fused_bf16_bias(const void* x, const void* w13, const float* b13,
+                                const void* w2, const float* b2,
+                                const float* topk_weights, const int32_t* topk_ids,
+                                int64_t m, int64_t hidden, int64_t inter,
+                                int32_t num_experts, int32_t topk, int32_t flags,
+                                float alpha, float limit, void* workspace,
+                                int64_t ws_bytes, void* out, void* stream);
 
 /* Fused MoE, fp8 w8a8 with block scales (block_n = block_k = 128).
  *   w13 e4m3fn [E, 2*inter, hidden], w13_scale f32 [E, 2*inter/128, hidden/128]

@@ -11,7 +11,11 @@ It restates, on the CPU in torch fp32 (plus the C alignment in
   (reference tests/test_fused_moe.py:37-41);
 * alignment: stable expert grouping (src/flaggems_sglang/ops/fused_moe.py:
   130-139), via ``align_ref.c``;
-* ``silu_and_mul`` (ops/fused_moe.py:44-63, fp32 math, bf16 store);
+* ``silu_and_mul`` (ops/fused_moe.py:44-63, fp32 math, bf16 store), the
+  erf ``gelu_and_mul`` (:219-220) and the bias variant's fused swiglu
+  (:274-314; triton_kernels / sgl_kernel are not in the image, their
+  published formulas are restated -- parity of those two is pinned by
+  closed forms and library identities only);
 * the fused expert computation (ops/fused_moe.py:197-232) with the rounding
   points of an unfused pipeline: GEMM1 output rounded to bf16, activation
   rounded to bf16, GEMM2 output rounded to bf16, fp32 weighted top-k sum
@@ -110,6 +114,33 @@ def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
     return (g / (1.0 + torch.exp(-g)) * u).to(torch.bfloat16)
 
 
+def gelu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    """bf16(gelu(f32 gate) * f32 up) over x = [gate | up] with the exact
+    gelu 0.5*g*(1 + erf(g/sqrt(2))): sgl_kernel's gelu_and_mul, which the
+    reference calls for activation="gelu" (ops/fused_moe.py:219-220; the
+    function is not in this image, its published formula is restated)."""
+    n = x.shape[-1] // 2
+    g = x[..., :n].float()
+    u = x[..., n:].float()
+    return (0.5 * g * (1.0 + torch.erf(g * 0.7071067811865476)) * u).to(torch.bfloat16)
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor, alpha: float = 1.0,
+           limit: float = 0.0) -> torch.Tensor:
+    """The swiglu the bias variant fuses into matmul_ogs
+    (ops/fused_moe.py:274-314, triton_kernels.swiglu.swiglu_fn with
+    gemm1_alpha / gemm1_clamp_limit; not in this image -- the published
+    GPT-OSS formula is restated): with limit > 0, g = min(g, limit) and
+    u = clamp(u, -limit, limit); out = g * sigmoid(alpha*g) * (u + 1), fp32
+    in, fp32 out (the caller rounds)."""
+    g = g.float()
+    u = u.float()
+    if limit > 0:
+        g = torch.clamp(g, max=limit)
+        u = torch.clamp(u, min=-limit, max=limit)
+    return g * torch.sigmoid(alpha * g) * (u + 1.0)
+
+
 def moe_sum(y: torch.Tensor) -> torch.Tensor:
     """[M, k, K] -> bf16(fp32 sum over k)."""
     return y.float().sum(dim=1).to(torch.bfloat16)
@@ -204,7 +235,9 @@ def fused_moe(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
               w2_scale: Optional[torch.Tensor] = None,
               apply_router_weight_on_input: bool = False,
               tokens: Optional[Sequence[int]] = None,
-              return_mag: bool = False):
+              return_mag: bool = False, activation: str = "silu",
+              b1: Optional[torch.Tensor] = None, b2: Optional[torch.Tensor] = None,
+              alpha: float = 1.0, limit: float = 0.0):
     """Reference fused MoE on CPU tensors (SGLang layout: w1 [E, 2N, K],
     w2 [E, K, N]). Returns bf16 [len(tokens), K] (all tokens by default);
     with ``return_mag`` also the fp32 magnitude sum_j |w_j| * (|y_j| + q_j)
@@ -222,6 +255,12 @@ def fused_moe(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
 
     Every token's output depends only on its own row and routing, so any
     subset of tokens can be checked exactly at full layer size.
+
+    ``activation``: "silu" or "gelu" (unfused pipeline, GEMM1 output rounded
+    to bf16 first), or "swiglu" -- the bias variant (ops/fused_moe.py:
+    235-325): GEMM1 + ``b1`` [E, 2N] (gate rows then linear rows, like w1)
+    with swiglu(alpha, limit) fused (no bf16 rounding before it), GEMM2 +
+    ``b2`` [E, K].
     """
     x = x.cpu()
     topk_weights = topk_weights.cpu().float()
@@ -247,12 +286,22 @@ def fused_moe(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
         rows, slots = torch.nonzero(ids == e, as_tuple=True)
         w13e, w2e = _expert_weights(mode, w1, w2, w1_scale, w2_scale, e)
         h = xq[rows] @ w13e.t()
+        if b1 is not None:
+            h = h + b1[e].cpu().float()
         if apply_router_weight_on_input:
             h = h * wts[rows, slots][:, None]
-        h = h.to(torch.bfloat16)
-        a = silu_and_mul(h)
+        if activation == "swiglu":
+            n = h.shape[1] // 2
+            a = swiglu(h[:, :n], h[:, n:], alpha, limit).to(torch.bfloat16)
+        elif activation == "gelu":
+            a = gelu_and_mul(h.to(torch.bfloat16))
+        else:
+            a = silu_and_mul(h.to(torch.bfloat16))
         aq = _quant_dequant_act(mode, a)
-        ye = (aq @ w2e.t()).to(torch.bfloat16).float()
+        ye = aq @ w2e.t()
+        if b2 is not None:
+            ye = ye + b2[e].cpu().float()
+        ye = ye.to(torch.bfloat16).float()
         y[rows, slots] = ye
         if return_mag and mode != "bf16":
             q[rows, slots] = (aq.abs() @ w2e.abs().t()) * 2.0 ** -2

@@ -116,6 +116,18 @@ def test_entry_points_reject_bad_arguments_before_launch():
     rc = lib.fgs_moe_fused_int8_channel(nul, nul, nul, nul, nul, nul, nul, 4,
                                         256, 256, 4, 2, 0, nul, 0, nul, nul)
     assert rc == -1 and "workspace" in _capi.last_error()
+    # bias variant: swiglu only, both biases, no NaN parameters
+    rc = lib.fgs_moe_fused_bf16_bias(nul, nul, nul, nul, nul, nul, nul, 4, 256, 128,
+                                     4, 2, _capi.FLAG_ACT_GELU, 1.0, 0.0, nul, need,
+                                     nul, nul)
+    assert rc == -2 and "swiglu" in _capi.last_error()
+    rc = lib.fgs_moe_fused_bf16_bias(nul, nul, nul, nul, nul, nul, nul, 4, 256, 128,
+                                     4, 2, 0, 1.0, 0.0, nul, need, nul, nul)
+    assert rc == -1 and "b13 and b2" in _capi.last_error()
+    rc = lib.fgs_moe_fused_bf16_bias(nul, nul, 16, nul, 16, nul, nul, 4, 256, 128,
+                                     4, 2, 0, float("nan"), 0.0, nul, need, nul, nul)
+    assert rc == -1 and "NaN" in _capi.last_error()
+    assert lib.fgs_moe_validate(4, 256, 128, 4, 2, 0, _capi.FLAG_ACT_GELU, need) == 0
 
 
 def test_error_codes_map_to_python_exceptions():
@@ -180,6 +192,13 @@ def test_unsupported_flags_keep_reference_messages():
         fused_moe(x, w1, w2, tw, ti, inplace=True)
     with pytest.raises(ValueError, match="Unsupported FusedMoe activation"):
         fused_moe(x, w1, w2, tw, ti, activation="relu")
+    from flaggems_sglang import triton_kernel_fused_experts_with_bias
+    with pytest.raises(ValueError, match="Unsupported FusedMoe activation"):
+        triton_kernel_fused_experts_with_bias(x, w1, None, None, w2, None, None,
+                                              None, None, None, activation="gelu")
+    with pytest.raises(AssertionError, match="Inplace is not supported"):
+        triton_kernel_fused_experts_with_bias(x, w1, None, None, w2, None, None,
+                                              None, None, None, inplace=True)
     with pytest.raises(AssertionError, match="use_fp8_w8a8 is not supported"):
         triton_kernel_fused_experts(x, w1, w2, None, None, None, use_fp8_w8a8=True)
     with pytest.raises(AssertionError, match="block_shape is not supported"):

@@ -166,6 +166,132 @@ def test_quantised_schedules_agree(gpu, mode):
     _check(pre.cpu()[toks], ref, mode, f"{mode} prefill")
 
 
+# ------------------------------------------------- activations and biases ---
+_SCHEDS = [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL]
+
+
+@pytest.mark.parametrize("sched", _SCHEDS, ids=["decode", "prefill"])
+@pytest.mark.parametrize("shape", [(5, 256, 128, 4, 2), (600, 512, 384, 8, 2)])
+def test_gelu_activation(gpu, shape, sched):
+    """activation="gelu": exact-erf gelu(gate) * up in GEMM1's epilogue
+    (sgl_kernel gelu_and_mul, ops/fused_moe.py:219-220)."""
+    M, K, N, E, topk = shape
+    x, w1, w2, w, ids = _ref_inputs(M, K, N, E, topk, gpu)
+    res = fm.fused_moe(x, w1, w2, w, ids, activation="gelu", _flags=sched)
+    toks = _sample(M, 48)
+    ref = moe_ref.fused_moe(x, w1, w2, w, ids, tokens=toks, return_mag=True,
+                            activation="gelu")
+    _check(res.cpu()[toks], ref, "bf16", f"gelu {shape}")
+    # the reference-signature entry point takes the same activation
+    routing, gather, scatter = flaggems_sglang.standard_topk_to_routing(w, ids, E)
+    res2 = flaggems_sglang.triton_kernel_fused_experts(
+        x, w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous(),
+        routing, gather, scatter, activation="gelu")
+    _check(res2.cpu()[toks], ref, "bf16", f"gelu compat {shape}")
+
+
+def _interleave_rows(w):
+    """[gate block | linear block] rows -> g0, u0, g1, u1, ... (the layout
+    matmul_ogs's fused swiglu reads)."""
+    n = w.shape[-2] // 2 if w.ndim == 3 else w.shape[-1] // 2
+    if w.ndim == 2:
+        return torch.stack([w[:, :n], w[:, n:]], dim=2).reshape(w.shape)
+    return torch.stack([w[:, :n], w[:, n:]], dim=2).reshape(w.shape)
+
+
+def _bias_inputs(M, K, N, E, topk, device):
+    x, w1, w2, w, ids = _ref_inputs(M, K, N, E, topk, device)
+    g = torch.Generator(device=device).manual_seed(M + 1)
+    b1 = torch.randn(E, 2 * N, generator=g, device=device) * 0.5
+    b2 = torch.randn(E, K, generator=g, device=device) * 0.5
+    return x, w1, w2, b1, b2, w, ids
+
+
+@pytest.mark.parametrize("on_input", [False, True], ids=["gammas_out", "gammas_in"])
+@pytest.mark.parametrize("sched", _SCHEDS, ids=["decode", "prefill"])
+@pytest.mark.parametrize("shape", [(7, 256, 128, 4, 2), (500, 512, 256, 8, 2)])
+def test_bias_swiglu(gpu, shape, sched, on_input):
+    """Bias variant (ops/fused_moe.py:235-325): GEMM1 + b1 with swiglu(alpha,
+    limit) fused, GEMM2 + b2, on interleaved gate/linear rows."""
+    M, K, N, E, topk = shape
+    x, w1, w2, b1, b2, w, ids = _bias_inputs(M, K, N, E, topk, gpu)
+    res = fm.fused_moe_with_bias(x, _interleave_rows(w1), _interleave_rows(b1), w2,
+                                 b2, w, ids, apply_router_weight_on_input=on_input,
+                                 gemm1_alpha=1.702, gemm1_clamp_limit=7.0,
+                                 _flags=sched)
+    toks = _sample(M, 48)
+    ref = moe_ref.fused_moe(x, w1, w2, w, ids, tokens=toks, return_mag=True,
+                            activation="swiglu", b1=b1, b2=b2, alpha=1.702,
+                            limit=7.0, apply_router_weight_on_input=on_input)
+    _check(res.cpu()[toks], ref, "bf16", f"bias swiglu {shape}")
+
+
+def test_bias_reference_signature(gpu):
+    """triton_kernel_fused_experts_with_bias with the reference's layouts
+    (w1 [E, K, 2N] interleaved columns, w2 [E, N, K]) and routing format;
+    scatter_indx=None returns the un-combined rows."""
+    M, K, N, E, topk = 64, 256, 128, 8, 2
+    x, w1, w2, b1, b2, w, ids = _bias_inputs(M, K, N, E, topk, gpu)
+    w1_ref = _interleave_rows(w1).transpose(1, 2).contiguous()
+    w2_ref = w2.transpose(1, 2).contiguous()
+    routing, gather, scatter = flaggems_sglang.standard_topk_to_routing(w, ids, E)
+    res = flaggems_sglang.triton_kernel_fused_experts_with_bias(
+        x, w1_ref, None, _interleave_rows(b1), w2_ref, None, b2, routing, gather,
+        scatter, gemm1_alpha=1.702, gemm1_clamp_limit=7.0)
+    ref = moe_ref.fused_moe(x, w1, w2, w, ids, return_mag=True, activation="swiglu",
+                            b1=b1, b2=b2, alpha=1.702, limit=7.0)
+    _check(res.cpu(), ref, "bf16", "bias compat")
+    rows = flaggems_sglang.triton_kernel_fused_experts_with_bias(
+        x, w1_ref, None, _interleave_rows(b1), w2_ref, None, b2, routing, gather,
+        None, gemm1_alpha=1.702, gemm1_clamp_limit=7.0)
+    assert rows.shape == (M * topk, K)
+    _check(rows.view(M, topk, K).float().sum(1).to(torch.bfloat16).cpu(), ref,
+           "bf16", "bias compat uncombined")
+    with pytest.raises(ValueError, match="Unsupported FusedMoe activation"):
+        flaggems_sglang.triton_kernel_fused_experts_with_bias(
+            x, w1_ref, None, b1, w2_ref, None, b2, routing, gather, scatter,
+            activation="gelu")
+
+
+class _NS:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+@pytest.mark.parametrize("variant", ["standard", "routing_tuple", "no_combine", "bias"])
+def test_fused_moe_flagos_adapter(gpu, variant):
+    """The SGLang runner adapter (ops/fused_moe.py:328-422) on native-layout
+    layer weights, duck-typed runner config / layer / dispatch output."""
+    M, K, N, E, topk = 40, 256, 128, 8, 2
+    x, w1, w2, b1, b2, w, ids = _bias_inputs(M, K, N, E, topk, gpu)
+    cfg = _NS(num_experts=E, activation="silu", apply_router_weight_on_input=False,
+              no_combine=variant == "no_combine", routed_scaling_factor=2.0,
+              gemm1_alpha=1.702, gemm1_clamp_limit=7.0)
+    obj = _NS(runner=_NS(config=cfg))
+    layer = _NS(w13_weight=w1, w2_weight=w2)
+    if variant == "bias":
+        layer = _NS(w13_weight=_interleave_rows(w1), w2_weight=w2,
+                    w13_weight_bias=_interleave_rows(b1), w2_weight_bias=b2)
+    topk_output = _NS(topk_weights=w, topk_ids=ids)
+    if variant == "routing_tuple":
+        topk_output = flaggems_sglang.standard_topk_to_routing(w, ids, E)
+    out = fm.fused_moe_flagos(obj, layer, _NS(hidden_states=x, topk_output=topk_output))
+    res = out.hidden_states
+    if variant == "bias":
+        ref, mag = moe_ref.fused_moe(x, w1, w2, w, ids, return_mag=True,
+                                     activation="swiglu", b1=b1, b2=b2, alpha=1.702,
+                                     limit=7.0)
+    else:
+        ref, mag = moe_ref.fused_moe(x, w1, w2, w, ids, return_mag=True)
+    if variant == "no_combine":
+        assert res.shape == (M, topk, K)
+        _check(res.float().sum(1).to(torch.bfloat16).cpu(), (ref, mag), "bf16",
+               "flagos no_combine")
+    else:
+        _check(res.cpu(), ((ref.float() * 2.0).to(torch.bfloat16), mag * 2.0), "bf16",
+               f"flagos {variant}")
+
+
 def test_dropped_slots_and_routed_scaling(gpu):
     x, w1, w2, w, ids = _ref_inputs(16, 256, 128, 4, 2, gpu)
     ids2 = ids.clone()

@@ -194,8 +194,10 @@ def test_weight_quantisers():
 
 
 # ------------------------------------------------------------- fused MoE ---
-def _brute_force_moe(x, w1, w2, tw, tid):
-    """Token-by-token float64 MoE (no intermediate rounding)."""
+def _brute_force_moe(x, w1, w2, tw, tid, act="silu", b1=None, b2=None,
+                     alpha=1.0, limit=0.0):
+    """Token-by-token float64 MoE (no intermediate rounding); activations
+    written from their textbook definitions with math.erf / exp."""
     x = x.double().numpy()
     w1 = w1.double().numpy()
     w2 = w2.double().numpy()
@@ -205,9 +207,22 @@ def _brute_force_moe(x, w1, w2, tw, tid):
         for j in range(tid.shape[1]):
             e = int(tid[t, j])
             h = w1[e] @ x[t]
+            if b1 is not None:
+                h = h + b1[e].double().numpy()
             gte, up = h[:N], h[N:]
-            a = gte / (1.0 + np.exp(-gte)) * up
-            out[t] += float(tw[t, j]) * (w2[e] @ a)
+            if act == "gelu":
+                a = np.array([0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))) for v in gte]) * up
+            elif act == "swiglu":
+                if limit > 0:
+                    gte = np.minimum(gte, limit)
+                    up = np.clip(up, -limit, limit)
+                a = gte / (1.0 + np.exp(-alpha * gte)) * (up + 1.0)
+            else:
+                a = gte / (1.0 + np.exp(-gte)) * up
+            y = w2[e] @ a
+            if b2 is not None:
+                y = y + b2[e].double().numpy()
+            out[t] += float(tw[t, j]) * y
     return out
 
 
@@ -227,6 +242,58 @@ def test_moe_matches_float64_brute_force(M, K, N, E, k):
     want = _brute_force_moe(x, w1, w2, w, ids)
     # three bf16 roundings on the way (h, a, y) plus the output rounding
     assert np.allclose(got, want, rtol=3e-2, atol=3e-2 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("act", ["gelu", "swiglu"])
+def test_moe_activations_and_biases_match_float64_brute_force(act):
+    M, K, N, E, k = 7, 64, 32, 4, 2
+    x, w1, w2, w, ids = _inputs(M, K, N, E, k, seed=21)
+    g = torch.Generator().manual_seed(22)
+    b1 = b2 = None
+    kw = {}
+    if act == "swiglu":
+        b1 = torch.randn(E, 2 * N, generator=g) * 0.5
+        b2 = torch.randn(E, K, generator=g) * 0.5
+        kw = dict(alpha=1.702, limit=1.5)  # a limit the activations do reach
+    got = moe_ref.fused_moe(x, w1, w2, w, ids, activation=act, b1=b1, b2=b2,
+                            **kw).double().numpy()
+    want = _brute_force_moe(x, w1, w2, w, ids, act=act, b1=b1, b2=b2, **kw)
+    assert np.allclose(got, want, rtol=3e-2, atol=3e-2 * np.abs(want).max())
+
+
+def test_gelu_and_mul_closed_form():
+    g = torch.Generator().manual_seed(4)
+    x = (torch.randn(32, 128, generator=g) * 3).to(torch.bfloat16)
+    got = moe_ref.gelu_and_mul(x).double().numpy()
+    xd = x.double().numpy()
+    gd, ud = xd[:, :64], xd[:, 64:]
+    want = 0.5 * gd * (1.0 + np.vectorize(math.erf)(gd / math.sqrt(2.0))) * ud
+    # one bf16 rounding, plus fp32 cancellation in 1 + erf(g) for g << 0
+    # (absolute, at most an fp32 ulp of 1 times |g * u|)
+    assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 2.0 ** -22 * np.abs(gd * ud))
+    # gelu(1) = Phi(1) = 0.8413447460685429; gelu(0) = 0; gelu(-6) ~ 0
+    t = torch.tensor([[1.0, 0.0, -6.0, 1.0, 5.0, 5.0]], dtype=torch.bfloat16)
+    o = moe_ref.gelu_and_mul(t).float()[0]
+    assert abs(o[0] - 0.8413447460685429) < 4e-3 and o[1] == 0.0 and abs(o[2]) < 1e-7
+
+
+def test_swiglu_identities():
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(1000, generator=g) * 4
+    b = torch.randn(1000, generator=g) * 4
+    # alpha = 1, no clamp: silu(g) * (u + 1) (torch library silu)
+    assert torch.allclose(moe_ref.swiglu(a, b),
+                          torch.nn.functional.silu(a) * (b + 1), rtol=1e-6, atol=1e-6)
+    # alpha = 1.702: g * sigmoid(1.702 g), the GPT-OSS gate
+    assert torch.allclose(moe_ref.swiglu(a, b, alpha=1.702),
+                          a * torch.sigmoid(1.702 * a) * (b + 1), rtol=1e-6, atol=1e-6)
+    # limit clamps the gate from above only and the linear part both ways
+    o = moe_ref.swiglu(torch.tensor([10.0, -10.0, 3.0]), torch.tensor([-10.0, 10.0, 0.0]),
+                       alpha=1.0, limit=7.0)
+    want = [7.0 * (1 / (1 + math.exp(-7.0))) * (-6.0),
+            -10.0 * (1 / (1 + math.exp(10.0))) * 8.0,
+            3.0 * (1 / (1 + math.exp(-3.0)))]
+    assert np.allclose(o.numpy(), want, rtol=1e-6)
 
 
 def test_moe_top1_unit_weight_is_plain_mlp():

@@ -445,6 +445,24 @@ int32_t fgs_moe_sum(const void* in, void* out, int64_t m, int32_t topk,
   return launch_moe_sum(in, out, m, topk, k, as_stream(stream));
 }
 
+int32_t fgs_moe_topk_gating(const void* logits, int32_t logits_bf16, int64_t m,
+                            int32_t num_experts, int32_t topk, int32_t scoring,
+                            int32_t renormalize, float* topk_weights,
+                            int32_t* topk_ids, void* stream) {
+  if (m < 0) return fail(FGS_EINVAL, "m must be >= 0");
+  if (num_experts < 1 || num_experts > 1024)
+    return fail(FGS_EINVAL, "num_experts must be in [1, 1024]");
+  if (topk < 1 || topk > num_experts || topk > 64)
+    return fail(FGS_EINVAL, "topk must be in [1, min(num_experts, 64)]");
+  if (scoring != FGS_SCORING_SOFTMAX && scoring != FGS_SCORING_SIGMOID)
+    return fail(FGS_EINVAL, "unknown scoring function");
+  if (m > 0 && (!logits || !topk_weights || !topk_ids))
+    return fail(FGS_EINVAL, "null pointer argument");
+  return launch_topk_gating(logits, logits_bf16 != 0, m, num_experts, topk,
+                            scoring == FGS_SCORING_SIGMOID, renormalize != 0,
+                            topk_weights, topk_ids, as_stream(stream));
+}
+
 int32_t fgs_moe_quant_fp8_group(const void* x, void* q, float* scales,
                                 int64_t rows, int64_t cols, int32_t group,
                                 void* stream) {

@@ -38,6 +38,13 @@ struct GemmParams {
   const float* bias;      // fp32 per expert: GEMM1 [E, 2N] (gate | up), GEMM2 [E, K]; or null
 };
 
+// Router gating (scores -> top-k -> renormalise), one wave per token;
+// num_experts <= 1024, topk <= min(num_experts, 64).
+int launch_topk_gating(const void* logits, bool bf16_in, int64_t m,
+                       int num_experts, int topk, bool sigmoid,
+                       bool renormalize, float* w_out, int32_t* id_out,
+                       hipStream_t stream);
+
 size_t align_smem_bytes(int num_experts);
 int launch_align(const int32_t* ids, int64_t numel, int num_experts,
                  int block_size, int32_t* sorted_ids, int32_t* expert_ids,

@@ -20,6 +20,9 @@ QMODE_BF16 = 0
 QMODE_FP8_BLOCK = 1
 QMODE_INT8_CHANNEL = 2
 
+SCORING_SOFTMAX = 0
+SCORING_SIGMOID = 1
+
 FLAG_ROUTER_WEIGHT_ON_INPUT = 0x1
 FLAG_ACT_GELU = 0x2
 FLAG_FORCE_DECODE = 0x100
@@ -49,6 +52,10 @@ SIGNATURES = {
     ),
     "fgs_moe_silu_and_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "fgs_moe_sum": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _i64, _c_void_p]),
+    "fgs_moe_topk_gating": (
+        _i32, [_c_void_p, _i32, _i64, _i32, _i32, _i32, _i32, _c_void_p, _c_void_p,
+               _c_void_p]
+    ),
     "fgs_moe_quant_fp8_group": (
         _i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]
     ),

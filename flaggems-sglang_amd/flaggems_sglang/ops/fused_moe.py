@@ -128,6 +128,41 @@ def _routing_to_topk(routing_data, gather_indx, num_tokens):
     return wts.view(num_tokens, top_k), ids.view(num_tokens, top_k)
 
 
+def fused_topk(hidden_states: torch.Tensor, gating_output: torch.Tensor,
+               topk: int, renormalize: bool = True,
+               scoring_func: str = "softmax"):
+    """Router gating on the GPU (HIP kernel, one wave per token): scores
+    (softmax or sigmoid of ``gating_output [M, E]``, fp32 or bf16), top-k
+    experts ranked by logit (ties: lower id), weights = their scores,
+    renormalised to sum 1 when ``renormalize``. Returns ``(topk_weights f32
+    [M, topk], topk_ids int32 [M, topk])`` -- the routing the reference's
+    tests build with torch ops (tests/test_fused_moe.py:37-41)."""
+    _require_gpu("gating_output", gating_output)
+    assert gating_output.ndim == 2, "gating_output must be [M, E]"
+    assert hidden_states.shape[0] == gating_output.shape[0], "token count mismatch"
+    if scoring_func == "softmax":
+        scoring = _capi.SCORING_SOFTMAX
+    elif scoring_func == "sigmoid":
+        scoring = _capi.SCORING_SIGMOID
+    else:
+        raise ValueError(f"Unsupported scoring function: {scoring_func}")
+    logits = gating_output
+    if logits.dtype not in (torch.float32, torch.bfloat16):
+        logits = logits.float()
+    logits = logits.contiguous()
+    M, E = logits.shape
+    w = torch.empty((M, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((M, topk), dtype=torch.int32, device=logits.device)
+    _capi.check(
+        _capi.load().fgs_moe_topk_gating(
+            logits.data_ptr(), 1 if logits.dtype == torch.bfloat16 else 0, M, E,
+            topk, scoring, 1 if renormalize else 0, w.data_ptr(), ids.data_ptr(),
+            _stream_ptr(logits)),
+        "fused_topk",
+    )
+    return w, ids
+
+
 # ------------------------------------------------------------ small ops ---
 def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int,
                          block_size: int):
@@ -688,6 +723,7 @@ def fused_moe_flagos(obj, layer, dispatch_output):
 
 
 __all__ = [
+    "fused_topk",
     "fused_moe",
     "fused_moe_with_bias",
     "fused_moe_flagos",

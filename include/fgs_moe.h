@@ -99,6 +99,23 @@ int32_t fgs_moe_silu_and_mul(const void* in, void* out, int64_t rows,
 int32_t fgs_moe_sum(const void* in, void* out, int64_t m, int32_t topk,
                     int64_t k, void* stream);
 
+/* Router gating: scores -> top-k -> optional renormalisation, producing
+ * the (topk_weights, topk_ids) the fused entry points consume. Replaces the
+ * torch routing of the reference's tests (tests/test_fused_moe.py:37-41:
+ * softmax, topk, renormalise) that feeds _standard_topk_to_triton_kernels
+ * (ops/fused_moe.py:119-146); sigmoid scoring for DeepSeek-style routers.
+ *   logits  f32 or bf16 (logits_bf16 != 0) [m, num_experts], num_experts <= 1024
+ *   topk_weights f32 [m, topk], topk_ids int32 [m, topk], topk <= 64
+ * Experts are ranked by logit (descending; equal logits: lower id first) and
+ * written in rank order; weights are the scores, divided by their top-k sum
+ * when renormalize != 0. */
+#define FGS_SCORING_SOFTMAX 0
+#define FGS_SCORING_SIGMOID 1
+int32_t fgs_moe_topk_gating(const void* logits, int32_t logits_bf16, int64_t m,
+                            int32_t num_experts, int32_t topk, int32_t scoring,
+                            int32_t renormalize, float* topk_weights,
+                            int32_t* topk_ids, void* stream);
+
 /* Dynamic per-(row, group) fp8 quantisation: x bf16 [rows, cols],
  * q e4m3fn [rows, cols], scales f32 [rows, cols / group] with
  * scale = max(amax, 1e-10) / 448 and q = e4m3fn(clamp(x / scale, +-448)).

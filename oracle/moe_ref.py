@@ -86,6 +86,24 @@ def route(logits: torch.Tensor, topk: int, scoring: str = "softmax",
     return w.float(), ids.to(torch.int32)
 
 
+def topk_gating(logits: torch.Tensor, topk: int, scoring: str = "softmax",
+                renormalize: bool = True):
+    """The gating kernel's contract: scores = softmax / sigmoid of the fp32
+    logits; the top-k experts ranked by logit descending with equal logits
+    in ascending id order (a stable descending sort), in rank order; weights
+    = their scores, divided by the top-k sum when ``renormalize``. Ranking
+    the logits selects the same experts as ranking the scores (both maps are
+    monotonic) -- what :func:`route` / the reference's tests do with
+    torch.topk -- but leaves no rounding ties."""
+    logits = logits.float()
+    ids = torch.sort(logits, dim=-1, descending=True, stable=True).indices[:, :topk]
+    scores = torch.softmax(logits, dim=-1) if scoring == "softmax" else torch.sigmoid(logits)
+    w = torch.gather(scores, 1, ids)
+    if renormalize:
+        w = w / w.sum(dim=-1, keepdim=True)
+    return w.float(), ids.to(torch.int32)
+
+
 # ------------------------------------------------------------- alignment ---
 def align(topk_ids, num_experts: int, block_size: int):
     """Stable block-padded expert grouping (C restatement in align_ref.c).

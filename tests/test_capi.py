@@ -101,6 +101,13 @@ def test_entry_points_reject_bad_arguments_before_launch():
     assert lib.fgs_moe_align_block_size(nul, 8, 4, 16, nul, nul, nul, 10, nul) == -1
     assert "max_padded" in _capi.last_error()
     assert lib.fgs_moe_align_block_size(nul, 8, 0, 16, nul, nul, nul, 100, nul) == -1
+    assert lib.fgs_moe_topk_gating(nul, 0, 4, 8, 9, 0, 1, nul, nul, nul) == -1
+    assert "topk" in _capi.last_error()
+    assert lib.fgs_moe_topk_gating(nul, 0, 4, 2000, 2, 0, 1, nul, nul, nul) == -1
+    assert lib.fgs_moe_topk_gating(nul, 0, 4, 8, 2, 5, 1, nul, nul, nul) == -1
+    assert lib.fgs_moe_topk_gating(nul, 0, 4, 8, 2, 0, 1, nul, nul, nul) == -1
+    assert "null pointer" in _capi.last_error()
+    assert lib.fgs_moe_topk_gating(nul, 0, 0, 8, 2, 0, 1, nul, nul, nul) == 0
     assert lib.fgs_moe_silu_and_mul(nul, nul, 4, 12, nul) == -2
     assert lib.fgs_moe_silu_and_mul(nul, nul, 4, 16, nul) == -1  # null pointers
     assert lib.fgs_moe_sum(nul, nul, 4, 0, 16, nul) == -1
@@ -163,7 +170,8 @@ def test_registry_surface():
 
     names = flaggems_sglang.all_registered_ops()
     for n in ("fused_moe", "triton_kernel_fused_experts", "moe_align_block_size",
-              "silu_and_mul", "moe_sum"):
+              "silu_and_mul", "moe_sum", "fused_topk", "fused_moe_flagos",
+              "triton_kernel_fused_experts_with_bias"):
         assert n in names
         assert getattr(flaggems_sglang, n) is flaggems_sglang.get_op(n)
     assert flaggems_sglang.get_op("nope") is None

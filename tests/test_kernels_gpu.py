@@ -132,3 +132,45 @@ def test_quant_int8_token_bit_exact(gpu, rows, cols):
     rq, rsc = moe_ref.quant_int8_token(x)
     assert torch.equal(s.cpu(), rsc)
     assert torch.equal(q.cpu(), rq)
+
+
+# ----------------------------------------------------------------- gating ---
+@pytest.mark.parametrize("M,E,k,scoring,dtype,renorm", [
+    (1, 8, 2, "softmax", torch.float32, True),
+    (333, 8, 2, "softmax", torch.float32, True),
+    (257, 128, 8, "softmax", torch.bfloat16, True),
+    (100, 256, 8, "sigmoid", torch.float32, True),
+    (64, 1024, 16, "softmax", torch.float32, False),
+    (17, 60, 64 - 4, "sigmoid", torch.bfloat16, False),
+    (0, 16, 4, "softmax", torch.float32, True),
+])
+def test_topk_gating(gpu, M, E, k, scoring, dtype, renorm):
+    """ids bit-exact against the oracle's ranking (logit descending, ties to
+    the lower id); weights to fp32 rounding."""
+    g = torch.Generator().manual_seed(M + E + k)
+    logits = torch.randn(M, E, generator=g).to(dtype)
+    if M > 3:
+        logits[3, :] = logits[3, 0]          # every logit tied
+        logits[2, 5 % E] = logits[2, 1 % E]  # one tie
+    x = torch.empty(M, 8, device=gpu)
+    w, ids = fm.fused_topk(x, logits.to(gpu), k, renormalize=renorm,
+                           scoring_func=scoring)
+    rw, rids = moe_ref.topk_gating(logits, k, scoring=scoring, renormalize=renorm)
+    assert torch.equal(ids.cpu(), rids)
+    assert torch.allclose(w.cpu(), rw, rtol=2e-6, atol=1e-7)
+
+
+def test_topk_gating_feeds_fused_moe(gpu):
+    """Gating kernel -> fused MoE equals the torch-routed path."""
+    M, K, N, E, k = 96, 256, 128, 8, 2
+    g = torch.Generator(device=gpu).manual_seed(3)
+    x = torch.randn(M, K, generator=g, device=gpu).to(torch.bfloat16)
+    w1 = (torch.randn(E, 2 * N, K, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    w2 = (torch.randn(E, K, N, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    logits = torch.randn(M, E, generator=g, device=gpu)
+    tw, ti = fm.fused_topk(x, logits, k)
+    rw, ri = moe_ref.route(logits.cpu(), k)
+    assert torch.equal(ti.cpu(), ri)
+    a = fm.fused_moe(x, w1, w2, tw, ti)
+    b = fm.fused_moe(x, w1, w2, rw.to(gpu), ri.to(gpu))
+    assert (a.float() - b.float()).abs().max() <= 2e-2 * b.float().abs().max()

@@ -84,6 +84,33 @@ def test_align_matches_reference_stable_order(M, k, E, B):
     assert (eids[npp // B:] == -1).all()
 
 
+# ---------------------------------------------------------------- gating ---
+def test_topk_gating_known_answers():
+    logits = torch.tensor([[1.0, 3.0, 3.0, 0.0], [0.5, -1.0, 2.0, 2.0]])
+    w, ids = moe_ref.topk_gating(logits, 2)
+    assert ids.tolist() == [[1, 2], [2, 3]]          # equal logits: lower id first
+    assert torch.allclose(w, torch.full((2, 2), 0.5))  # equal scores, renormalised
+    w, ids = moe_ref.topk_gating(logits, 3, renormalize=False)
+    sm = torch.softmax(logits, -1)
+    assert ids.tolist() == [[1, 2, 0], [2, 3, 0]]
+    assert torch.allclose(w, torch.gather(sm, 1, ids.long()))
+    w, ids = moe_ref.topk_gating(logits, 1, scoring="sigmoid", renormalize=False)
+    assert ids.tolist() == [[1], [2]]
+    assert torch.allclose(w[:, 0], torch.sigmoid(torch.tensor([3.0, 2.0])))
+
+
+@pytest.mark.parametrize("scoring", ["softmax", "sigmoid"])
+def test_topk_gating_equals_reference_routing(scoring):
+    """Without ties, ranking logits = ranking scores: same experts, same
+    order and weights as the reference tests' torch.topk routing (route)."""
+    g = torch.Generator().manual_seed(11)
+    logits = torch.randn(200, 64, generator=g)
+    w1, i1 = moe_ref.topk_gating(logits, 8, scoring=scoring)
+    w2, i2 = moe_ref.route(logits, 8, scoring=scoring)
+    assert torch.equal(i1, i2)
+    assert torch.allclose(w1, w2, rtol=1e-6, atol=1e-7)
+
+
 # -------------------------------------------------------------- silu*mul ---
 def test_silu_and_mul_closed_form_float64():
     g = torch.Generator().manual_seed(0)

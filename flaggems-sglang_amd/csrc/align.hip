@@ -20,6 +20,7 @@
 namespace fgs {
 
 constexpr int kAlignWaves = 16;
+constexpr int64_t kAlignMultiMin = 4096;  // slots from which the multi-WG path runs
 constexpr int kAlignThreads = kAlignWaves * kWave;
 
 __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
@@ -149,6 +150,162 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
 }
 
+// ------------------------------------------------ multi-workgroup variant ---
+// For many slots: the ids are cut into chunks of kChunk consecutive slots.
+// Kernel 1 counts each chunk's ids per expert (counts[c][e]). Kernel 2 runs
+// one workgroup per chunk: it sums the counts of every chunk (totals) and of
+// the chunks before its own (its per-expert base, so lower slots come
+// first), redoes the padded scan over experts, then ranks its own chunk like
+// pass 3 above (per-wave LDS counts, ballots over the id bits) and scatters.
+// Pads, the tail and the block -> expert map are split over the
+// workgroups. Same output, bit for bit, as moe_align_kernel.
+constexpr int kChunkWaves = 4;
+constexpr int kChunkThreads = kChunkWaves * kWave;
+constexpr int kChunk = 1024;  // slots per chunk (256 per wave)
+
+__global__ __launch_bounds__(kChunkThreads) void moe_align_count_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int num_experts,
+    int32_t* __restrict__ counts) {
+  extern __shared__ int32_t hist[];  // [E]
+  const int E = num_experts;
+  for (int e = threadIdx.x; e < E; e += kChunkThreads) hist[e] = 0;
+  __syncthreads();
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
+  for (int64_t i = c0 + threadIdx.x; i < c0 + kChunk && i < numel; i += kChunkThreads) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kChunkThreads)
+    counts[static_cast<int64_t>(blockIdx.x) * E + e] = hist[e];
+}
+
+__global__ __launch_bounds__(kChunkThreads) void moe_align_scatter_kernel(
+    const int32_t* __restrict__ ids, int64_t numel, int num_experts,
+    int block_size, int id_bits, const int32_t* __restrict__ counts,
+    int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ num_post_pad, int64_t max_padded) {
+  extern __shared__ int32_t smem[];
+  const int E = num_experts;
+  int32_t* cnt = smem;                         // [4][E]: wave counts, then cursors
+  int32_t* off = cnt + kChunkWaves * E;        // [E + 1] padded expert offsets
+  int32_t* tot = off + E + 1;                  // [E]
+  int32_t* pre = tot + E;                      // [E] slots of earlier chunks
+  __shared__ int32_t scan_tmp[kChunkWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int c = blockIdx.x;
+  const int nchunks = gridDim.x;
+
+  for (int e = tid; e < E; e += kChunkThreads) {
+    int before = 0, all = 0;
+    for (int cc = 0; cc < nchunks; ++cc) {
+      const int v = counts[static_cast<int64_t>(cc) * E + e];
+      if (cc < c) before += v;
+      all += v;
+    }
+    pre[e] = before;
+    tot[e] = all;
+  }
+  for (int i = tid; i < kChunkWaves * E; i += kChunkThreads) cnt[i] = 0;
+  __syncthreads();
+
+  // exclusive scan of padded sizes over experts
+  int carry = 0;
+  for (int base = 0; base < E; base += kChunkThreads) {
+    const int e = base + tid;
+    const int padded = e < E ? (tot[e] + block_size - 1) / block_size * block_size : 0;
+    int v = padded;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int t = __shfl_up(v, d, kWave);
+      if (lane >= d) v += t;
+    }
+    if (lane == kWave - 1) scan_tmp[wave] = v;
+    __syncthreads();
+    int wave_base = 0, all = 0;
+    for (int w = 0; w < kChunkWaves; ++w) {
+      const int sw = scan_tmp[w];
+      if (w < wave) wave_base += sw;
+      all += sw;
+    }
+    if (e < E) off[e] = carry + wave_base + v - padded;
+    carry += all;
+    __syncthreads();
+  }
+  if (tid == 0) off[E] = carry;
+  if (c == 0 && tid == 0) num_post_pad[0] = carry;
+
+  // this chunk's per-(wave, expert) counts; each wave owns 256 slots
+  const int64_t wbeg = static_cast<int64_t>(c) * kChunk + wave * (kChunk / kChunkWaves);
+  const int64_t wend = wbeg + kChunk / kChunkWaves < numel ? wbeg + kChunk / kChunkWaves : numel;
+  for (int64_t i = wbeg + lane; i < wend; i += kWave) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
+  }
+  __syncthreads();
+  // cursors: expert offset + earlier chunks + earlier waves of this chunk
+  for (int e = tid; e < E; e += kChunkThreads) {
+    int run = off[e] + pre[e];
+    for (int w = 0; w < kChunkWaves; ++w) {
+      const int v = cnt[w * E + e];
+      cnt[w * E + e] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+
+  // pads and block -> expert map of experts c, c + nchunks, ...; the tail
+  const int total_padded = off[E];
+  for (int e = c * kChunkWaves + wave; e < E; e += nchunks * kChunkWaves) {
+    const int64_t p0 = static_cast<int64_t>(off[e]) + tot[e];
+    for (int64_t p = p0 + lane; p < off[e + 1]; p += kWave)
+      sorted_ids[p] = static_cast<int32_t>(numel);
+    for (int b = off[e] / block_size + lane; b < off[e + 1] / block_size; b += kWave)
+      expert_ids[b] = e;
+  }
+  for (int64_t p = total_padded + static_cast<int64_t>(c) * kChunkThreads + tid;
+       p < max_padded; p += static_cast<int64_t>(nchunks) * kChunkThreads)
+    sorted_ids[p] = static_cast<int32_t>(numel);
+  for (int64_t b = total_padded / block_size + static_cast<int64_t>(c) * kChunkThreads + tid;
+       b < max_padded / block_size; b += static_cast<int64_t>(nchunks) * kChunkThreads)
+    expert_ids[b] = -1;
+
+  // stable scatter, 64 slots at a time
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  for (int64_t c0 = wbeg; c0 < wend; c0 += kWave) {
+    const int64_t i = c0 + lane;
+    int e = -1;
+    if (i < wend) {
+      e = ids[i];
+      if (e < 0 || e >= E) e = -1;
+    }
+    const bool valid = e >= 0;
+    uint64_t match = __ballot(valid);
+    for (int b = 0; b < id_bits; ++b) {
+      const bool bit = valid && ((e >> b) & 1);
+      const uint64_t on = __ballot(bit);
+      match &= bit ? on : ~on;
+    }
+    int base = 0;
+    if (valid) base = cnt[wave * E + e];
+    const int rank = __popcll(match & lt_mask);
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      sorted_ids[base + rank] = static_cast<int32_t>(i);
+      const bool leader = (match >> lane) == 1ull;
+      if (leader) cnt[wave * E + e] = base + __popcll(match);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+int64_t align_scratch_bytes(int64_t numel, int num_experts) {
+  if (numel < kAlignMultiMin) return 0;
+  return (numel + kChunk - 1) / kChunk * num_experts * static_cast<int64_t>(sizeof(int32_t));
+}
+
 size_t align_smem_bytes(int num_experts) {
   return sizeof(int32_t) *
          (static_cast<size_t>(kAlignWaves) * num_experts + 2 * num_experts + 1);
@@ -157,9 +314,22 @@ size_t align_smem_bytes(int num_experts) {
 int launch_align(const int32_t* ids, int64_t numel, int num_experts,
                  int block_size, int32_t* sorted_ids, int32_t* expert_ids,
                  int32_t* num_post_pad, int64_t max_padded,
-                 hipStream_t stream) {
+                 hipStream_t stream, int32_t* scratch) {
   int id_bits = 0;
   while ((1 << id_bits) < num_experts) ++id_bits;
+  if (scratch && numel >= kAlignMultiMin) {
+    const int nchunks = static_cast<int>((numel + kChunk - 1) / kChunk);
+    const size_t smem1 = sizeof(int32_t) * num_experts;
+    const size_t smem2 = sizeof(int32_t) * ((kChunkWaves + 3) * num_experts + 1);
+    hipLaunchKernelGGL(moe_align_count_kernel, dim3(nchunks), dim3(kChunkThreads),
+                       smem1, stream, ids, numel, num_experts, scratch);
+    int rc = check_launch("moe_align_count_kernel");
+    if (rc) return rc;
+    hipLaunchKernelGGL(moe_align_scatter_kernel, dim3(nchunks), dim3(kChunkThreads),
+                       smem2, stream, ids, numel, num_experts, block_size, id_bits,
+                       scratch, sorted_ids, expert_ids, num_post_pad, max_padded);
+    return check_launch("moe_align_scatter_kernel");
+  }
   const size_t smem = align_smem_bytes(num_experts);
   if (smem > 64 * 1024) {
     // gfx950 has 160 KiB of LDS per CU; opt in beyond the 64 KiB default.

@@ -54,7 +54,7 @@ struct Plan {
   int ksplit2;     // GEMM2 k splits (tiled only; > 1 -> fp32 partials)
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
-  int64_t o_sorted, o_eids, o_npp, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, total;
+  int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, total;
 };
 
 // k splits for the tiled GEMM2: its grid (row blocks x hidden/256 column
@@ -139,6 +139,8 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   p.o_sorted = take(p.max_padded * 4);
   p.o_eids = take(std::max<int64_t>(p.n_blocks, 1) * 4);
   p.o_npp = take(4);
+  const int64_t alg = align_scratch_bytes(numel, e);
+  p.o_alg = alg > 0 ? take(alg) : -1;
   p.o_a2 = take(p.max_padded * inter * 2);
   p.o_xq = p.o_xs = p.o_a2q = p.o_a2s = -1;
   if (p.dt != kDtBf16) {
@@ -285,7 +287,8 @@ static int run_fused(const FusedArgs& a) {
   g_prof.begin();
   g_prof.mark(0, a.stream);
   rc = launch_align(a.topk_ids, numel, a.e, p.block_m, sorted, eids, npp,
-                    p.max_padded, a.stream);
+                    p.max_padded, a.stream,
+                    p.o_alg >= 0 ? reinterpret_cast<int32_t*>(ws + p.o_alg) : nullptr);
   if (rc) return rc;
   g_prof.mark(1, a.stream);
 
@@ -402,10 +405,16 @@ int64_t fgs_moe_align_max_padded(int64_t numel, int32_t num_experts,
   return numel + static_cast<int64_t>(num_experts) * (block_size - 1);
 }
 
+int64_t fgs_moe_align_scratch_bytes(int64_t numel, int32_t num_experts) {
+  if (numel < 0 || num_experts < 1 || num_experts > kMaxExperts) return -1;
+  return align_scratch_bytes(numel, num_experts);
+}
+
 int32_t fgs_moe_align_block_size(const int32_t* topk_ids, int64_t numel,
                                  int32_t num_experts, int32_t block_size,
                                  int32_t* sorted_ids, int32_t* expert_ids,
                                  int32_t* num_post_pad, int64_t max_padded,
+                                 void* scratch, int64_t scratch_bytes,
                                  void* stream) {
   if (numel < 0) return fail(FGS_EINVAL, "numel must be >= 0");
   if (num_experts < 1 || num_experts > kMaxExperts)
@@ -420,8 +429,12 @@ int32_t fgs_moe_align_block_size(const int32_t* topk_ids, int64_t numel,
     return fail(FGS_EUNSUPPORTED, "max_padded must fit in int32");
   if ((numel > 0 && !topk_ids) || !sorted_ids || !expert_ids || !num_post_pad)
     return fail(FGS_EINVAL, "null pointer argument");
+  // the multi-workgroup path only with enough scratch (else one workgroup)
+  const int64_t need_scratch = align_scratch_bytes(numel, num_experts);
+  int32_t* sc = (scratch && need_scratch > 0 && scratch_bytes >= need_scratch)
+                    ? static_cast<int32_t*>(scratch) : nullptr;
   return launch_align(topk_ids, numel, num_experts, block_size, sorted_ids,
-                      expert_ids, num_post_pad, max_padded, as_stream(stream));
+                      expert_ids, num_post_pad, max_padded, as_stream(stream), sc);
 }
 
 int32_t fgs_moe_silu_and_mul(const void* in, void* out, int64_t rows,

@@ -46,9 +46,15 @@ int launch_topk_gating(const void* logits, bool bf16_in, int64_t m,
                        hipStream_t stream);
 
 size_t align_smem_bytes(int num_experts);
+// Scratch (int32 per chunk and expert) the multi-workgroup alignment uses for
+// `numel` slots; 0 when the single-workgroup kernel runs.
+int64_t align_scratch_bytes(int64_t numel, int num_experts);
+// With `scratch` (align_scratch_bytes of it) large inputs run on many
+// workgroups; without it, one workgroup. Same output either way.
 int launch_align(const int32_t* ids, int64_t numel, int num_experts,
                  int block_size, int32_t* sorted_ids, int32_t* expert_ids,
-                 int32_t* num_post_pad, int64_t max_padded, hipStream_t stream);
+                 int32_t* num_post_pad, int64_t max_padded, hipStream_t stream,
+                 int32_t* scratch = nullptr);
 
 int launch_silu_and_mul(const void* in, void* out, int64_t rows, int64_t n,
                         hipStream_t stream);

@@ -48,8 +48,9 @@ SIGNATURES = {
     "fgs_moe_align_block_size": (
         _i32,
         [_c_void_p, _i64, _i32, _i32, _c_void_p, _c_void_p, _c_void_p, _i64,
-         _c_void_p],
+         _c_void_p, _i64, _c_void_p],
     ),
+    "fgs_moe_align_scratch_bytes": (_i64, [_i64, _i32]),
     "fgs_moe_silu_and_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "fgs_moe_sum": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _i64, _c_void_p]),
     "fgs_moe_topk_gating": (

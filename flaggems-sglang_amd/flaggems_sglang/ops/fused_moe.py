@@ -165,7 +165,7 @@ def fused_topk(hidden_states: torch.Tensor, gating_output: torch.Tensor,
 
 # ------------------------------------------------------------ small ops ---
 def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int,
-                         block_size: int):
+                         block_size: int, _single_workgroup: bool = False):
     """Expert-grouped, block-padded routing order (HIP kernel).
 
     Returns ``(sorted_ids, expert_ids, num_tokens_post_padded)``; the
@@ -185,11 +185,15 @@ def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int,
     expert_ids = torch.empty(max(max_padded // block_size, 1),
                              dtype=torch.int32, device=dev)
     npp = torch.empty(1, dtype=torch.int32, device=dev)
+    sc_bytes = 0 if _single_workgroup else max(
+        lib.fgs_moe_align_scratch_bytes(numel, num_experts), 0)
+    scratch = torch.empty(max(sc_bytes, 1), dtype=torch.uint8, device=dev)
     _capi.check(
         lib.fgs_moe_align_block_size(
             ids.data_ptr(), numel, num_experts, block_size,
             sorted_ids.data_ptr(), expert_ids.data_ptr(), npp.data_ptr(),
-            max_padded, _stream_ptr(ids)),
+            max_padded, scratch.data_ptr() if sc_bytes else None, sc_bytes,
+            _stream_ptr(ids)),
         "moe_align_block_size",
     )
     return sorted_ids, expert_ids[: max_padded // block_size], npp

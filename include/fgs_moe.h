@@ -79,12 +79,21 @@ int64_t fgs_moe_align_max_padded(int64_t numel, int32_t num_experts,
  *                -1 past the padded total.
  *   num_post_pad int32 [1]: padded total.
  * Slots whose id is outside [0, num_experts) are dropped (not routed).
- * Bit-exact and deterministic (no atomics decide any order). */
+ * Bit-exact and deterministic (no atomics decide any order).
+ * scratch: device memory of fgs_moe_align_scratch_bytes() bytes (or null /
+ * too small: the computation then runs on one workgroup, slower for large
+ * numel); the result is identical either way. */
 int32_t fgs_moe_align_block_size(const int32_t* topk_ids, int64_t numel,
                                  int32_t num_experts, int32_t block_size,
                                  int32_t* sorted_ids, int32_t* expert_ids,
                                  int32_t* num_post_pad, int64_t max_padded,
+                                 void* scratch, int64_t scratch_bytes,
                                  void* stream);
+
+/* Scratch bytes fgs_moe_align_block_size uses for numel slots (0: none
+ * needed), or -1 for invalid arguments. No reference counterpart (the
+ * reference's conversion runs as torch ops, ops/fused_moe.py:130-139). */
+int64_t fgs_moe_align_scratch_bytes(int64_t numel, int32_t num_experts);
 
 /* silu_and_mul: out[r, c] = bf16(silu(f32(in[r, c])) * f32(in[r, n + c])).
  * in bf16 [rows, 2n], out bf16 [rows, n].

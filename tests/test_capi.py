@@ -98,9 +98,14 @@ def test_entry_points_reject_bad_arguments_before_launch():
     lib = _capi.load()
     nul = None
     # max_padded below numel + E*(B-1)
-    assert lib.fgs_moe_align_block_size(nul, 8, 4, 16, nul, nul, nul, 10, nul) == -1
+    assert lib.fgs_moe_align_block_size(nul, 8, 4, 16, nul, nul, nul, 10, nul, 0,
+                                        nul) == -1
     assert "max_padded" in _capi.last_error()
-    assert lib.fgs_moe_align_block_size(nul, 8, 0, 16, nul, nul, nul, 100, nul) == -1
+    assert lib.fgs_moe_align_block_size(nul, 8, 0, 16, nul, nul, nul, 100, nul, 0,
+                                        nul) == -1
+    assert lib.fgs_moe_align_scratch_bytes(100, 8) == 0      # one workgroup
+    assert lib.fgs_moe_align_scratch_bytes(65536, 128) == 64 * 128 * 4
+    assert lib.fgs_moe_align_scratch_bytes(-1, 8) == -1
     assert lib.fgs_moe_topk_gating(nul, 0, 4, 8, 9, 0, 1, nul, nul, nul) == -1
     assert "topk" in _capi.last_error()
     assert lib.fgs_moe_topk_gating(nul, 0, 4, 2000, 2, 0, 1, nul, nul, nul) == -1

@@ -31,10 +31,17 @@ ALIGN_CASES = [
 ]
 
 
-@pytest.mark.parametrize("M,k,E,B", ALIGN_CASES)
-def test_align_bit_exact(gpu, M, k, E, B):
+@pytest.mark.parametrize("single_wg", [False, True], ids=["default", "one_wg"])
+@pytest.mark.parametrize("M,k,E,B", ALIGN_CASES + [(5000, 3, 1024, 16), (4097, 1, 64, 64)])
+def test_align_bit_exact(gpu, M, k, E, B, single_wg):
+    """Both the multi-workgroup path (>= 4096 slots, with scratch) and the
+    one-workgroup path, bit for bit against the oracle."""
     w, ids = _routing(M, E, k, seed=M + k + E + B, device=gpu)
-    s, eids, npp = fm.moe_align_block_size(ids.to(gpu), E, B)
+    if M > 100:
+        ids[::97, 0] = -1          # dropped slots inside the chunks
+        ids[5::101, -1] = E + 3
+    s, eids, npp = fm.moe_align_block_size(ids.to(gpu), E, B,
+                                           _single_workgroup=single_wg)
     rs, reids, rnpp = moe_ref.align(ids.numpy(), E, B)
     torch.cuda.synchronize()
     assert int(npp.item()) == rnpp

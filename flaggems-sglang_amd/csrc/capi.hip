@@ -332,6 +332,7 @@ static int run_fused(const FusedArgs& a) {
   g1.alpha = a.alpha;
   g1.limit = a.limit;
   g1.bias = a.b13;
+  g1.a_rows = a.m;
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, static_cast<int>(p.n_launch),
                                    a.stream)
                : launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
@@ -370,6 +371,7 @@ static int run_fused(const FusedArgs& a) {
   g2.n_out = a.hidden;
   g2.nrows_w = a.hidden;
   g2.ksplit = p.ksplit2;
+  g2.a_rows = p.max_padded;
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, false, g2, static_cast<int>(p.n_launch),
                                    a.stream)
                : launch_gemm_stream(p.dt, false, g2, p.mt, p.kw2,

@@ -36,6 +36,7 @@ struct GemmParams {
   int32_t act;            // GEMM1 activation (kActSilu / kActGelu / kActSwiglu)
   float alpha, limit;     // swiglu parameters
   const float* bias;      // fp32 per expert: GEMM1 [E, 2N] (gate | up), GEMM2 [E, K]; or null
+  int64_t a_rows;         // rows of `a` (GEMM1: tokens; GEMM2: padded rows)
 };
 
 // Router gating (scores -> top-k -> renormalise), one wave per token;
@@ -93,5 +94,11 @@ int tiled_block_m(int cfg);
 int tiled_n_align(bool gemm1);
 int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
                       int row_blocks, hipStream_t stream);
+
+// 4-wave kernel of the 256-row configuration (bf16, int8): whether it
+// covers a launch, and the launch.
+bool wide_supported(int dt, bool gemm1, const GemmParams& p);
+int launch_gemm_wide(int dt, bool gemm1, const GemmParams& p, int row_blocks,
+                     hipStream_t stream);
 
 }  // namespace fgs

@@ -22,30 +22,9 @@
 #include <string>
 #include <type_traits>
 
-#include "fgs_moe_kernels.h"
+#include "gemm_tiled_common.h"
 
 namespace fgs {
-
-// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// One wave-wide LDS-DMA load: lane l copies 16 bytes from `src` (its own
-// global address) to byte 16*l of the 1 KiB block at `lds_dst` (uniform).
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds(
-      src, (__attribute__((address_space(3))) void*)(lds_dst), 16, 0, 0);
-}
-
-__device__ __forceinline__ void wave_barrier_all() { __builtin_amdgcn_s_barrier(); }
-
-// s_waitcnt lgkmcnt(0): this wave's LDS reads have completed.
-__device__ __forceinline__ void wait_lgkm0() {
-  __builtin_amdgcn_s_waitcnt((63 & 15) | (7 << 4) | (0 << 8) | ((63 >> 4) << 14));
-}
 
 // Tile order. The grid is 1-D and padded to a multiple of the 8 XCDs.
 // Workgroup `pid` runs on XCD pid % 8, so logical tile
@@ -77,18 +56,6 @@ __device__ __forceinline__ bool tile_of(int pid, int grid, int n_rb, int n_ct,
   return true;
 }
 
-// Calls f(std::integral_constant<int, n>) for a runtime n in [0, N].
-template <int N, class F>
-__device__ __forceinline__ void dispatch_count(int n, F&& f) {
-  if constexpr (N >= 0) {
-    if (n == N) {
-      f(std::integral_constant<int, N>{});
-      return;
-    }
-    dispatch_count<N - 1>(n, f);
-  }
-}
-
 template <int BM_, int BNR_, int WM_, int WN_, int SK_, int STAGES_>
 struct TileCfg {
   static constexpr int BM = BM_;        // rows (alignment block size)
@@ -113,44 +80,6 @@ template <class C>
 __device__ __forceinline__ int chunk_pos(int r, int c) {
   return c ^ ((r / C::RPL) % C::CPR);
 }
-
-// Element types of the tiled kernels. A 32x32 MFMA k step reads 16 bytes
-// per lane of each operand (bf16: 8 elements, int8: 16) -- one LDS chunk --
-// except fp8, whose 32x32x64 MFMA reads 32 bytes per lane (two chunks).
-template <int DT>
-struct TiledType;
-template <>
-struct TiledType<kDtBf16> {
-  static constexpr int ESZ = 2, FC = 1;
-  using Frag = bf16x8;
-  using Acc = f32x16;
-  static __device__ __forceinline__ Acc mma(Frag w, Frag x, Acc c) {
-    return mfma32_bf16(w, x, c);
-  }
-};
-template <>
-struct TiledType<kDtInt8> {
-  static constexpr int ESZ = 1, FC = 1;
-  using Frag = i32x4;
-  using Acc = i32x16;
-  // v_mfma_i32_32x32x32_i8: same lane layout as the bf16 32x32x16 form
-  // with 16 int8 of k per lane.
-  static __device__ __forceinline__ Acc mma(Frag w, Frag x, Acc c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(w, x, c, 0, 0, 0);
-  }
-};
-template <>
-struct TiledType<kDtFp8> {
-  static constexpr int ESZ = 1, FC = 2;
-  using Frag = i32x8;
-  using Acc = f32x16;
-  // v_mfma_scale_f32_32x32x64_f8f6f4, both operands OCP e4m3 (format 0),
-  // unit e8m0 block scales (127): 32 fp8 of k per lane.
-  static __device__ __forceinline__ Acc mma(Frag w, Frag x, Acc c) {
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w, x, c, 0, 0, 0, 127,
-                                                           0, 127);
-  }
-};
 
 // Bytes of the per-stage scale area (fp8 only): one float slot per lane of
 // the workgroup, filled by one 4-byte LDS-DMA load per wave per stage.
@@ -581,6 +510,14 @@ static int group_m_choice() {
   static const int g = env_choice("FGS_MOE_GROUPM", 0, 0, 64);
   return g;
 }
+// Which GEMMs of the 256-row configuration run the 4-wave kernel
+// (gemm_wide.hip): 1 (default) GEMM1, 2 both, 0 neither (FGS_MOE_WIDE, a
+// tuning aid; read once). GEMM1 gains on every measured configuration;
+// GEMM2 measured slower than the 8-wave kernel on the Mixtral layer.
+static int wide_choice() {
+  static const int mode = env_choice("FGS_MOE_WIDE", 1, 0, 2);
+  return mode;
+}
 static int group_n_choice() {
   static const int g = env_choice("FGS_MOE_GROUPN", 4, 1, 64);
   return g;
@@ -669,6 +606,8 @@ int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
     return fail(FGS_EINVAL, "tiled GEMM: configuration " + std::to_string(cfg) +
                                 " not available for this element type");
   if (row_blocks <= 0) return FGS_OK;
+  if (cfg == 0 && wide_choice() >= (gemm1 ? 1 : 2) && wide_supported(dt, gemm1, p))
+    return launch_gemm_wide(dt, gemm1, p, row_blocks, stream);
   switch (dt) {
     case kDtBf16:
       switch (cfg) {

@@ -1,0 +1,498 @@
+// 4-wave grouped GEMM for the prefill regime (bf16, int8).
+//
+// Same contraction, row order and epilogues as moe_gemm_tiled_kernel
+// (gemm_tiled.hip) on 256-row blocks, organised for one wave per SIMD:
+//
+// * a tile is 256 padded rows x 256 weight rows; wave (wm, wn) of the 2x2
+//   grid computes 128 rows x 128 weight rows with 16 accumulators of
+//   v_mfma_f32_32x32x16_bf16 / v_mfma_i32_32x32x32_i8 (256 AGPRs), so each
+//   k step reads 8 fragments from LDS for 16 MFMAs (the 8-wave 64x128 layout
+//   reads 6 for 8). Its rows are the 32-row blocks wm, wm+2, wm+4, wm+6:
+//   the pad rows of a partial block (a suffix) then fall evenly on both
+//   row halves, i.e. on all four SIMDs, whose all-pad blocks skip their
+//   MFMAs;
+// * operand tiles stream through an NS-slot LDS ring of SK-byte k stages
+//   (A slots first, then B slots) filled by buffer_load ... lds: one buffer
+//   resource per operand (the weight resource starts at the tile's expert),
+//   32-bit row offsets per lane and the k offset in the scalar offset, so a
+//   stage costs no address arithmetic. A stage's refill loads go out one
+//   between each pair of MFMAs of its last k step;
+// * tiles are ordered for the L2 of each XCD: the live tiles are cut into 8
+//   row-block-major ranges, one per XCD (about one expert in eight each),
+//   walked in column groups.
+#include <stdlib.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+
+#include "gemm_tiled_common.h"
+
+namespace fgs {
+
+template <int SK_, int NS_>
+struct WideCfg {
+  static constexpr int BM = 256;              // rows per tile (= alignment block)
+  static constexpr int BNR = 256;             // weight rows per tile
+  static constexpr int NW = 4;                // waves: 2 row halves x 2 weight-row halves
+  static constexpr int WROWS = 128;           // rows per wave (4 interleaved 32-row blocks)
+  static constexpr int WCOLS = 128;           // weight rows per wave
+  static constexpr int RB = WROWS / 32;       // 32-row MFMA blocks per wave
+  static constexpr int CB = WCOLS / 32;       // 32-col MFMA blocks per wave
+  static constexpr int SK = SK_;              // k bytes per stage row
+  static constexpr int NS = NS_;              // ring slots
+  static constexpr int KK = SK / 32;          // MFMA k steps per stage (32 bytes each)
+  static constexpr int CPR = SK / 16;         // 16-byte chunks per stage row
+  static constexpr int LR = 64 / CPR;         // rows one wave load (1 KiB) covers
+  static constexpr int RPL = 256 / SK;        // stage rows per 256-byte bank line
+  static constexpr int NLA = BM / (LR * NW);  // loads per wave per stage
+  static constexpr int NLB = BNR / (LR * NW);
+  static constexpr int NL = NLA + NLB;
+  static constexpr int SLOT = BM * SK;        // bytes per operand slot
+  static constexpr int B_OFF = NS * SLOT;
+  static constexpr int LDS_BYTES = 2 * NS * SLOT;
+  static_assert(BM == BNR, "one slot size for both operands");
+  static_assert(KK % 2 == 0, "fragment double buffer wraps at a stage boundary");
+  static_assert(NS >= 2 && (NS - 2) * NL < 64, "ring depth / vmcnt range");
+  static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KiB");
+  static_assert((NS - 1) * SLOT + (RB - 1) * 32 * SK < 65536, "ds_read offset range");
+};
+using WideRing = WideCfg<128, 2>;
+
+// Position of logical 16-byte chunk c of stage row r: RPL rows share a
+// 256-byte bank line, and the XOR gives the 16 rows a fragment read serves
+// at once 16 distinct bank positions.
+template <class C>
+__device__ __forceinline__ int wide_chunk(int r, int c) {
+  return c ^ ((r / C::RPL) % C::CPR);
+}
+
+// One wave-wide buffer load into LDS: lane l copies 16 bytes from
+// rsrc + voff + soff to byte 16*l of the 1 KiB block at `lds_dst` (uniform).
+__device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff,
+                                              int soff, void* lds_dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)(lds_dst), 16, voff, soff, 0, 0);
+}
+
+// gfx9 buffer resource word 3 for raw 32-bit loads.
+constexpr int kBufWord3 = 0x00020000;
+
+template <int DT, bool GEMM1, class C>
+__global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const GemmParams p) {
+  using T = TiledType<DT>;
+  using Frag = typename T::Frag;
+  using Acc = typename T::Acc;
+  constexpr bool INT8 = DT == kDtInt8;
+  constexpr int ESZ = T::ESZ;
+  constexpr int BM = C::BM, BNR = C::BNR, WROWS = C::WROWS, WCOLS = C::WCOLS;
+  constexpr int RB = C::RB, CB = C::CB, SK = C::SK, NS = C::NS, KK = C::KK;
+  constexpr int NLA = C::NLA, NLB = C::NLB, NL = C::NL, SLOT = C::SLOT, B_OFF = C::B_OFF;
+  static_assert(T::FC == 1, "one LDS chunk per fragment");
+
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / 2;
+  const int wn = wave % 2;
+  const int64_t row_bytes = p.kdim * ESZ;
+  const int npp = __builtin_amdgcn_readfirstlane(p.num_post_pad[0]);
+  constexpr int N_PER_TILE = GEMM1 ? BNR / 2 : BNR;
+  const int n_ct = static_cast<int>(p.n_out / N_PER_TILE);
+  const int KT_all = static_cast<int>(row_bytes / SK);
+
+  // ---- tile walk. The live tiles -- row blocks below
+  // num_tokens_post_padded (times the k splits) x column tiles -- are
+  // numbered row-block-major and cut into 8 equal contiguous ranges, one per
+  // XCD (workgroup b runs on XCD b % 8): an XCD works on about 1/8 of the
+  // row blocks, i.e. a few experts, across all columns, so each weight tile
+  // is fetched into its L2 once for all the row blocks of its expert. Inside
+  // a range, positions run over groups of group_n columns, then row blocks,
+  // then the columns of the group. Workgroup b takes position b / 8 of its
+  // XCD's walk (the hardware hands out workgroups in order as CUs free up),
+  // so the tiles in flight at once share weight and activation tiles.
+  const int rb_live = npp / BM;
+  const int rows_all = rb_live * p.ksplit;  // row-block index space over splits
+  const int total = rows_all * n_ct;
+  const int xcd = blockIdx.x % 8;
+  const int lo = static_cast<int>(static_cast<int64_t>(total) * xcd / 8);
+  const int hi = static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8);
+  const int rb_lo = lo / n_ct;
+  const int n_rb = hi > lo ? (hi - 1) / n_ct - rb_lo + 1 : 0;
+  const int gn = p.group_n;
+  const int n_pos = (n_ct + gn - 1) / gn * n_rb * gn;
+
+  struct Tile {
+    int pos;  // >= n_pos: none
+    int rb, ct, e, kt0, KT, ks;
+  };
+  auto live_tile = [&](int pos, Tile& t) -> bool {
+    const int span = n_rb * gn;
+    const int group = pos / span;
+    const int idx = pos - group * span;
+    const int gsize = min(gn, n_ct - group * gn);
+    if (idx >= n_rb * gsize) return false;
+    const int rball = rb_lo + idx / gsize;
+    t.ct = group * gn + idx % gsize;
+    const int tile = rball * n_ct + t.ct;
+    if (tile < lo || tile >= hi) return false;
+    t.ks = rball / rb_live;
+    t.rb = rball - t.ks * rb_live;
+    t.e = __builtin_amdgcn_readfirstlane(p.expert_ids[t.rb]);
+    if (t.e < 0) return false;
+    t.kt0 = t.ks * KT_all / p.ksplit;
+    t.KT = (t.ks + 1) * KT_all / p.ksplit - t.kt0;
+    return true;
+  };
+
+  // ---- per-tile DMA sources: the expert and this lane's row offsets
+  struct Src {
+    int e;  // expert of the weight rows
+    uint32_t va[NLA], vb[NLB];
+  };
+  const int lrow = lane / C::CPR;   // row of a load this lane copies
+  const int lchunk = lane % C::CPR;  // its physical chunk
+  auto act_row = [&](int row0, int r) -> int64_t {
+    const int sid = p.sorted_ids[row0 + r];
+    const bool ok = sid < p.numel;
+    return GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? r : 0);
+  };
+  auto make_src = [&](const Tile& t, Src& s) {
+    const int row0 = t.rb * BM;
+    s.e = t.e;
+#pragma unroll
+    for (int i = 0; i < NLA; ++i) {
+      const int r = (wave * NLA + i) * C::LR + lrow;
+      s.va[i] = static_cast<uint32_t>(act_row(row0, r) * row_bytes +
+                                      wide_chunk<C>(r, lchunk) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < NLB; ++i) {
+      const int j = (wave * NLB + i) * C::LR + lrow;  // tile row
+      int64_t wrow;
+      if constexpr (GEMM1) {
+        // wave column wc's tile rows: WCOLS/2 gate rows, then the same
+        // output columns' up rows
+        constexpr int HALF = WCOLS / 2;
+        const int wc = j / WCOLS;
+        const int in = j % WCOLS;
+        wrow = (in >= HALF ? p.n_out : 0) + t.ct * (BNR / 2) + wc * HALF + in % HALF;
+      } else {
+        wrow = static_cast<int64_t>(t.ct) * BNR + j;
+      }
+      s.vb[i] = static_cast<uint32_t>(wrow * row_bytes + wide_chunk<C>(j, lchunk) * 16);
+    }
+  };
+  // Buffer resources are built from scalars at each issue (the operands'
+  // sources change between tiles), so they stay in SGPRs.
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(p.a), 0, static_cast<int>(p.a_rows * row_bytes), kBufWord3);
+  const int w_bytes = static_cast<int>(p.nrows_w * row_bytes);
+  // Loads of one stage (k offset kbyte) into ring slot `slot`.
+  auto issue = [&](const Src& s, int kbyte, int slot) {
+    kbyte = __builtin_amdgcn_readfirstlane(kbyte);  // the scalar offset (uniform)
+    const int e = __builtin_amdgcn_readfirstlane(s.e);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(p.w) + static_cast<int64_t>(e) * w_bytes, 0, w_bytes, kBufWord3);
+    uint8_t* a_dst = lds + slot * SLOT + wave * NLA * 1024;
+    uint8_t* b_dst = lds + B_OFF + slot * SLOT + wave * NLB * 1024;
+#pragma unroll
+    for (int i = 0; i < NLA; ++i) lds_dma16_buf(ra, s.va[i], kbyte, a_dst + i * 1024);
+#pragma unroll
+    for (int i = 0; i < NLB; ++i) lds_dma16_buf(rb, s.vb[i], kbyte, b_dst + i * 1024);
+  };
+
+  // Fragment reads: lane reads row (lane & 31) of a 32-row block, logical
+  // chunk 2*kk + (lane >> 5). Offsets within the wave's A / B region.
+  const int fr = lane & 31;
+  int a_off[KK], b_off[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    const int o = fr * SK + wide_chunk<C>(fr, 2 * kk + (lane >> 5)) * 16;
+    a_off[kk] = wm * 32 * SK + o;  // block i of the wave: tile rows (2i + wm) * 32
+    b_off[kk] = B_OFF + wn * WCOLS * SK + o;
+  }
+
+  Tile cur;
+  cur.pos = static_cast<int>(blockIdx.x / 8);
+  if (cur.pos >= n_pos || !live_tile(cur.pos, cur)) return;
+  Src src;
+  make_src(cur, src);
+  // stage s lives in ring slot s % NS; stages 0..NS-1 load first
+  const int KT = cur.KT;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) issue(src, (cur.kt0 + s) * SK, s);
+
+  const int row0 = cur.rb * BM;
+  // live 32-row blocks of this wave (pad rows are a suffix of the tile, so
+  // the wave's live blocks are a prefix of i)
+  int nlive = 0;
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+    nlive += p.sorted_ids[row0 + i * 64 + wm * 32] < p.numel ? 1 : 0;
+  nlive = __builtin_amdgcn_readfirstlane(nlive);
+
+  // The tile (accumulators, k loop, epilogue) is instantiated per count of
+  // live 32-row blocks: all-pad blocks (the tail of an expert's last block)
+  // skip their MFMAs with no branch in the MFMA stream, and no accumulator
+  // crosses a control-flow join.
+  auto tile_body = [&](auto nlive_c) {
+    constexpr int NLIVE = decltype(nlive_c)::value;
+    Acc acc[RB][CB];
+    Frag fa[2][RB], fb[2][CB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+    auto read_frags = [&](int slot, int kk, Frag (&a)[RB], Frag (&b)[CB]) {
+      const uint8_t* st = lds + slot * SLOT;
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+        a[i] = *reinterpret_cast<const Frag*>(st + a_off[kk] + i * 64 * SK);
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        b[j] = *reinterpret_cast<const Frag*>(st + b_off[kk] + j * 32 * SK);
+    };
+    auto mma = [&](const Frag (&a)[RB], const Frag (&b)[CB]) {
+#pragma unroll
+      for (int i = 0; i < NLIVE; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j) acc[i][j] = T::mma(b[j], a[i], acc[i][j]);
+    };
+    // one MFMA, the next k step's fragment reads, the other MFMAs
+    auto sched_step = [&]() {
+      if constexpr (NLIVE > 0) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, RB + CB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - 1, 0);
+      }
+    };
+    // after a stage barrier: one MFMA, the next k step's fragment reads,
+    // then the stage's refill loads one between each pair of MFMAs, so the
+    // wave never stalls on a burst of vector-memory issues
+    auto sched_tail = [&]() {
+      if constexpr (NLIVE > 0) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, RB + CB, 0);
+#pragma unroll
+        for (int t = 0; t < NL; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          if (t < NLIVE * CB - 1) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        if constexpr (NLIVE * CB - 1 > NL)
+          __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - 1 - NL, 0);
+      }
+    };
+    // The barrier before the last k step of stage s publishes stage s+1
+    // (every wave has waited for its own loads of it; later stages may
+    // still be in flight) and frees slot s % NS, which then takes stage
+    // s+NS when there is one.
+    auto stage = [&](int s, bool refill) {
+      const int slot = s % NS;
+#pragma unroll
+      for (int kk = 0; kk + 1 < KK; ++kk) {
+        read_frags(slot, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+        mma(fa[kk & 1], fb[kk & 1]);
+        sched_step();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_lgkm0();
+      if (refill) wait_vmcnt<(NS - 2) * NL>();
+      else wait_vmcnt<0>();
+      wave_barrier_all();
+      read_frags((s + 1) % NS, 0, fa[0], fb[0]);
+      if (refill) issue(src, (cur.kt0 + s + NS) * SK, slot);
+      mma(fa[1], fb[1]);
+      sched_tail();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    wait_vmcnt<(NS - 1) * NL>();
+    wave_barrier_all();
+    read_frags(0, 0, fa[0], fb[0]);
+    int s = 0;
+    for (; s + NS < KT; ++s) stage(s, true);
+    for (; s + 1 < KT; ++s) stage(s, false);
+    const int slot = (KT - 1) % NS;
+#pragma unroll
+    for (int kk = 0; kk + 1 < KK; ++kk) {
+      read_frags(slot, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+      mma(fa[kk & 1], fb[kk & 1]);
+      sched_step();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    mma(fa[1], fb[1]);
+
+    // ---- epilogue (as moe_gemm_tiled_kernel): lane owns token row
+    // (lane & 31) of each 32-row block and, per 32-column block, columns
+    // 8*q + 4*(lane>>5) + {0..3} (accumulator registers 4q..4q+3).
+    {
+      const int ks = cur.ks;
+      const int64_t wbase = static_cast<int64_t>(cur.e) * p.nrows_w;
+      uint16_t* out = static_cast<uint16_t*>(p.out);
+      const int csub = 4 * (lane >> 5);
+      const float* wsc = INT8 ? p.w_scale + wbase : nullptr;
+      auto wscale4 = [&](int64_t wrow) -> f32x4 {
+        if constexpr (INT8) return *reinterpret_cast<const f32x4*>(wsc + wrow);
+        else return f32x4{1.f, 1.f, 1.f, 1.f};
+      };
+      auto value = [&](const Acc& a, int v, float sa, float sw) -> float {
+        if constexpr (INT8) return static_cast<float>(a[v]) * sa * sw;
+        else return a[v];
+      };
+      const float* bias = p.bias && (GEMM1 || ks == 0) ? p.bias + wbase : nullptr;
+      auto bias4 = [&](int64_t col) -> f32x4 {
+        return bias ? *reinterpret_cast<const f32x4*>(bias + col) : f32x4{0.f, 0.f, 0.f, 0.f};
+      };
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int rr = i * 64 + wm * 32 + (lane & 31);
+        const int r = row0 + rr;
+        const int sid = p.sorted_ids[r];
+        if (sid >= p.numel) continue;  // pad rows: never stored
+        const float sa = INT8 ? p.a_scale[act_row(row0, rr)] : 1.f;
+        if constexpr (GEMM1) {
+          const bool scale = p.weight_on_input != 0;
+          const float gamma = scale ? p.topk_w[sid] : 0.f;
+          uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
+#pragma unroll
+          for (int jb = 0; jb < CB / 2; ++jb) {
+            const int col0 = cur.ct * (BNR / 2) + wn * (WCOLS / 2) + jb * 32 + csub;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const f32x4 swg = wscale4(col0 + 8 * g4);
+              const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
+              const f32x4 bg = bias4(col0 + 8 * g4);
+              const f32x4 bu = bias4(p.n_out + col0 + 8 * g4);
+              uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                const uint32_t b = gemm1_epilogue(
+                    value(acc[i][jb], 4 * g4 + t, sa, swg[t]) + bg[t],
+                    value(acc[i][jb + CB / 2], 4 * g4 + t, sa, swu[t]) + bu[t], scale,
+                    gamma, kActSilu);
+                if (t < 2) w0 |= b << (16 * t);
+                else w1 |= b << (16 * (t - 2));
+              }
+              uint2 v2;
+              v2.x = w0;
+              v2.y = w1;
+              *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
+            }
+          }
+        } else if (p.ksplit > 1) {
+          float* orow = static_cast<float*>(p.out) +
+                        (static_cast<int64_t>(ks) * p.numel + sid) * p.n_out;
+#pragma unroll
+          for (int j = 0; j < CB; ++j) {
+            const int col0 = cur.ct * BNR + wn * WCOLS + j * 32 + csub;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const f32x4 sw = wscale4(col0 + 8 * g4);
+              const f32x4 bb = bias4(col0 + 8 * g4);
+              const int v = 4 * g4;
+              *reinterpret_cast<f32x4*>(orow + col0 + 8 * g4) =
+                  f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0],
+                        value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
+                        value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                        value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
+            }
+          }
+        } else {
+          uint16_t* orow = out + static_cast<int64_t>(sid) * p.n_out;
+#pragma unroll
+          for (int j = 0; j < CB; ++j) {
+            const int col0 = cur.ct * BNR + wn * WCOLS + j * 32 + csub;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const f32x4 sw = wscale4(col0 + 8 * g4);
+              const f32x4 bb = bias4(col0 + 8 * g4);
+              const int v = 4 * g4;
+              uint2 v2;
+              v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
+                                 value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
+              v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                                 value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
+              *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
+            }
+          }
+        }
+      }
+    }
+  };
+  dispatch_count<RB>(nlive, tile_body);
+}
+
+// Whether the 4-wave kernel covers a launch: bf16 / int8, GEMM1 with
+// the silu activation and no bias (gelu and the swiglu bias variant keep the
+// 8-wave kernel), k split into >= NS stages per split, output tiles that
+// divide n_out, and operands whose byte offsets fit the 32-bit buffer
+// addressing.
+bool wide_supported(int dt, bool gemm1, const GemmParams& p) {
+  using C = WideRing;
+  if (dt != kDtBf16 && dt != kDtInt8) return false;
+  if (gemm1 && (p.act != kActSilu || p.bias != nullptr)) return false;
+  const int64_t esz = dt == kDtBf16 ? 2 : 1;
+  const int64_t row_bytes = p.kdim * esz;
+  if (row_bytes % C::SK != 0) return false;
+  const int ks = std::max(1, gemm1 ? 1 : p.ksplit);
+  if (row_bytes / C::SK < static_cast<int64_t>(C::NS) * ks) return false;
+  if (p.n_out % (gemm1 ? C::BNR / 2 : C::BNR) != 0) return false;
+  constexpr int64_t kMax = (int64_t{1} << 31) - 1;
+  return p.a_rows > 0 && p.a_rows * row_bytes <= kMax && p.nrows_w * row_bytes <= kMax;
+}
+
+// FGS_MOE_WIDE_GROUPN overrides the column-group width of the tile walk
+// (default 8; a tuning aid, read once).
+static int wide_group_n_choice() {
+  static const int g = [] {
+    const char* s = getenv("FGS_MOE_WIDE_GROUPN");
+    const int v = s ? atoi(s) : 8;
+    return (v >= 1 && v <= 64) ? v : 8;
+  }();
+  return g;
+}
+
+template <int DT, bool GEMM1>
+static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream) {
+  using C = WideRing;
+  auto kern = moe_gemm_wide_kernel<DT, GEMM1, C>;
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [&] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+  });
+  if (attr != hipSuccess)
+    return fail(FGS_ELAUNCH, std::string("wide GEMM LDS opt-in: ") + hipGetErrorString(attr));
+  GemmParams q = p;
+  q.row_blocks = row_blocks;
+  if (GEMM1 || q.ksplit < 1) q.ksplit = 1;
+  if (q.group_n < 1) q.group_n = wide_group_n_choice();
+  // enough positions for the largest XCD walk the kernel can form from the
+  // launched row blocks (it splits the live ones, known on the device)
+  const int n_ct = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
+  const int64_t total = static_cast<int64_t>(row_blocks) * q.ksplit * n_ct;
+  const int64_t n_rb = (total + 7) / 8 / n_ct + 2;
+  const int64_t n_pos = (n_ct + q.group_n - 1) / q.group_n * n_rb * q.group_n;
+  const int grid = static_cast<int>(8 * n_pos);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(C::NW * 64), C::LDS_BYTES, stream, q);
+  return check_launch("moe_gemm_wide_kernel");
+}
+
+int launch_gemm_wide(int dt, bool gemm1, const GemmParams& p, int row_blocks,
+                     hipStream_t stream) {
+  if (!wide_supported(dt, gemm1, p))
+    return fail(FGS_EINVAL, "wide GEMM: launch not covered by the 4-wave kernel");
+  if (row_blocks <= 0) return FGS_OK;
+  if (dt == kDtBf16)
+    return gemm1 ? launch_wide_t<kDtBf16, true>(p, row_blocks, stream)
+                 : launch_wide_t<kDtBf16, false>(p, row_blocks, stream);
+  return gemm1 ? launch_wide_t<kDtInt8, true>(p, row_blocks, stream)
+               : launch_wide_t<kDtInt8, false>(p, row_blocks, stream);
+}
+
+}  // namespace fgs

@@ -51,6 +51,8 @@ struct Plan {
   int kw1, kw2;    // waves splitting the contraction of GEMM1 / GEMM2
   bool tiled;      // LDS-tiled MFMA kernels (prefill) instead of streaming
   int tile_cfg;    // tiled kernel configuration
+  int tile_cfg2;   // GEMM2's configuration (rows per block <= block_m)
+  int eid_shift2;  // log2(block_m / GEMM2 block rows)
   int ksplit2;     // GEMM2 k splits (tiled only; > 1 -> fp32 partials)
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
@@ -117,7 +119,17 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   if (p.tiled) {
     p.tile_cfg = forced_cfg >= 0 ? forced_cfg : tiled_config_for(p.dt, rows_per_expert);
     p.block_m = tiled_block_m(p.tile_cfg);
-    p.ksplit2 = pick_ksplit(numel, e, p.block_m, hidden, inter * esz);
+    // fp8 GEMM2 runs its 128-row kernel on 256-row blocks (as two halves,
+    // the all-pad ones skipped): the 256-row fp8 tile spans only 128 weight
+    // rows, so GEMM2 would re-read each activation tile for twice as many
+    // column tiles
+    p.tile_cfg2 = p.tile_cfg;
+    p.eid_shift2 = 0;
+    if (p.dt == kDtFp8 && p.tile_cfg == 0 && forced_cfg < 0) {
+      p.tile_cfg2 = 1;
+      p.eid_shift2 = 1;
+    }
+    p.ksplit2 = pick_ksplit(numel, e, tiled_block_m(p.tile_cfg2), hidden, inter * esz);
   }
   const int step = stream_step_k(p.dt);
   p.kw1 = pick_kw(hidden, step, 4);
@@ -175,7 +187,8 @@ static int validate(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   if (((flags & FGS_FLAG_TILE_MASK) >> 12) > kTiledConfigs)
     return fail(FGS_EINVAL, "unknown FGS_FLAG_TILE configuration");
   const int64_t numel = m * topk;
-  if (numel + static_cast<int64_t>(e) * 64 >= (int64_t(1) << 31))
+  // padded slots (alignment blocks of up to 256 rows) must fit int32 ids
+  if (numel + static_cast<int64_t>(e) * 256 >= (int64_t(1) << 31))
     return fail(FGS_EUNSUPPORTED, "m * topk too large for int32 slot ids");
   const int dt = qmode == FGS_QMODE_FP8_BLOCK ? kDtFp8
                  : qmode == FGS_QMODE_INT8_CHANNEL ? kDtInt8 : kDtBf16;
@@ -190,6 +203,9 @@ static int validate(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
                                       std::to_string(step));
   if ((inter / 16) > 65535 || (hidden / 16) > 65535)
     return fail(FGS_EUNSUPPORTED, "hidden / inter too large");
+  if (dt == kDtInt8 && (hidden > 512 * kInt8QuantMaxVec || inter > 512 * kInt8QuantMaxVec))
+    return fail(FGS_EUNSUPPORTED, "int8 w8a8: hidden and inter must be <= " +
+                                      std::to_string(512 * kInt8QuantMaxVec));
   if (check_ws) {
     Plan p;
     make_plan(m, hidden, inter, e, topk, qmode, flags, &p);
@@ -346,14 +362,14 @@ static int run_fused(const FusedArgs& a) {
     // only the padded rows in use (num_tokens_post_padded, on the device)
     rc = launch_quant_fp8_group(a2, ws + p.o_a2q,
                                 reinterpret_cast<float*>(ws + p.o_a2s),
-                                p.max_padded, a.inter, 128, a.stream, npp);
+                                p.max_padded, a.inter, 128, a.stream, npp, sorted, numel);
     if (rc) return rc;
     act2 = ws + p.o_a2q;
     act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
   } else if (p.dt == kDtInt8) {
     rc = launch_quant_int8_token(a2, reinterpret_cast<int8_t*>(ws + p.o_a2q),
                                  reinterpret_cast<float*>(ws + p.o_a2s),
-                                 p.max_padded, a.inter, a.stream, npp);
+                                 p.max_padded, a.inter, a.stream, npp, sorted, numel);
     if (rc) return rc;
     act2 = ws + p.o_a2q;
     act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
@@ -372,8 +388,9 @@ static int run_fused(const FusedArgs& a) {
   g2.nrows_w = a.hidden;
   g2.ksplit = p.ksplit2;
   g2.a_rows = p.max_padded;
-  rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, false, g2, static_cast<int>(p.n_launch),
-                                   a.stream)
+  g2.eid_shift = p.tiled ? p.eid_shift2 : 0;
+  rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg2, false, g2,
+                                   static_cast<int>(p.n_launch << p.eid_shift2), a.stream)
                : launch_gemm_stream(p.dt, false, g2, p.mt, p.kw2,
                                     static_cast<int>(p.n_launch), a.stream);
   if (rc) return rc;
@@ -497,6 +514,9 @@ int32_t fgs_moe_quant_int8_token(const void* x, int8_t* q, float* scales,
                                  int64_t rows, int64_t cols, void* stream) {
   if (rows < 0 || cols <= 0) return fail(FGS_EINVAL, "rows >= 0 and cols > 0 required");
   if (cols % 8) return fail(FGS_EUNSUPPORTED, "cols must be a multiple of 8");
+  if (cols > 512 * kInt8QuantMaxVec)
+    return fail(FGS_EUNSUPPORTED,
+                "cols must be <= " + std::to_string(512 * kInt8QuantMaxVec));
   if (rows > 0 && (!x || !q || !scales))
     return fail(FGS_EINVAL, "null pointer argument");
   if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(q) % 8)

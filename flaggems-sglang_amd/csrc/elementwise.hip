@@ -2,7 +2,10 @@
 // the dynamic activation quantisers. Every thread moves 16-byte vectors;
 // a row is processed by consecutive threads so each wave touches one or two
 // contiguous 1 KiB spans per instruction.
-#include "fgs_common.h"
+#include <string>
+#include <type_traits>
+
+#include "fgs_moe_kernels.h"
 
 namespace fgs {
 
@@ -122,18 +125,20 @@ __global__ __launch_bounds__(256) void moe_sum_partials_kernel(
 // butterfly shuffles, so a wave covers 512 columns.
 // scale = max(amax, 1e-10) / 448; q = e4m3fn(clamp(x / scale, +-448)).
 // With `rows_dev` given, rows >= *rows_dev are skipped (padded-row buffers
-// whose live prefix is only known on the device).
+// whose live prefix is only known on the device); with `sorted_ids` given,
+// so are the pad rows (sorted_ids[r] >= numel), which no GEMM reads.
 __global__ __launch_bounds__(256) void quant_fp8_group_kernel(
     const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
     float* __restrict__ scales, int64_t rows, int64_t cols, int group,
-    const int32_t* __restrict__ rows_dev) {
+    const int32_t* __restrict__ rows_dev, const int32_t* __restrict__ sorted_ids,
+    int64_t numel) {
   const int lane = threadIdx.x & 63;
   const int lanes_per_group = group / 8;
   const int64_t vec_per_row = cols / 8;
   const int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   const int64_t r = v / vec_per_row;
   const int64_t live_rows = rows_dev ? min(rows, static_cast<int64_t>(*rows_dev)) : rows;
-  const bool active = r < live_rows;
+  const bool active = r < live_rows && (!sorted_ids || sorted_ids[r] < numel);
   const int64_t c = (v - r * vec_per_row) * 8;
   float f[8];
   float amax = 0.f;
@@ -170,39 +175,50 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(
 }
 
 // ----------------------------------------------------- int8 token quant ---
-// One workgroup (256 threads) per row; cols % 8 == 0. With `rows_dev`
-// given, rows >= *rows_dev are skipped.
+constexpr int64_t kInt8WaveRows = 1024;  // rows from which a wave takes a row
+// One wave per row (4 rows per workgroup), the row held in registers: NV
+// vectors of 8 columns per lane (cols <= 512 * NV, cols % 8 == 0), one read
+// of x. With `rows_dev` given, rows >= *rows_dev are skipped; with
+// `sorted_ids` given, so are the pad rows (sorted_ids[r] >= numel).
 // scale = max(amax, 1e-10) / 127; q = clamp(rne(x / scale), -127, 127).
+template <int NV>
 __global__ __launch_bounds__(256) void quant_int8_token_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q,
-    float* __restrict__ scales, int64_t cols, const int32_t* __restrict__ rows_dev) {
-  const int64_t r = blockIdx.x;
-  if (rows_dev && r >= *rows_dev) return;
+    float* __restrict__ scales, int64_t rows, int64_t cols,
+    const int32_t* __restrict__ rows_dev, const int32_t* __restrict__ sorted_ids,
+    int64_t numel) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows || (rows_dev && r >= *rows_dev)) return;
+  if (sorted_ids && sorted_ids[r] >= numel) return;
   const uint16_t* src = x + r * cols;
   int8_t* dst = q + r * cols;
+  u32x4 w[NV];
   float amax = 0.f;
-  for (int64_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(src + c);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      amax = fmaxf(amax, fabsf(__uint_as_float(w[j] << 16)));
-      amax = fmaxf(amax, fabsf(__uint_as_float(w[j] & 0xffff0000u)));
+  for (int v = 0; v < NV; ++v) {
+    const int64_t c = (static_cast<int64_t>(v) * 64 + lane) * 8;
+    if (c < cols) {
+      w[v] = *reinterpret_cast<const u32x4*>(src + c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        amax = fmaxf(amax, fabsf(__uint_as_float(w[v][j] << 16)));
+        amax = fmaxf(amax, fabsf(__uint_as_float(w[v][j] & 0xffff0000u)));
+      }
     }
   }
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
-  __shared__ float red[4];
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float scale = fmaxf(amax, 1e-10f) / 127.0f;
-  for (int64_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(src + c);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int64_t c = (static_cast<int64_t>(v) * 64 + lane) * 8;
+    if (c >= cols) continue;
     uint32_t packed[2] = {0, 0};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float f = (j & 1) ? __uint_as_float(w[j / 2] & 0xffff0000u)
-                              : __uint_as_float(w[j / 2] << 16);
+      const float f = (j & 1) ? __uint_as_float(w[v][j / 2] & 0xffff0000u)
+                              : __uint_as_float(w[v][j / 2] << 16);
       float rq = __builtin_rintf(f / scale);
       rq = fminf(fmaxf(rq, -127.f), 127.f);
       const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(rq)) & 0xffu;
@@ -213,7 +229,7 @@ __global__ __launch_bounds__(256) void quant_int8_token_kernel(
     o.y = packed[1];
     *reinterpret_cast<uint2*>(dst + c) = o;
   }
-  if (threadIdx.x == 0) scales[r] = scale;
+  if (lane == 0) scales[r] = scale;
 }
 
 // ------------------------------------------------------------- launchers ---
@@ -267,24 +283,105 @@ int launch_moe_sum_partials(const float* part, int nsplit, void* out, int64_t m,
   return check_launch("moe_sum_partials_kernel");
 }
 
+// Few rows (under kInt8WaveRows): a workgroup of 256 threads per row, two
+// passes over the row (amax, then quantise), for parallelism at small M.
+__global__ __launch_bounds__(256) void quant_int8_token_wg_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+    float* __restrict__ scales, int64_t cols, const int32_t* __restrict__ rows_dev,
+    const int32_t* __restrict__ sorted_ids, int64_t numel) {
+  const int64_t r = blockIdx.x;
+  if (rows_dev && r >= *rows_dev) return;
+  if (sorted_ids && sorted_ids[r] >= numel) return;
+  const uint16_t* src = x + r * cols;
+  int8_t* dst = q + r * cols;
+  float amax = 0.f;
+  for (int64_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(src + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      amax = fmaxf(amax, fabsf(__uint_as_float(w[j] << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(w[j] & 0xffff0000u)));
+    }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float scale = fmaxf(amax, 1e-10f) / 127.0f;
+  for (int64_t c = threadIdx.x * 8; c < cols; c += 256 * 8) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(src + c);
+    uint32_t packed[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = (j & 1) ? __uint_as_float(w[j / 2] & 0xffff0000u)
+                              : __uint_as_float(w[j / 2] << 16);
+      float rq = __builtin_rintf(f / scale);
+      rq = fminf(fmaxf(rq, -127.f), 127.f);
+      const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(rq)) & 0xffu;
+      packed[j / 4] |= b << (8 * (j & 3));
+    }
+    uint2 o;
+    o.x = packed[0];
+    o.y = packed[1];
+    *reinterpret_cast<uint2*>(dst + c) = o;
+  }
+  if (threadIdx.x == 0) scales[r] = scale;
+}
+
+// Calls f(std::integral_constant<int, n>) for a runtime n in [0, N].
+template <int N, class F>
+static void dispatch_nv(int n, F&& f) {
+  if constexpr (N >= 0) {
+    if (n == N) {
+      f(std::integral_constant<int, N>{});
+      return;
+    }
+    dispatch_nv<N - 1>(n, f);
+  }
+}
+
 int launch_quant_fp8_group(const void* x, void* q, float* scales,
                            int64_t rows, int64_t cols, int group,
-                           hipStream_t stream, const int32_t* rows_dev) {
+                           hipStream_t stream, const int32_t* rows_dev,
+                           const int32_t* sorted_ids, int64_t numel) {
   const int64_t vecs = rows * (cols / 8);
   if (vecs == 0) return FGS_OK;
   hipLaunchKernelGGL(quant_fp8_group_kernel, dim3(static_cast<unsigned>((vecs + 255) / 256)),
                      dim3(256), 0, stream, static_cast<const uint16_t*>(x),
-                     static_cast<uint8_t*>(q), scales, rows, cols, group, rows_dev);
+                     static_cast<uint8_t*>(q), scales, rows, cols, group, rows_dev,
+                     sorted_ids, numel);
   return check_launch("quant_fp8_group_kernel");
 }
 
 int launch_quant_int8_token(const void* x, int8_t* q, float* scales,
                             int64_t rows, int64_t cols, hipStream_t stream,
-                            const int32_t* rows_dev) {
+                            const int32_t* rows_dev, const int32_t* sorted_ids,
+                            int64_t numel) {
   if (rows == 0) return FGS_OK;
-  hipLaunchKernelGGL(quant_int8_token_kernel, dim3(static_cast<unsigned>(rows)),
-                     dim3(256), 0, stream, static_cast<const uint16_t*>(x), q,
-                     scales, cols, rows_dev);
+  if (cols > 512 * kInt8QuantMaxVec)
+    return fail(FGS_EUNSUPPORTED, "int8 token quantiser: more than " +
+                                      std::to_string(512 * kInt8QuantMaxVec) + " columns");
+  const uint16_t* xs = static_cast<const uint16_t*>(x);
+  if (rows < kInt8WaveRows) {
+    hipLaunchKernelGGL(quant_int8_token_wg_kernel, dim3(static_cast<unsigned>(rows)),
+                       dim3(256), 0, stream, xs, q, scales, cols, rows_dev, sorted_ids,
+                       numel);
+    return check_launch("quant_int8_token_wg_kernel");
+  }
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  const int nv = static_cast<int>((cols + 511) / 512);
+  bool launched = false;
+  dispatch_nv<kInt8QuantMaxVec>(nv, [&](auto nv_c) {
+    constexpr int NV = decltype(nv_c)::value;
+    if constexpr (NV >= 1) {
+      hipLaunchKernelGGL(quant_int8_token_kernel<NV>, grid, dim3(256), 0, stream, xs, q,
+                         scales, rows, cols, rows_dev, sorted_ids, numel);
+      launched = true;
+    }
+  });
+  if (!launched) return fail(FGS_EINVAL, "int8 token quantiser: bad column count");
   return check_launch("quant_int8_token_kernel");
 }
 

@@ -37,6 +37,7 @@ struct GemmParams {
   float alpha, limit;     // swiglu parameters
   const float* bias;      // fp32 per expert: GEMM1 [E, 2N] (gate | up), GEMM2 [E, K]; or null
   int64_t a_rows;         // rows of `a` (GEMM1: tokens; GEMM2: padded rows)
+  int32_t eid_shift;      // tiled: row block rb belongs to alignment block rb >> eid_shift
 };
 
 // Router gating (scores -> top-k -> renormalise), one wave per token;
@@ -71,13 +72,18 @@ int launch_moe_sum_partials(const float* part, int nsplit, void* out, int64_t m,
                             int num_experts, const float* weights,
                             hipStream_t stream);
 // Activation quantisers; with `rows_dev` given only rows < *rows_dev (a
-// device-side count such as num_tokens_post_padded) are processed.
+// device-side count such as num_tokens_post_padded) are processed, and with
+// `sorted_ids` given the pad rows (sorted_ids[r] >= numel) are skipped.
+// The int8 quantiser takes at most 512 * kInt8QuantMaxVec columns.
+constexpr int kInt8QuantMaxVec = 16;
 int launch_quant_fp8_group(const void* x, void* q, float* scales, int64_t rows,
                            int64_t cols, int group, hipStream_t stream,
-                           const int32_t* rows_dev = nullptr);
+                           const int32_t* rows_dev = nullptr,
+                           const int32_t* sorted_ids = nullptr, int64_t numel = 0);
 int launch_quant_int8_token(const void* x, int8_t* q, float* scales,
                             int64_t rows, int64_t cols, hipStream_t stream,
-                            const int32_t* rows_dev = nullptr);
+                            const int32_t* rows_dev = nullptr,
+                            const int32_t* sorted_ids = nullptr, int64_t numel = 0);
 
 // k elements per pipeline step of the streaming kernels (kdim must be a
 // multiple of it).

@@ -129,8 +129,9 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   static_assert(!GEMM1 || CB % 2 == 0, "gate/up pairing");
   static_assert(tiled_lds_bytes<DT, C>() <= 160 * 1024, "gfx950 LDS is 160 KiB");
   // fp8: one stage is one 128-wide k block of the block scales, and a tile's
-  // weight rows span whole 128-row scale blocks
-  static_assert(!FP8 || (SK == 128 && BNR % 256 == 0 && BM + 4 <= NW * 64), "fp8 tile");
+  // weight rows (GEMM1: each of its gate and up halves) lie in whole 128-row
+  // scale blocks or inside one
+  static_assert(!FP8 || (SK == 128 && BNR % 128 == 0 && BM + 4 <= NW * 64), "fp8 tile");
 
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
@@ -144,8 +145,11 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   const int ks = rb_id / p.row_blocks;
   rb_id -= ks * p.row_blocks;
   if (rb_id * BM >= p.num_post_pad[0]) return;
-  const int e = p.expert_ids[rb_id];
+  // row blocks smaller than the alignment block (eid_shift > 0): the expert
+  // of the enclosing block; a block that is all padding has nothing to do
+  const int e = p.expert_ids[rb_id >> p.eid_shift];
   if (e < 0) return;
+  if (p.eid_shift > 0 && p.sorted_ids[rb_id * BM] >= p.numel) return;
 
   const int lane = threadIdx.x & 63;
   // wave index in an SGPR: LDS-DMA destinations (M0) then stay scalar
@@ -555,8 +559,9 @@ using Cfg128 = TileCfg<128, 256, 2, 4, 128, 3>;  // 8 waves of 64x64
 using Cfg64 = TileCfg<64, 256, 1, 4, 128, 4>;   // 4 waves of 64x64
 using Cfg32 = TileCfg<32, 256, 1, 4, 128, 4>;   // 4 waves of 32x64
 // fp8 keeps a second accumulator set per k block (the block-scale fold), so
-// it has no 256-row configuration, and the stage scale area costs a stage
-// at 64 and 32 rows.
+// its 256-row configuration has 64x64 wave tiles over 128 weight rows, and
+// the stage scale area costs a stage at 64 and 32 rows.
+using Fp8Cfg256 = TileCfg<256, 128, 4, 2, 128, 3>;  // 8 waves of 64x64
 using Fp8Cfg64 = TileCfg<64, 256, 1, 4, 128, 3>;
 using Fp8Cfg32 = TileCfg<32, 256, 1, 4, 128, 3>;
 
@@ -575,16 +580,22 @@ static int forced_tile() {
 }
 
 int tiled_config_supported(int dt, int cfg) {
-  return cfg >= 0 && cfg < kTiledConfigs && !(dt == kDtFp8 && cfg == 0);
+  (void)dt;
+  return cfg >= 0 && cfg < kTiledConfigs;
 }
 
+// From about 112 rows per expert a noticeable share of the experts would
+// spill into a second, mostly empty 128-row block that streams the expert's
+// weights again; 256-row blocks read each weight tile once per expert and
+// skip the MFMAs of their all-pad 32-row blocks.
 int tiled_config_for(int dt, double rows_per_expert) {
+  (void)dt;
   int c = 3;
-  if (rows_per_expert >= 192) c = 0;
+  if (rows_per_expert >= 112) c = 0;
   else if (rows_per_expert >= 96) c = 1;
   else if (rows_per_expert >= 24) c = 2;
   if (forced_tile() >= 0) c = forced_tile();
-  return (dt == kDtFp8 && c == 0) ? 1 : c;
+  return c;
 }
 
 int tiled_block_m(int cfg) { return kTileRows[cfg]; }
@@ -625,6 +636,7 @@ int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
       }
     case kDtFp8:
       switch (cfg) {
+        case 0: return launch_cfg<kDtFp8, Fp8Cfg256>(gemm1, p, row_blocks, stream);
         case 1: return launch_cfg<kDtFp8, Cfg128>(gemm1, p, row_blocks, stream);
         case 2: return launch_cfg<kDtFp8, Fp8Cfg64>(gemm1, p, row_blocks, stream);
         default: return launch_cfg<kDtFp8, Fp8Cfg32>(gemm1, p, row_blocks, stream);

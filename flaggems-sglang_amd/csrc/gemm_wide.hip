@@ -434,6 +434,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
 bool wide_supported(int dt, bool gemm1, const GemmParams& p) {
   using C = WideRing;
   if (dt != kDtBf16 && dt != kDtInt8) return false;
+  if (p.eid_shift != 0) return false;  // row blocks are whole alignment blocks
   if (gemm1 && (p.act != kActSilu || p.bias != nullptr)) return false;
   const int64_t esz = dt == kDtBf16 ? 2 : 1;
   const int64_t row_bytes = p.kdim * esz;

@@ -137,8 +137,9 @@ int32_t fgs_moe_quant_fp8_group(const void* x, void* q, float* scales,
 
 /* Dynamic per-row int8 quantisation: scale = max(amax, 1e-10) / 127,
  * q = clamp(rne(x / scale), -127, 127). x bf16 [rows, cols], q int8,
- * scales f32 [rows]. No reference counterpart (ops/fused_moe.py:173-175
- * asserts per-channel quant off); needed by the int8 w8a8 path. */
+ * scales f32 [rows]; cols a multiple of 8 and at most 8192 (else -2).
+ * No reference counterpart (ops/fused_moe.py:173-175 asserts per-channel
+ * quant off); needed by the int8 w8a8 path. */
 int32_t fgs_moe_quant_int8_token(const void* x, int8_t* q, float* scales,
                                  int64_t rows, int64_t cols, void* stream);
 
@@ -216,7 +217,8 @@ int32_t fgs_moe_fused_fp8_block(const void* x, const void* w13,
 /* Fused MoE, int8 w8a8 with per-output-channel weight scales.
  *   w13 int8 [E, 2*inter, hidden], w13_scale f32 [E, 2*inter]
  *   w2  int8 [E, hidden, inter],   w2_scale  f32 [E, hidden]
- * Activations are quantised dynamically per token (row) inside the call.
+ * Activations are quantised dynamically per token (row) inside the call;
+ * hidden and inter at most 8192 (else -2).
  * No reference counterpart (per_channel_quant asserted off,
  * ops/fused_moe.py:173-175). */
 int32_t fgs_moe_fused_int8_channel(const void* x, const void* w13,

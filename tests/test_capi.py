@@ -59,11 +59,13 @@ def test_align_max_padded():
         ((1, 4096, 14336, 8, 2, 0, 0x100 | 0x1000), _capi.FGS_EINVAL, "excludes"),
         ((1, 4096, 14336, 8, 2, 0, 0x5000), _capi.FGS_EINVAL, "TILE"),
         ((1, 4096, 14336, 8, 2, 0, 0x4000), 0, ""),
-        ((1, 7168, 2048, 256, 8, 1, 0x1000), _capi.FGS_EUNSUPPORTED, "not available"),
+        ((1, 7168, 2048, 256, 8, 1, 0x1000), 0, ""),
         ((1, 7168, 2048, 256, 8, 1, 0x2000), 0, ""),
         ((1, 4000, 14336, 8, 2, 0, 0), _capi.FGS_EUNSUPPORTED, "multiples"),
         ((1, 3584, 2560, 64, 8, 2, 0), 0, ""),
         ((1, 3584 - 128, 2560, 64, 8, 2, 0), _capi.FGS_EUNSUPPORTED, "multiples"),
+        ((1, 9216, 2560, 64, 8, 2, 0), _capi.FGS_EUNSUPPORTED, "<= 8192"),
+        ((1, 9216, 2560, 64, 8, 0, 0), 0, ""),
     ],
 )
 def test_validate(args, code, msg):
@@ -118,6 +120,8 @@ def test_entry_points_reject_bad_arguments_before_launch():
     assert lib.fgs_moe_sum(nul, nul, 4, 0, 16, nul) == -1
     assert lib.fgs_moe_quant_fp8_group(nul, nul, nul, 4, 256, 100, nul) == -2
     assert lib.fgs_moe_quant_int8_token(nul, nul, nul, 4, 12, nul) == -2
+    assert lib.fgs_moe_quant_int8_token(nul, nul, nul, 4, 8200, nul) == -2
+    assert "<= 8192" in _capi.last_error()
     need = lib.fgs_moe_workspace_bytes(4, 256, 128, 4, 2, 0, 0)
     rc = lib.fgs_moe_fused_bf16(nul, nul, nul, nul, nul, 4, 256, 128, 4, 2, 0,
                                 nul, need, nul, nul)

@@ -126,7 +126,7 @@ def test_tiled_configs(gpu, shape, cfg):
     _check(res.cpu()[toks], ref, "bf16", f"tile {cfg} {shape}")
 
 
-_QUANT_TILES = [("fp8", c) for c in range(1, _capi.TILED_CONFIGS)] + \
+_QUANT_TILES = [("fp8", c) for c in range(_capi.TILED_CONFIGS)] + \
                [("int8", c) for c in range(_capi.TILED_CONFIGS)]
 
 

@@ -129,7 +129,8 @@ def test_quant_fp8_group_bit_exact(gpu, rows, cols, group):
     assert torch.equal(q.cpu().view(torch.uint8), rq.view(torch.uint8))
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 128), (37, 3584), (300, 2560)])
+@pytest.mark.parametrize("rows,cols", [(1, 128), (37, 3584), (300, 2560), (5, 520),
+                                       (9, 8192), (1030, 520), (2048, 8192)])
 def test_quant_int8_token_bit_exact(gpu, rows, cols):
     g = torch.Generator().manual_seed(rows + cols)
     x = (torch.randn(rows, cols, generator=g) * 2).to(torch.bfloat16)

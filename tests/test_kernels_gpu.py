@@ -28,6 +28,9 @@ ALIGN_CASES = [
     (1, 8, 128, 64), (16, 8, 128, 64), (256, 8, 128, 64), (2048, 8, 128, 64),
     (8192, 8, 128, 64), (4096, 8, 256, 16), (1024, 8, 64, 32),
     (300, 3, 1024, 16), (5, 1, 1, 7), (8192, 2, 8, 128),
+    # decode sizes around the one-wave kernel's limit of 64 slots
+    (8, 8, 256, 16), (3, 8, 256, 64), (4, 8, 64, 32), (32, 2, 8, 256),
+    (13, 5, 64, 8),
 ]
 
 
@@ -60,6 +63,21 @@ def test_align_qwen3_skewed_block64(gpu, skew):
         assert int(npp.item()) == rnpp, M
         assert np.array_equal(s.cpu().numpy(), rs), M
         assert np.array_equal(eids.cpu().numpy(), reids), M
+
+
+@pytest.mark.parametrize("numel", [64, 63, 65])
+def test_align_small_dropped_ids(gpu, numel):
+    """Decode-sized inputs with dropped (-1) and out-of-range ids, one expert
+    holding most slots, against the oracle."""
+    g = np.random.default_rng(numel)
+    raw = g.integers(-1, 20, size=(numel,), dtype=np.int32)  # E = 16: 16..19 out of range
+    raw[::3] = 5
+    ids = torch.from_numpy(raw.reshape(numel, 1))
+    s, eids, npp = fm.moe_align_block_size(ids.to(gpu), 16, 8)
+    rs, reids, rnpp = moe_ref.align(raw.reshape(numel, 1), 16, 8)
+    assert int(npp.item()) == rnpp
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(eids.cpu().numpy(), reids)
 
 
 def test_align_edge_cases(gpu):

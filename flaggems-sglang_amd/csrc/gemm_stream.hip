@@ -176,6 +176,23 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 
   u32x4 bf[2][NB][NV];
   u32x4 af[2][MT][NV];
+  // fp8 block scales of a step (one 128-k group), fetched with its operands
+  float sw[2][NB], sa[2][MT][4];
+  auto load_scales = [&](int buf, int kb) {
+    if constexpr (DT == kDtFp8) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int64_t wrow = (nb ? p.n_out : 0) + n0;
+        sw[buf][nb] = p.w_scale[(static_cast<int64_t>(e) * (p.nrows_w / 128) +
+                                 wrow / 128) * kblocks + kb];
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sa[buf][mt][i] = cvalid[mt][i] ? p.a_scale[crow[mt][i] * kblocks + kb] : 0.f;
+    }
+  };
   if (s0 < s1) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -183,6 +200,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
       load_act(af[0][mt], arow[mt] + s0 * step_bytes, avalid[mt]);
+    load_scales(0, s0);
   }
   for (int s = s0; s < s1; s += 2) {
     // Two-deep register pipeline: fetch s+1 while s is multiplied.
@@ -198,6 +216,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           load_act(af[h ^ 1][mt], arow[mt] + nxt * step_bytes, avalid[mt]);
+        load_scales(h ^ 1, nxt);
       }
       if constexpr (DT == kDtBf16) {
 #pragma unroll
@@ -212,26 +231,15 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
           for (int mt = 0; mt < MT; ++mt)
             mma_step_i8<DT>(acc[nb][mt], af[h][mt], bf[h][nb]);
       } else {
-        // fp8 block scales: one 128-k group per step.
-        const int kb = cur;
-        float sw[NB];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const int64_t wrow = (nb ? p.n_out : 0) + n0;
-          sw[nb] = p.w_scale[(static_cast<int64_t>(e) * (p.nrows_w / 128) +
-                              wrow / 128) * kblocks + kb];
-        }
+        // fp8 block scales: one 128-k group per step (fetched a step ahead).
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          float sa[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            sa[i] = cvalid[mt][i] ? p.a_scale[crow[mt][i] * kblocks + kb] : 0.f;
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
             const f32x4 t = mma_fp8(af[h][mt], bf[h][nb]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[nb][mt][i] += t[i] * (sa[i] * sw[nb]);
+            for (int i = 0; i < 4; ++i)
+              acc[nb][mt][i] += t[i] * (sa[h][mt][i] * sw[h][nb]);
           }
         }
       }

@@ -1,6 +1,7 @@
 // C ABI of libfgs_moe.so (declared in include/fgs_moe.h): host-side
 // validation, the kernel schedule of one fused-MoE call, the workspace
 // layout and the launch sequence. No device allocation, no synchronisation.
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -87,6 +88,17 @@ static int pick_ksplit(int64_t numel, int e, int bm, int64_t hidden,
   return best;
 }
 
+// FGS_MOE_KSPLIT (1..4) forces the tiled GEMM2's k split (a tuning aid;
+// read once).
+static int forced_ksplit() {
+  static const int k = [] {
+    const char* v = getenv("FGS_MOE_KSPLIT");
+    const int x = v ? atoi(v) : 0;
+    return (x >= 1 && x <= 4) ? x : 0;
+  }();
+  return k;
+}
+
 static int pick_kw(int64_t kdim, int step, int cap) {
   const int64_t steps = kdim / step;
   int kw = 1;
@@ -130,6 +142,9 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
       p.eid_shift2 = 1;
     }
     p.ksplit2 = pick_ksplit(numel, e, tiled_block_m(p.tile_cfg2), hidden, inter * esz);
+    // a forced split still keeps >= 8 LDS stages of k per split
+    if (forced_ksplit() > 0 && inter * esz / 128 >= 8 * forced_ksplit())
+      p.ksplit2 = forced_ksplit();
   }
   const int step = stream_step_k(p.dt);
   p.kw1 = pick_kw(hidden, step, 4);

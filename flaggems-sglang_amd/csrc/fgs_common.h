@@ -83,6 +83,35 @@ __device__ __forceinline__ uint16_t gemm1_epilogue(float g, float u, bool scale,
   return f32_to_bf16_bits(act == kActGelu ? gelu_mul(g, u) : silu_mul(g, u));
 }
 
+// Two f32 -> one word of two bf16 (round to nearest even), one
+// v_cvt_pk_bf16_f32.
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
+
+// gemm1_epilogue's silu path for two adjacent outputs, word-packed: the same
+// roundings (g and u to bf16, silu(g) * u in fp32, bf16 out) with the
+// conversions done pairwise.
+template <bool SCALE>
+__device__ __forceinline__ uint32_t silu_mul_bf16x2(float g0, float g1, float u0, float u1,
+                                                    float gamma) {
+  if (SCALE) {
+    g0 *= gamma;
+    g1 *= gamma;
+    u0 *= gamma;
+    u1 *= gamma;
+  }
+  const uint32_t gp = cvt_pk_bf16(g0, g1);
+  const uint32_t up = cvt_pk_bf16(u0, u1);
+  const float o0 = silu_mul(__builtin_bit_cast(float, gp << 16),
+                            __builtin_bit_cast(float, up << 16));
+  const float o1 = silu_mul(__builtin_bit_cast(float, gp & 0xffff0000u),
+                            __builtin_bit_cast(float, up & 0xffff0000u));
+  return cvt_pk_bf16(o0, o1);
+}
+
 // ------------------------------------------------------------------ MFMA ---
 // v_mfma_f32_16x16x32_bf16: A 16x32, B 32x16, C 16x16 fp32.
 // Lane l holds A row (l & 15) / B column (l & 15), eight consecutive

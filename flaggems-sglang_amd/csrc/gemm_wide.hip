@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "gemm_tiled_common.h"
 
@@ -348,80 +349,93 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
         if constexpr (INT8) return static_cast<float>(a[v]) * sa * sw;
         else return a[v];
       };
-      const float* bias = p.bias && (GEMM1 || ks == 0) ? p.bias + wbase : nullptr;
-      auto bias4 = [&](int64_t col) -> f32x4 {
-        return bias ? *reinterpret_cast<const f32x4*>(bias + col) : f32x4{0.f, 0.f, 0.f, 0.f};
-      };
+      if constexpr (GEMM1) {
+        // silu, no bias (the launch guarantees both); the router-weight
+        // scaling is a compile-time branch so the common case carries no
+        // per-element select
+        auto emit = [&](auto scale_c) {
+          constexpr bool SCALE = decltype(scale_c)::value;
 #pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const int rr = i * 64 + wm * 32 + (lane & 31);
-        const int r = row0 + rr;
-        const int sid = p.sorted_ids[r];
-        if (sid >= p.numel) continue;  // pad rows: never stored
-        const float sa = INT8 ? p.a_scale[act_row(row0, rr)] : 1.f;
-        if constexpr (GEMM1) {
-          const bool scale = p.weight_on_input != 0;
-          const float gamma = scale ? p.topk_w[sid] : 0.f;
-          uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
+          for (int i = 0; i < RB; ++i) {
+            const int rr = i * 64 + wm * 32 + (lane & 31);
+            const int r = row0 + rr;
+            const int sid = p.sorted_ids[r];
+            if (sid >= p.numel) continue;  // pad rows: never stored
+            const float sa = INT8 ? p.a_scale[act_row(row0, rr)] : 1.f;
+            const float gamma = SCALE ? p.topk_w[sid] : 1.f;
+            uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
 #pragma unroll
-          for (int jb = 0; jb < CB / 2; ++jb) {
-            const int col0 = cur.ct * (BNR / 2) + wn * (WCOLS / 2) + jb * 32 + csub;
+            for (int jb = 0; jb < CB / 2; ++jb) {
+              const int col0 = cur.ct * (BNR / 2) + wn * (WCOLS / 2) + jb * 32 + csub;
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-              const f32x4 swg = wscale4(col0 + 8 * g4);
-              const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
-              const f32x4 bg = bias4(col0 + 8 * g4);
-              const f32x4 bu = bias4(p.n_out + col0 + 8 * g4);
-              uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-              for (int t = 0; t < 4; ++t) {
-                const uint32_t b = gemm1_epilogue(
-                    value(acc[i][jb], 4 * g4 + t, sa, swg[t]) + bg[t],
-                    value(acc[i][jb + CB / 2], 4 * g4 + t, sa, swu[t]) + bu[t], scale,
-                    gamma, kActSilu);
-                if (t < 2) w0 |= b << (16 * t);
-                else w1 |= b << (16 * (t - 2));
+              for (int g4 = 0; g4 < 4; ++g4) {
+                const f32x4 swg = wscale4(col0 + 8 * g4);
+                const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
+                const Acc& ag = acc[i][jb];
+                const Acc& au = acc[i][jb + CB / 2];
+                const int v = 4 * g4;
+                uint2 v2;
+                v2.x = silu_mul_bf16x2<SCALE>(
+                    value(ag, v, sa, swg[0]), value(ag, v + 1, sa, swg[1]),
+                    value(au, v, sa, swu[0]), value(au, v + 1, sa, swu[1]), gamma);
+                v2.y = silu_mul_bf16x2<SCALE>(
+                    value(ag, v + 2, sa, swg[2]), value(ag, v + 3, sa, swg[3]),
+                    value(au, v + 2, sa, swu[2]), value(au, v + 3, sa, swu[3]), gamma);
+                *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
               }
-              uint2 v2;
-              v2.x = w0;
-              v2.y = w1;
-              *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
             }
           }
-        } else if (p.ksplit > 1) {
-          float* orow = static_cast<float*>(p.out) +
-                        (static_cast<int64_t>(ks) * p.numel + sid) * p.n_out;
+        };
+        if (p.weight_on_input) emit(std::true_type{});
+        else emit(std::false_type{});
+      } else {
+        const float* bias = p.bias && ks == 0 ? p.bias + wbase : nullptr;
+        auto bias4 = [&](int64_t col) -> f32x4 {
+          return bias ? *reinterpret_cast<const f32x4*>(bias + col)
+                      : f32x4{0.f, 0.f, 0.f, 0.f};
+        };
 #pragma unroll
-          for (int j = 0; j < CB; ++j) {
-            const int col0 = cur.ct * BNR + wn * WCOLS + j * 32 + csub;
+        for (int i = 0; i < RB; ++i) {
+          const int rr = i * 64 + wm * 32 + (lane & 31);
+          const int r = row0 + rr;
+          const int sid = p.sorted_ids[r];
+          if (sid >= p.numel) continue;  // pad rows: never stored
+          const float sa = INT8 ? p.a_scale[act_row(row0, rr)] : 1.f;
+          if (p.ksplit > 1) {
+            float* orow = static_cast<float*>(p.out) +
+                          (static_cast<int64_t>(ks) * p.numel + sid) * p.n_out;
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-              const f32x4 sw = wscale4(col0 + 8 * g4);
-              const f32x4 bb = bias4(col0 + 8 * g4);
-              const int v = 4 * g4;
-              *reinterpret_cast<f32x4*>(orow + col0 + 8 * g4) =
-                  f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0],
-                        value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
-                        value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
-                        value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
+            for (int j = 0; j < CB; ++j) {
+              const int col0 = cur.ct * BNR + wn * WCOLS + j * 32 + csub;
+#pragma unroll
+              for (int g4 = 0; g4 < 4; ++g4) {
+                const f32x4 sw = wscale4(col0 + 8 * g4);
+                const f32x4 bb = bias4(col0 + 8 * g4);
+                const int v = 4 * g4;
+                *reinterpret_cast<f32x4*>(orow + col0 + 8 * g4) =
+                    f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0],
+                          value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
+                          value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                          value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
+              }
             }
-          }
-        } else {
-          uint16_t* orow = out + static_cast<int64_t>(sid) * p.n_out;
+          } else {
+            uint16_t* orow = out + static_cast<int64_t>(sid) * p.n_out;
 #pragma unroll
-          for (int j = 0; j < CB; ++j) {
-            const int col0 = cur.ct * BNR + wn * WCOLS + j * 32 + csub;
+            for (int j = 0; j < CB; ++j) {
+              const int col0 = cur.ct * BNR + wn * WCOLS + j * 32 + csub;
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-              const f32x4 sw = wscale4(col0 + 8 * g4);
-              const f32x4 bb = bias4(col0 + 8 * g4);
-              const int v = 4 * g4;
-              uint2 v2;
-              v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
-                                 value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
-              v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
-                                 value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
-              *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
+              for (int g4 = 0; g4 < 4; ++g4) {
+                const f32x4 sw = wscale4(col0 + 8 * g4);
+                const f32x4 bb = bias4(col0 + 8 * g4);
+                const int v = 4 * g4;
+                uint2 v2;
+                v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
+                                   value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
+                v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                                   value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
+                *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
+              }
             }
           }
         }

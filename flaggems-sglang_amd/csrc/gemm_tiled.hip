@@ -426,6 +426,48 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   auto bias4 = [&](int64_t col) -> f32x4 {
     return bias ? *reinterpret_cast<const f32x4*>(bias + col) : f32x4{0.f, 0.f, 0.f, 0.f};
   };
+  // GEMM1 with silu and no bias (the common case): the router-weight
+  // scaling as a compile-time branch, no bias adds, pairwise conversions
+  if constexpr (GEMM1) {
+    if (p.act == kActSilu && bias == nullptr) {
+      auto emit = [&](auto scale_c) {
+        constexpr bool SCALE = decltype(scale_c)::value;
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          const int rr = wm * WROWS + i * 32 + (lane & 31);
+          const int r = row0 + rr;
+          const int sid = p.sorted_ids[r];
+          if (sid >= p.numel) continue;  // pad rows: never stored
+          const float sa = INT8 ? p.a_scale[act_row(rr)] : 1.f;
+          const float gamma = SCALE ? p.topk_w[sid] : 1.f;
+          uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
+#pragma unroll
+          for (int jb = 0; jb < CB / 2; ++jb) {
+            const int col0 = tile_n * (BNR / 2) + wn * (WCOLS / 2) + jb * 32 + csub;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const f32x4 swg = wscale4(col0 + 8 * g4);
+              const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
+              const Acc& ag = acc[i][jb];
+              const Acc& au = acc[i][jb + CB / 2];
+              const int v = 4 * g4;
+              uint2 v2;
+              v2.x = silu_mul_bf16x2<SCALE>(
+                  value(ag, v, sa, swg[0]), value(ag, v + 1, sa, swg[1]),
+                  value(au, v, sa, swu[0]), value(au, v + 1, sa, swu[1]), gamma);
+              v2.y = silu_mul_bf16x2<SCALE>(
+                  value(ag, v + 2, sa, swg[2]), value(ag, v + 3, sa, swg[3]),
+                  value(au, v + 2, sa, swu[2]), value(au, v + 3, sa, swu[3]), gamma);
+              *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
+            }
+          }
+        }
+      };
+      if (p.weight_on_input) emit(std::true_type{});
+      else emit(std::false_type{});
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < RB; ++i) {
     const int rr = wm * WROWS + i * 32 + (lane & 31);

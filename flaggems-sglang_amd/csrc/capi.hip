@@ -55,6 +55,10 @@ struct Plan {
   int tile_cfg2;   // GEMM2's configuration (rows per block <= block_m)
   int eid_shift2;  // log2(block_m / GEMM2 block rows)
   int ksplit2;     // GEMM2 k splits (tiled only; > 1 -> fp32 partials)
+  bool direct;     // one token, streaming: slots index the GEMM rows directly
+                   // (no alignment; distinct experts per token)
+  bool direct_sum; // ... and GEMM2 folds the top-k sum (no moe_sum)
+  int kwd;         // waves of the folded GEMM2
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
   int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, total;
@@ -86,6 +90,19 @@ static int pick_ksplit(int64_t numel, int e, int bm, int64_t hidden,
     }
   }
   return best;
+}
+
+// FGS_MOE_DIRECT selects the single-token schedule (a tuning aid; read
+// once): 0 aligned rows, 1 direct rows with GEMM2 folding the top-k sum
+// for bf16 / int8 outputs of >= 192 column tiles (the default), 2 direct
+// rows with moe_sum, 3 direct rows, always folded.
+static int direct_choice() {
+  static const int d = [] {
+    const char* v = getenv("FGS_MOE_DIRECT");
+    const int x = v ? atoi(v) : 1;
+    return (x >= 0 && x <= 3) ? x : 1;
+  }();
+  return d;
 }
 
 // FGS_MOE_KSPLIT (1..4) forces the tiled GEMM2's k split (a tuning aid;
@@ -149,6 +166,20 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   const int step = stream_step_k(p.dt);
   p.kw1 = pick_kw(hidden, step, 4);
   p.kw2 = pick_kw(inter, step, 8);
+  // One token: its top-k slots go to distinct experts, so the streaming
+  // GEMMs take slot j as row tile j (expert topk_ids[j]) and the alignment
+  // is skipped; GEMM2 also folds the weighted top-k sum when the output
+  // spans enough column tiles (one workgroup each) to fill the chip.
+  const int dc = direct_choice();
+  p.direct = !p.tiled && m == 1 && dc != 0;
+  // (measured: folding wins for bf16 and int8 from 192 column tiles --
+  // Mixtral, Qwen2 -- and loses slightly for fp8, whose per-step block
+  // scales keep the unfolded GEMM2 + moe_sum ahead)
+  p.direct_sum = p.direct && (dc == 3 || (dc == 1 && p.dt != kDtFp8 && hidden / 16 >= 192));
+  // the folded GEMM2's waves: as many as keep its grid (one workgroup per
+  // 16 output columns) resident in one round at 16 waves per CU
+  const int64_t wgs = hidden / 16;
+  p.kwd = wgs * 16 <= kNumCUs * 16 ? 16 : wgs * 8 <= kNumCUs * 16 ? 8 : 4;
   p.max_padded = max_padded_of(numel, e, p.block_m);
   p.n_blocks = p.max_padded / p.block_m;
   // Blocks that can hold rows: each touched expert pads at most one partial
@@ -317,10 +348,12 @@ static int run_fused(const FusedArgs& a) {
 
   g_prof.begin();
   g_prof.mark(0, a.stream);
-  rc = launch_align(a.topk_ids, numel, a.e, p.block_m, sorted, eids, npp,
-                    p.max_padded, a.stream,
-                    p.o_alg >= 0 ? reinterpret_cast<int32_t*>(ws + p.o_alg) : nullptr);
-  if (rc) return rc;
+  if (!p.direct) {
+    rc = launch_align(a.topk_ids, numel, a.e, p.block_m, sorted, eids, npp,
+                      p.max_padded, a.stream,
+                      p.o_alg >= 0 ? reinterpret_cast<int32_t*>(ws + p.o_alg) : nullptr);
+    if (rc) return rc;
+  }
   g_prof.mark(1, a.stream);
 
   const bool on_input = (a.flags & FGS_FLAG_ROUTER_WEIGHT_ON_INPUT) != 0;
@@ -364,27 +397,37 @@ static int run_fused(const FusedArgs& a) {
   g1.limit = a.limit;
   g1.bias = a.b13;
   g1.a_rows = a.m;
+  if (p.direct) {
+    // slot j is row tile j; a2 holds the compact slot rows
+    g1.direct_ids = a.topk_ids;
+    g1.num_experts = a.e;
+  }
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, static_cast<int>(p.n_launch),
                                    a.stream)
                : launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
-                                    static_cast<int>(p.n_launch), a.stream);
+                                    static_cast<int>(p.direct ? numel : p.n_launch),
+                                    a.stream);
   if (rc) return rc;
   g_prof.mark(3, a.stream);
 
   const uint8_t* act2 = reinterpret_cast<const uint8_t*>(a2);
   const float* act2_scale = nullptr;
+  // direct rows: the compact slot rows; else only the padded rows in use
+  // (num_tokens_post_padded, on the device)
+  const int64_t a2_rows = p.direct ? numel : p.max_padded;
+  const int32_t* a2_npp = p.direct ? nullptr : npp;
+  const int32_t* a2_sorted = p.direct ? nullptr : sorted;
   if (p.dt == kDtFp8) {
-    // only the padded rows in use (num_tokens_post_padded, on the device)
     rc = launch_quant_fp8_group(a2, ws + p.o_a2q,
                                 reinterpret_cast<float*>(ws + p.o_a2s),
-                                p.max_padded, a.inter, 128, a.stream, npp, sorted, numel);
+                                a2_rows, a.inter, 128, a.stream, a2_npp, a2_sorted, numel);
     if (rc) return rc;
     act2 = ws + p.o_a2q;
     act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
   } else if (p.dt == kDtInt8) {
     rc = launch_quant_int8_token(a2, reinterpret_cast<int8_t*>(ws + p.o_a2q),
                                  reinterpret_cast<float*>(ws + p.o_a2s),
-                                 p.max_padded, a.inter, a.stream, npp, sorted, numel);
+                                 a2_rows, a.inter, a.stream, a2_npp, a2_sorted, numel);
     if (rc) return rc;
     act2 = ws + p.o_a2q;
     act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
@@ -404,10 +447,20 @@ static int run_fused(const FusedArgs& a) {
   g2.ksplit = p.ksplit2;
   g2.a_rows = p.max_padded;
   g2.eid_shift = p.tiled ? p.eid_shift2 : 0;
+  if (p.direct_sum) {
+    // out = the weighted top-k sum, straight from GEMM2
+    g2.out = a.out;
+    rc = launch_gemm2_direct(p.dt, g2, p.kwd, a.stream);
+    if (rc) return rc;
+    g_prof.mark(5, a.stream);
+    g_prof.mark(6, a.stream);
+    return FGS_OK;
+  }
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg2, false, g2,
                                    static_cast<int>(p.n_launch << p.eid_shift2), a.stream)
                : launch_gemm_stream(p.dt, false, g2, p.mt, p.kw2,
-                                    static_cast<int>(p.n_launch), a.stream);
+                                    static_cast<int>(p.direct ? numel : p.n_launch),
+                                    a.stream);
   if (rc) return rc;
   g_prof.mark(5, a.stream);
 

@@ -38,6 +38,9 @@ struct GemmParams {
   const float* bias;      // fp32 per expert: GEMM1 [E, 2N] (gate | up), GEMM2 [E, K]; or null
   int64_t a_rows;         // rows of `a` (GEMM1: tokens; GEMM2: padded rows)
   int32_t eid_shift;      // tiled: row block rb belongs to alignment block rb >> eid_shift
+  const int32_t* direct_ids;  // streaming, one token: topk_ids ([numel] slots) in
+                              // place of the alignment; null: aligned rows
+  int32_t num_experts;        // with direct_ids: valid ids are [0, num_experts)
 };
 
 // Router gating (scores -> top-k -> renormalise), one wave per token;
@@ -90,6 +93,9 @@ int launch_quant_int8_token(const void* x, int8_t* q, float* scales,
 int stream_step_k(int dt);
 int launch_gemm_stream(int dt, bool gemm1, const GemmParams& p, int mt, int kw,
                        int row_blocks, hipStream_t stream);
+// GEMM2 of one token with the top-k sum folded in (p.direct_ids set, p.out
+// the bf16 [1, n_out] output); kw in {4, 8, 16}.
+int launch_gemm2_direct(int dt, const GemmParams& p, int kw, hipStream_t stream);
 
 // LDS-tiled MFMA kernels (bf16, fp8, int8): configuration per element type
 // and rows-per-expert regime, its row block, n_out granularity, launch.

@@ -13,6 +13,12 @@
 //          ops/fused_moe.py:205-218): a2[row, c] = bf16(silu(g) * u)
 //   GEMM2 (replaces matmul_ogs with scatter + gammas, :224-231):
 //          y[slot, c] = bf16(acc); the gamma-weighted top-k sum is moe_sum's
+//
+// Direct rows (one token, DIRECT): the token's top-k slots go to distinct
+// experts, so no alignment is needed -- row tile j is slot j alone, its
+// expert topk_ids[j], and the activations are compact [slots, k] rows.
+// moe_gemm2_direct_kernel also folds the gamma-weighted top-k sum into
+// GEMM2: a workgroup owns 16 output columns for every slot.
 #include "fgs_moe_kernels.h"
 
 namespace fgs {
@@ -108,7 +114,7 @@ __device__ __forceinline__ f32x4 mma_fp8(const u32x4 (&a)[2],
   return mfma16_fp8(av, bv, f32x4{0.f, 0.f, 0.f, 0.f});
 }
 
-template <int DT, int MT, int KW, bool GEMM1>
+template <int DT, int MT, int KW, bool GEMM1, bool DIRECT>
 __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
     const GemmParams p) {
   typedef StreamTraits<DT> T;
@@ -117,12 +123,31 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
   constexpr int NV = T::kVecs;
   constexpr int ESZ = (DT == kDtBf16) ? 2 : 1;
   constexpr int BM = 16 * MT;
+  static_assert(!DIRECT || MT == 1, "direct rows: one slot per row tile");
 
   const int rb = blockIdx.x;
   const int n0 = blockIdx.y * 16;
-  if (rb * BM >= p.num_post_pad[0]) return;
-  const int e = p.expert_ids[rb];
-  if (e < 0) return;
+  int e;
+  if constexpr (DIRECT) {
+    if (rb >= p.numel) return;
+    e = p.direct_ids[rb];
+    if (e < 0 || e >= p.num_experts) return;  // dropped slot: never read
+  } else {
+    if (rb * BM >= p.num_post_pad[0]) return;
+    e = p.expert_ids[rb];
+    if (e < 0) return;
+  }
+  // slot of row r of the tile (p.numel: a pad row)
+  auto row_sid = [&](int r) -> int {
+    if constexpr (DIRECT) return r == rb * BM ? rb : static_cast<int>(p.numel);
+    else return p.sorted_ids[r];
+  };
+  // activation / scale row of a valid slot: GEMM1 the token, GEMM2 the
+  // padded row (direct: the compact slot row)
+  auto src_row = [&](int r, int sid) -> int64_t {
+    if constexpr (GEMM1) return sid / p.topk;
+    else return DIRECT ? sid : r;
+  };
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -135,9 +160,9 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int r = rb * BM + mt * 16 + ln;
-    const int sid = p.sorted_ids[r];
+    const int sid = row_sid(r);
     avalid[mt] = sid < p.numel;
-    const int64_t src = GEMM1 ? (avalid[mt] ? sid / p.topk : 0) : r;
+    const int64_t src = avalid[mt] ? src_row(r, sid) : 0;
     arow[mt] = p.a + (src * p.kdim) * ESZ + lg * 16;
   }
   // Weight rows of lane ln.
@@ -157,9 +182,9 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = rb * BM + mt * 16 + lg * 4 + i;
-      const int sid = p.sorted_ids[r];
+      const int sid = row_sid(r);
       cvalid[mt][i] = sid < p.numel;
-      crow[mt][i] = GEMM1 ? (cvalid[mt][i] ? sid / p.topk : 0) : r;
+      crow[mt][i] = cvalid[mt][i] ? src_row(r, sid) : 0;
     }
 
   Acc acc[NB][MT];
@@ -274,7 +299,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
     for (int i = 0; i < 4; ++i) {
       const int r = rb * BM + mt * 16 + lg * 4 + i;
       const bool valid = cvalid[mt][i];
-      const int sid = p.sorted_ids[r];
+      const int sid = row_sid(r);
       float v[NB];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
@@ -292,9 +317,11 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
         v[nb] = x;
       }
       if constexpr (GEMM1) {
-        out[static_cast<int64_t>(r) * p.n_out + col] =
-            gemm1_epilogue(v[0], v[NB - 1], p.weight_on_input && valid,
-                           valid ? p.topk_w[sid] : 0.f, p.act, p.alpha, p.limit);
+        // padded row order; direct rows write the compact slot rows only
+        if (!DIRECT || valid)
+          out[static_cast<int64_t>(DIRECT ? sid : r) * p.n_out + col] =
+              gemm1_epilogue(v[0], v[NB - 1], p.weight_on_input && valid,
+                             valid ? p.topk_w[sid] : 0.f, p.act, p.alpha, p.limit);
       } else {
         if (valid)
           out[static_cast<int64_t>(sid) * p.n_out + col] = f32_to_bf16_bits(v[0]);
@@ -303,10 +330,10 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
   }
 }
 
-template <int DT, int MT, int KW, bool GEMM1>
+template <int DT, int MT, int KW, bool GEMM1, bool DIRECT>
 static int launch_one(const GemmParams& p, int row_blocks, hipStream_t stream) {
   dim3 grid(row_blocks, static_cast<unsigned>(p.n_out / 16));
-  hipLaunchKernelGGL((moe_gemm_stream_kernel<DT, MT, KW, GEMM1>), grid,
+  hipLaunchKernelGGL((moe_gemm_stream_kernel<DT, MT, KW, GEMM1, DIRECT>), grid,
                      dim3(KW * 64), 0, stream, p);
   return check_launch("moe_gemm_stream_kernel");
 }
@@ -314,14 +341,155 @@ static int launch_one(const GemmParams& p, int row_blocks, hipStream_t stream) {
 template <int DT, bool GEMM1>
 static int dispatch_kw(const GemmParams& p, int mt, int kw, int row_blocks,
                        hipStream_t stream) {
+  if (p.direct_ids) {
+    // direct rows: one slot per 16-row tile
+#define FGS_CASE(KW_) \
+  if (mt == 1 && kw == KW_) return launch_one<DT, 1, KW_, GEMM1, true>(p, row_blocks, stream);
+    FGS_CASE(1) FGS_CASE(2) FGS_CASE(4) FGS_CASE(8)
+#undef FGS_CASE
+    return fail(FGS_EUNSUPPORTED, "stream GEMM: no direct-row kernel for this tile");
+  }
 #define FGS_CASE(MT_, KW_)                                           \
   if (mt == MT_ && kw == KW_)                                        \
-    return launch_one<DT, MT_, KW_, GEMM1>(p, row_blocks, stream);
+    return launch_one<DT, MT_, KW_, GEMM1, false>(p, row_blocks, stream);
   FGS_CASE(1, 1) FGS_CASE(1, 2) FGS_CASE(1, 4) FGS_CASE(1, 8)
   FGS_CASE(2, 1) FGS_CASE(2, 2) FGS_CASE(2, 4) FGS_CASE(2, 8)
   FGS_CASE(4, 1) FGS_CASE(4, 2) FGS_CASE(4, 4) FGS_CASE(4, 8)
 #undef FGS_CASE
   return fail(FGS_EUNSUPPORTED, "stream GEMM: no kernel for this tile");
+}
+
+// GEMM2 of one token with the top-k sum folded in (direct rows):
+//   out[c] = bf16( sum_j gamma_j * (a2[j] . W2[e_j][c]) (+ gamma_j * b2[e_j][c]) )
+// gamma_j = topk_w[j] (1 with the router weight on the input), dropped slots
+// (ids outside [0, E)) skipped. The sum over slots runs in fp32 in a fixed
+// order (slots in a wave, then waves), so it replaces GEMM2's bf16 y rows and
+// moe_sum with one pass and no intermediate rounding. A workgroup owns 16
+// output columns; with S slots, S <= KW gives each slot KW / S waves that
+// split its contraction, S > KW deals whole slots to the waves in turn. Only
+// row 0 of the MFMA tile is live (the token; the other activation rows are
+// zero).
+template <int DT, int KW>
+__global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmParams p) {
+  typedef StreamTraits<DT> T;
+  typedef typename T::Acc Acc;
+  constexpr int NV = T::kVecs;
+  constexpr int ESZ = (DT == kDtBf16) ? 2 : 1;
+  const int n0 = blockIdx.x * 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int ln = lane & 15;
+  const int lg = lane >> 4;
+  const int col = n0 + ln;
+  const int slots = static_cast<int>(p.numel);
+  const int steps = static_cast<int>(p.kdim / T::kStepK);
+  const int64_t step_bytes = static_cast<int64_t>(T::kStepK) * ESZ;
+  const int kblocks = static_cast<int>(p.kdim / 128);
+
+  int j0, jstride, s0, s1;
+  bool lead;  // the slot's first wave: adds its bias once
+  if (slots <= KW) {
+    const int wps = KW / slots;  // waves per slot
+    j0 = wave / wps;             // >= slots: an idle wave (KW % slots != 0)
+    jstride = slots;
+    const int sub = wave % wps;
+    s0 = sub * steps / wps;      // empty for some waves when steps < wps
+    s1 = (sub + 1) * steps / wps;
+    lead = sub == 0;
+  } else {
+    j0 = wave;
+    jstride = KW;
+    s0 = 0;
+    s1 = steps;
+    lead = true;
+  }
+
+  f32x4 tot = {0.f, 0.f, 0.f, 0.f};
+  for (int j = j0; j < slots; j += jstride) {
+    const int e = p.direct_ids[j];
+    if (e < 0 || e >= p.num_experts) continue;
+    const float gamma = p.weight_on_input ? 1.f : p.topk_w[j];
+    const uint8_t* brow =
+        p.w + ((static_cast<int64_t>(e) * p.nrows_w + col) * p.kdim) * ESZ + lg * 16;
+    const uint8_t* arow = p.a + (static_cast<int64_t>(j) * p.kdim) * ESZ + lg * 16;
+    const bool avalid = ln == 0;  // activation row 0 is the slot's row
+    const float* wsc = DT == kDtFp8
+                           ? p.w_scale + (static_cast<int64_t>(e) * (p.nrows_w / 128) +
+                                          n0 / 128) * kblocks
+                           : nullptr;
+    Acc acc = {0, 0, 0, 0};
+    u32x4 bf[2][NV], af[2][NV];
+    float sc[2];  // fp8: activation x weight block scale of the step
+    auto load = [&](int buf, int st) {
+      load_frag<DT>(bf[buf], brow + st * step_bytes, true);
+      load_act(af[buf], arow + st * step_bytes, avalid);
+      if constexpr (DT == kDtFp8) sc[buf] = p.a_scale[j * kblocks + st] * wsc[st];
+    };
+    if (s0 < s1) load(0, s0);
+    for (int s = s0; s < s1; s += 2) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int cur = s + h;
+        if (cur >= s1) break;
+        if (cur + 1 < s1) load(h ^ 1, cur + 1);
+        if constexpr (DT == kDtBf16) {
+          mma_step<DT>(acc, af[h], bf[h]);
+        } else if constexpr (DT == kDtInt8) {
+          mma_step_i8<DT>(acc, af[h], bf[h]);
+        } else {
+          const f32x4 t = mma_fp8(af[h], bf[h]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] += t[i] * sc[h];
+        }
+      }
+    }
+    float f = gamma;
+    if constexpr (DT == kDtInt8)
+      f *= p.a_scale[j] * p.w_scale[static_cast<int64_t>(e) * p.nrows_w + col];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tot[i] += static_cast<float>(acc[i]) * f;
+    if (p.bias && lead) {
+      const float b = gamma * p.bias[static_cast<int64_t>(e) * p.nrows_w + col];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tot[i] += b;
+    }
+  }
+
+  __shared__ f32x4 red[KW > 1 ? KW - 1 : 1][64];
+  if (KW > 1) {
+    if (wave > 0) red[wave - 1][lane] = tot;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < KW - 1; ++w) tot += red[w][lane];
+  }
+  // row 0 of the tile: lane group 0, register 0
+  if (lg == 0) static_cast<uint16_t*>(p.out)[col] = f32_to_bf16_bits(tot[0]);
+}
+
+template <int DT>
+static int launch_gemm2_direct_t(const GemmParams& p, int kw, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.n_out / 16));
+#define FGS_CASE(KW_)                                                               \
+  if (kw == KW_) {                                                                  \
+    hipLaunchKernelGGL((moe_gemm2_direct_kernel<DT, KW_>), grid, dim3(KW_ * 64), 0, \
+                       stream, p);                                                  \
+    return check_launch("moe_gemm2_direct_kernel");                                 \
+  }
+  FGS_CASE(4) FGS_CASE(8) FGS_CASE(16)
+#undef FGS_CASE
+  return fail(FGS_EUNSUPPORTED, "direct GEMM2: no kernel for this wave count");
+}
+
+int launch_gemm2_direct(int dt, const GemmParams& p, int kw, hipStream_t stream) {
+  if (!p.direct_ids || p.numel < 1)
+    return fail(FGS_EINVAL, "direct GEMM2: needs the slot ids");
+  switch (dt) {
+    case kDtBf16: return launch_gemm2_direct_t<kDtBf16>(p, kw, stream);
+    case kDtFp8: return launch_gemm2_direct_t<kDtFp8>(p, kw, stream);
+    case kDtInt8: return launch_gemm2_direct_t<kDtInt8>(p, kw, stream);
+  }
+  return fail(FGS_EUNSUPPORTED, "direct GEMM2: unknown dtype");
 }
 
 int stream_step_k(int dt) {

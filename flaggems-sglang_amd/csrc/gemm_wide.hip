@@ -86,7 +86,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   using Acc = typename T::Acc;
   constexpr bool INT8 = DT == kDtInt8;
   constexpr int ESZ = T::ESZ;
-  constexpr int BM = C::BM, BNR = C::BNR, WROWS = C::WROWS, WCOLS = C::WCOLS;
+  constexpr int BM = C::BM, BNR = C::BNR, WCOLS = C::WCOLS;
   constexpr int RB = C::RB, CB = C::CB, SK = C::SK, NS = C::NS, KK = C::KK;
   constexpr int NLA = C::NLA, NLB = C::NLB, NL = C::NL, SLOT = C::SLOT, B_OFF = C::B_OFF;
   static_assert(T::FC == 1, "one LDS chunk per fragment");

@@ -16,6 +16,7 @@ Reference interface mirrored: src/flaggems_sglang/ops/fused_moe.py
 from __future__ import annotations
 
 import logging
+import weakref
 from dataclasses import dataclass
 from typing import Optional
 
@@ -45,16 +46,19 @@ _DEINTERLEAVE_CACHE: dict = {}
 
 
 def _cached(cache: dict, w: torch.Tensor, fn):
-    """``fn(w)`` cached per weight version (a model's weights are converted
-    once, not on every call)."""
+    """``fn(w)`` cached per weight tensor and version (a model's weights are
+    converted once, not on every call). An entry holds a weak reference to
+    its source and only serves that same tensor object: a freed weight's
+    address can be reused by a new tensor of the same shape."""
     key = (w.data_ptr(), w._version, tuple(w.shape), tuple(w.stride()), w.dtype)
     hit = cache.get(key)
-    if hit is None:
-        if len(cache) > 64:
-            cache.clear()
-        hit = fn(w)
-        cache[key] = hit
-    return hit
+    if hit is not None and hit[0]() is w:
+        return hit[1]
+    if len(cache) > 64:
+        cache.clear()
+    out = fn(w)
+    cache[key] = (weakref.ref(w), out)
+    return out
 
 
 # --------------------------------------------------------------- routing ---

@@ -252,3 +252,33 @@ def test_standard_topk_to_routing_roundtrip_cpu():
     assert torch.equal(ids2.long(), torch.gather(ids, 1, order))
     assert torch.equal(w2, torch.gather(w, 1, order))
     assert torch.equal(gi.dst_indx[gi.src_indx.long()], torch.arange(36, dtype=torch.int32))
+
+
+def test_weight_cache_serves_only_its_tensor():
+    """The converted-weight cache (deinterleave / transpose of a model's
+    weights) answers only for the tensor object it converted: a freed weight's
+    address and shape can come back on a new tensor."""
+    import weakref
+
+    from flaggems_sglang.ops import fused_moe as fm
+
+    cache, calls = {}, []
+
+    def fn(t):
+        calls.append(1)
+        return t * 2
+
+    a = torch.ones(4, 4)
+    assert fm._cached(cache, a, fn) is fm._cached(cache, a, fn)
+    assert len(calls) == 1
+    # an entry under b's key whose source is gone is not served
+    b = torch.full((4, 4), 3.0)
+    key = (b.data_ptr(), b._version, tuple(b.shape), tuple(b.stride()), b.dtype)
+    gone = torch.zeros(1)
+    cache[key] = (weakref.ref(gone), torch.zeros(4, 4))
+    del gone
+    assert torch.equal(fm._cached(cache, b, fn), b * 2)
+    # an in-place update is a new version
+    a.add_(1)
+    assert torch.equal(fm._cached(cache, a, fn), torch.full((4, 4), 4.0))
+    assert len(calls) == 3

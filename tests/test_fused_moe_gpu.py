@@ -166,12 +166,49 @@ def test_quantised_schedules_agree(gpu, mode):
     _check(pre.cpu()[toks], ref, mode, f"{mode} prefill")
 
 
+# ------------------------------------------------------ one-token decode ---
+# M = 1 runs the direct-row schedule: no alignment, slot j is row tile j
+# (its expert topk_ids[j]); with >= 192 output column tiles (hidden >= 3072)
+# GEMM2 also folds the weighted top-k sum, below that moe_sum does. Covered:
+# both GEMM2 forms, top-k of 2, odd (3: idle waves), above the 16 waves (20:
+# slots dealt round robin), dropped slots and the router weight on the input.
+@pytest.mark.parametrize("mode", ["bf16", "fp8", "int8"])
+@pytest.mark.parametrize("K,N,E,topk", [(3072, 256, 8, 2), (3072, 256, 32, 3),
+                                        (3072, 256, 64, 20), (1024, 512, 16, 4)],
+                         ids=lambda v: str(v))
+@pytest.mark.parametrize("variant", ["plain", "dropped", "on_input"])
+def test_single_token(gpu, mode, K, N, E, topk, variant):
+    wts = testing.make_weights(K, N, E, mode, 0.1, device=gpu, seed=K + N + E + topk)
+    x, tw, ti = testing.make_tokens(1, K, E, topk, device=gpu, seed=K + E + topk)
+    if variant == "dropped":
+        ti = ti.clone()
+        ti[0, 0] = -1
+        if topk > 2:
+            ti[0, -1] = E + 2
+    on_input = variant == "on_input"
+    res = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, apply_router_weight_on_input=on_input,
+                       **wts.kwargs(mode))
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=mode, w1_scale=wts.w1_scale,
+                            w2_scale=wts.w2_scale, apply_router_weight_on_input=on_input,
+                            return_mag=True)
+    _check(res.cpu(), ref, mode, f"M=1 {mode} {(K, N, E, topk)} {variant}")
+
+
+def test_single_token_deterministic(gpu):
+    wts = testing.make_weights(3072, 256, 8, "bf16", 0.1, device=gpu, seed=5)
+    x, tw, ti = testing.make_tokens(1, 3072, 8, 2, device=gpu, seed=5)
+    a = fm.fused_moe(x, wts.w1, wts.w2, tw, ti)
+    for _ in range(3):
+        assert torch.equal(fm.fused_moe(x, wts.w1, wts.w2, tw, ti), a)
+
+
 # ------------------------------------------------- activations and biases ---
 _SCHEDS = [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL]
 
 
 @pytest.mark.parametrize("sched", _SCHEDS, ids=["decode", "prefill"])
-@pytest.mark.parametrize("shape", [(5, 256, 128, 4, 2), (600, 512, 384, 8, 2)])
+@pytest.mark.parametrize("shape", [(5, 256, 128, 4, 2), (600, 512, 384, 8, 2),
+                                   (1, 3072, 128, 4, 2)])
 def test_gelu_activation(gpu, shape, sched):
     """activation="gelu": exact-erf gelu(gate) * up in GEMM1's epilogue
     (sgl_kernel gelu_and_mul, ops/fused_moe.py:219-220)."""
@@ -209,7 +246,8 @@ def _bias_inputs(M, K, N, E, topk, device):
 
 @pytest.mark.parametrize("on_input", [False, True], ids=["gammas_out", "gammas_in"])
 @pytest.mark.parametrize("sched", _SCHEDS, ids=["decode", "prefill"])
-@pytest.mark.parametrize("shape", [(7, 256, 128, 4, 2), (500, 512, 256, 8, 2)])
+@pytest.mark.parametrize("shape", [(7, 256, 128, 4, 2), (500, 512, 256, 8, 2),
+                                   (1, 3072, 128, 4, 2), (1, 256, 128, 4, 3)])
 def test_bias_swiglu(gpu, shape, sched, on_input):
     """Bias variant (ops/fused_moe.py:235-325): GEMM1 + b1 with swiglu(alpha,
     limit) fused, GEMM2 + b2, on interleaved gate/linear rows."""

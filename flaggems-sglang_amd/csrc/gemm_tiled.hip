@@ -557,9 +557,8 @@ static int group_m_choice() {
   return g;
 }
 // Which GEMMs of the 256-row configuration run the 4-wave kernel
-// (gemm_wide.hip): 1 (default) GEMM1, 2 both, 0 neither (FGS_MOE_WIDE, a
-// tuning aid; read once). GEMM1 gains on every measured configuration;
-// GEMM2 measured slower than the 8-wave kernel on the Mixtral layer.
+// (gemm_wide.hip): 1 (default) GEMM1 and short-k GEMM2s, 2 both always, 0
+// neither (FGS_MOE_WIDE, a tuning aid; read once).
 static int wide_choice() {
   static const int mode = env_choice("FGS_MOE_WIDE", 1, 0, 2);
   return mode;
@@ -659,7 +658,14 @@ int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
     return fail(FGS_EINVAL, "tiled GEMM: configuration " + std::to_string(cfg) +
                                 " not available for this element type");
   if (row_blocks <= 0) return FGS_OK;
-  if (cfg == 0 && wide_choice() >= (gemm1 ? 1 : 2) && wide_supported(dt, gemm1, p))
+  // The 4-wave kernel runs GEMM1 of the 256-row configuration, and GEMM2
+  // where its k row is short (<= 8 KiB: Qwen3, Qwen2 int8 -2..-5 %); a long
+  // GEMM2 contraction (Mixtral, 28 KiB) keeps the 8-wave kernel (+6 % on
+  // the 4-wave one at M=4096). FGS_MOE_WIDE=2 forces it for every GEMM2.
+  const int64_t k_row = p.kdim * (dt == kDtBf16 ? 2 : 1);
+  const bool wide_gemm =
+      gemm1 ? wide_choice() >= 1 : (wide_choice() >= 2 || (wide_choice() == 1 && k_row <= 8192));
+  if (cfg == 0 && wide_gemm && wide_supported(dt, gemm1, p))
     return launch_gemm_wide(dt, gemm1, p, row_blocks, stream);
   switch (dt) {
     case kDtBf16:

@@ -146,7 +146,7 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
             ((flags & FGS_FLAG_FORCE_PREFILL) || forced_cfg >= 0 || many_rows);
   p.ksplit2 = 1;
   if (p.tiled) {
-    p.tile_cfg = forced_cfg >= 0 ? forced_cfg : tiled_config_for(p.dt, rows_per_expert);
+    p.tile_cfg = forced_cfg >= 0 ? forced_cfg : tiled_config_for(p.dt, rows_per_expert, e);
     p.block_m = tiled_block_m(p.tile_cfg);
     // fp8 GEMM2 runs its 128-row kernel on 256-row blocks (as two halves,
     // the all-pad ones skipped): the 256-row fp8 tile spans only 128 weight

@@ -101,7 +101,7 @@ int launch_gemm2_direct(int dt, const GemmParams& p, int kw, hipStream_t stream)
 // and rows-per-expert regime, its row block, n_out granularity, launch.
 constexpr int kTiledConfigs = 4;
 int tiled_config_supported(int dt, int cfg);
-int tiled_config_for(int dt, double rows_per_expert);
+int tiled_config_for(int dt, double rows_per_expert, int num_experts);
 int tiled_block_m(int cfg);
 int tiled_n_align(bool gemm1);
 int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,

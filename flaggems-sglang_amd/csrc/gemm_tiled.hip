@@ -625,16 +625,26 @@ int tiled_config_supported(int dt, int cfg) {
   return cfg >= 0 && cfg < kTiledConfigs;
 }
 
-// From about 112 rows per expert a noticeable share of the experts would
-// spill into a second, mostly empty 128-row block that streams the expert's
-// weights again; 256-row blocks read each weight tile once per expert and
-// skip the MFMAs of their all-pad 32-row blocks.
-int tiled_config_for(int dt, double rows_per_expert) {
+// Configuration by rows per expert and expert count (measured on the four
+// model shapes, M from 32 to 8192):
+// * from 112 rows, 256-row blocks: fewer would spill a noticeable share of
+//   the experts into a second, mostly empty block that streams the
+//   expert's weights again, and the 256-row kernels skip the MFMAs of their
+//   all-pad 32-row blocks;
+// * with many experts (>= 32) the 256-row configuration already wins from
+//   48 rows (64 rows: Qwen3 -14 %, Qwen2 int8 -15 %, DeepSeek fp8 -10 %
+//   against the 64-row kernel); with 8 experts (Mixtral) it loses there;
+// * otherwise the 8-wave 128-row kernel from 24 rows (Mixtral M=256 -11 %,
+//   Qwen2 M=256 -6 %, DeepSeek M=1024 -4 %), and for many experts also from
+//   8 rows (Qwen2 M=64 -6 %, DeepSeek M=256/512 -3/-5 %, Qwen3 M=256 -7 %);
+// * the 32-row kernel below that (Mixtral M=32/64, DeepSeek M=32).
+// The 64-row configuration is no longer chosen; it stays for FGS_MOE_TILE.
+int tiled_config_for(int dt, double rows_per_expert, int num_experts) {
   (void)dt;
+  const bool many = num_experts >= 32;
   int c = 3;
-  if (rows_per_expert >= 112) c = 0;
-  else if (rows_per_expert >= 96) c = 1;
-  else if (rows_per_expert >= 24) c = 2;
+  if (rows_per_expert >= 112 || (many && rows_per_expert >= 48)) c = 0;
+  else if (rows_per_expert >= 24 || (many && rows_per_expert >= 8)) c = 1;
   if (forced_tile() >= 0) c = forced_tile();
   return c;
 }

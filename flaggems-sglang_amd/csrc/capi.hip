@@ -132,16 +132,27 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   const double rows_per_expert = static_cast<double>(numel) / e;
   p.mt = rows_per_expert <= 16 ? 1 : rows_per_expert <= 32 ? 2 : 4;
   p.block_m = 16 * p.mt;
-  // LDS-tiled kernels (deep DMA pipeline) from two rows per expert, or from
-  // one where GEMM2's k (inter) holds >= 16 LDS stages to amortise each
-  // tile's pipeline fill; the streaming kernels below that (single-token
-  // decode). Shapes the tiled kernels do not cover always stream.
+  // LDS-tiled kernels (deep DMA pipeline) or the streaming kernels (weights
+  // straight into registers), by the rows per expert at which the tiled
+  // kernels' pipeline fill pays off, measured per contraction length
+  // (kmin: the shorter of the two GEMMs' k rows in bytes):
+  // * fp8 from two tokens (its streaming steps carry 32 bytes per lane:
+  //   DeepSeek M=2..16 tiled -2..-12 %);
+  // * a short k row (< 2 KiB, Qwen3) from 12 rows per expert (streaming
+  //   -14 % at 2 rows, -3 % at 8);
+  // * a long one (>= 8 KiB, Mixtral) from half a row (-2..-4 % at M=2, 3);
+  // * else (Qwen2 int8) from one row (streaming -30 % at a quarter row).
+  // One token always streams (its direct-row schedule); shapes the tiled
+  // kernels do not cover always stream.
   const int64_t esz = p.dt == kDtBf16 ? 2 : 1;
   const bool tiled_ok = inter % tiled_n_align(true) == 0 &&
                         hidden % tiled_n_align(false) == 0;
   const int forced_cfg = ((flags & FGS_FLAG_TILE_MASK) >> 12) - 1;
-  const bool many_rows = rows_per_expert >= 2.0 ||
-                         (rows_per_expert >= 1.0 && inter * esz >= 16 * 128);
+  const int64_t kmin = std::min(hidden, inter) * esz;
+  double tiled_from = 1.0;
+  if (kmin < 2048) tiled_from = 12.0;
+  else if (kmin >= 8192) tiled_from = 0.5;
+  const bool many_rows = m >= 2 && (p.dt == kDtFp8 || rows_per_expert >= tiled_from);
   p.tiled = tiled_ok && !(flags & FGS_FLAG_FORCE_DECODE) &&
             ((flags & FGS_FLAG_FORCE_PREFILL) || forced_cfg >= 0 || many_rows);
   p.ksplit2 = 1;

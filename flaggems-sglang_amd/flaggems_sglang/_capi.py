@@ -27,6 +27,7 @@ FLAG_ROUTER_WEIGHT_ON_INPUT = 0x1
 FLAG_ACT_GELU = 0x2
 FLAG_FORCE_DECODE = 0x100
 FLAG_FORCE_PREFILL = 0x200
+FLAG_SEPARATE_SUM = 0x400
 TILED_CONFIGS = 4  # row blocks 256, 128, 64, 32
 
 

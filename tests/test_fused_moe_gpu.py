@@ -168,16 +168,18 @@ def test_quantised_schedules_agree(gpu, mode):
 
 # ------------------------------------------------------ one-token decode ---
 # M = 1 runs the direct-row schedule: no alignment, slot j is row tile j
-# (its expert topk_ids[j]); with >= 192 output column tiles (hidden >= 3072)
-# GEMM2 also folds the weighted top-k sum, below that moe_sum does. Covered:
-# both GEMM2 forms, top-k of 2, odd (3: idle waves), above the 16 waves (20:
-# slots dealt round robin), dropped slots and the router weight on the input.
+# (its expert topk_ids[j]); GEMM2 folds the weighted top-k sum, or with
+# FLAG_SEPARATE_SUM leaves it to moe_sum. Covered: both GEMM2 forms, top-k
+# of 2, odd (3: idle waves), above the 16 waves (20: slots dealt round
+# robin), 64 and 192 output column tiles, dropped slots and the router
+# weight on the input.
 @pytest.mark.parametrize("mode", ["bf16", "fp8", "int8"])
 @pytest.mark.parametrize("K,N,E,topk", [(3072, 256, 8, 2), (3072, 256, 32, 3),
                                         (3072, 256, 64, 20), (1024, 512, 16, 4)],
                          ids=lambda v: str(v))
 @pytest.mark.parametrize("variant", ["plain", "dropped", "on_input"])
-def test_single_token(gpu, mode, K, N, E, topk, variant):
+@pytest.mark.parametrize("fold", [True, False], ids=["folded", "separate"])
+def test_single_token(gpu, mode, K, N, E, topk, variant, fold):
     wts = testing.make_weights(K, N, E, mode, 0.1, device=gpu, seed=K + N + E + topk)
     x, tw, ti = testing.make_tokens(1, K, E, topk, device=gpu, seed=K + E + topk)
     if variant == "dropped":
@@ -187,7 +189,7 @@ def test_single_token(gpu, mode, K, N, E, topk, variant):
             ti[0, -1] = E + 2
     on_input = variant == "on_input"
     res = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, apply_router_weight_on_input=on_input,
-                       **wts.kwargs(mode))
+                       _flags=0 if fold else _capi.FLAG_SEPARATE_SUM, **wts.kwargs(mode))
     ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=mode, w1_scale=wts.w1_scale,
                             w2_scale=wts.w2_scale, apply_router_weight_on_input=on_input,
                             return_mag=True)

@@ -412,6 +412,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   // float(acc) * a_scale[row] * w_scale[channel].
   uint16_t* out = static_cast<uint16_t*>(p.out);
   const int csub = 4 * (lane >> 5);
+  const int half = lane >> 5;
   const float* wsc = INT8 ? p.w_scale + wbase : nullptr;
   auto wscale4 = [&](int64_t wrow) -> f32x4 {
     if constexpr (INT8) return *reinterpret_cast<const f32x4*>(wsc + wrow);
@@ -426,40 +427,98 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   auto bias4 = [&](int64_t col) -> f32x4 {
     return bias ? *reinterpret_cast<const f32x4*>(bias + col) : f32x4{0.f, 0.f, 0.f, 0.f};
   };
+  // A store straight from the accumulator layout touches 32 output rows per
+  // instruction; the silu GEMM1 and the GEMM2 outputs instead go through
+  // this wave's share of a free stage slot (stage KT-2's: no wave reads it
+  // again and no refill targets it; with a single stage, after a barrier)
+  // in passes of 32 rows x JP column blocks, and leave as whole row
+  // segments, 16 bytes per lane. Chunks (16 bytes) of a staged row are
+  // XOR-swizzled by the row so the column-major writes spread over the
+  // banks.
+  constexpr int REGION = (STAGE / NW) & ~15;
+  const int fslot = KT >= 2 ? (KT - 2) % STAGES : 0;
+  if (KT < 2) wave_barrier_all();
+  uint8_t* stg = lds + fslot * STAGE + wave * REGION;
+  // orders this wave's staging writes before its reads (and the reads
+  // before the next pass's writes)
+  auto stage_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  // staged bytes of lane row r, chunk c (CH chunks per row)
+  auto slot_at = [&](auto ch_c, int r, int c) -> uint8_t* {
+    constexpr int CH = decltype(ch_c)::value;
+    return stg + r * (CH * 16) + ((c ^ (r % CH)) * 16);
+  };
+  // writes the staged 32 x CH-chunk block: staged row sr goes to dst(sr)
+  // (a byte address; null: not stored)
+  auto drain = [&](auto ch_c, auto&& dst) {
+    constexpr int CH = decltype(ch_c)::value;
+    stage_sync();
+#pragma unroll
+    for (int k = 0; k < 32 / (64 / CH); ++k) {
+      const int sr = k * (64 / CH) + lane / CH;
+      const int c = lane % CH;
+      const uint4 val = *reinterpret_cast<const uint4*>(slot_at(ch_c, sr, c));
+      uint8_t* d = dst(sr);
+      if (d) *reinterpret_cast<uint4*>(d + c * 16) = val;
+    }
+    stage_sync();
+  };
+  // column blocks per pass for `ob`-byte outputs over `cb` column blocks
+  constexpr auto pass_blocks = [](int ob, int cb) {
+    int jp = cb;
+    while (jp > 1 && 32 * jp * 32 * ob > REGION) jp /= 2;
+    return jp;
+  };
   // GEMM1 with silu and no bias (the common case): the router-weight
   // scaling as a compile-time branch, no bias adds, pairwise conversions
   if constexpr (GEMM1) {
     if (p.act == kActSilu && bias == nullptr) {
+      constexpr int JP = pass_blocks(2, CB / 2);
+      constexpr std::integral_constant<int, JP * 4> ch{};
+      static_assert(32 * JP * 32 * 2 <= REGION, "staging fits");
+      const int col_base = tile_n * (BNR / 2) + wn * (WCOLS / 2);
       auto emit = [&](auto scale_c) {
         constexpr bool SCALE = decltype(scale_c)::value;
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
+          if (i >= nlive) break;  // all-pad blocks (wave-uniform)
           const int rr = wm * WROWS + i * 32 + (lane & 31);
-          const int r = row0 + rr;
-          const int sid = p.sorted_ids[r];
-          if (sid >= p.numel) continue;  // pad rows: never stored
+          const int sid = p.sorted_ids[row0 + rr];
+          const bool ok = sid < p.numel;
           const float sa = INT8 ? p.a_scale[act_row(rr)] : 1.f;
-          const float gamma = SCALE ? p.topk_w[sid] : 1.f;
-          uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
+          const float gamma = SCALE && ok ? p.topk_w[sid] : 1.f;
+          const int r = lane & 31;
 #pragma unroll
-          for (int jb = 0; jb < CB / 2; ++jb) {
-            const int col0 = tile_n * (BNR / 2) + wn * (WCOLS / 2) + jb * 32 + csub;
+          for (int jp0 = 0; jp0 < CB / 2; jp0 += JP) {
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-              const f32x4 swg = wscale4(col0 + 8 * g4);
-              const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
-              const Acc& ag = acc[i][jb];
-              const Acc& au = acc[i][jb + CB / 2];
-              const int v = 4 * g4;
-              uint2 v2;
-              v2.x = silu_mul_bf16x2<SCALE>(
-                  value(ag, v, sa, swg[0]), value(ag, v + 1, sa, swg[1]),
-                  value(au, v, sa, swu[0]), value(au, v + 1, sa, swu[1]), gamma);
-              v2.y = silu_mul_bf16x2<SCALE>(
-                  value(ag, v + 2, sa, swg[2]), value(ag, v + 3, sa, swg[3]),
-                  value(au, v + 2, sa, swu[2]), value(au, v + 3, sa, swu[3]), gamma);
-              *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
+            for (int jl = 0; jl < JP; ++jl) {
+              const int jb = jp0 + jl;
+              const int col0 = col_base + jb * 32 + csub;
+#pragma unroll
+              for (int g4 = 0; g4 < 4; ++g4) {
+                const f32x4 swg = wscale4(col0 + 8 * g4);
+                const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
+                const Acc& ag = acc[i][jb];
+                const Acc& au = acc[i][jb + CB / 2];
+                const int v = 4 * g4;
+                uint2 v2;
+                v2.x = silu_mul_bf16x2<SCALE>(
+                    value(ag, v, sa, swg[0]), value(ag, v + 1, sa, swg[1]),
+                    value(au, v, sa, swu[0]), value(au, v + 1, sa, swu[1]), gamma);
+                v2.y = silu_mul_bf16x2<SCALE>(
+                    value(ag, v + 2, sa, swg[2]), value(ag, v + 3, sa, swg[3]),
+                    value(au, v + 2, sa, swu[2]), value(au, v + 3, sa, swu[3]), gamma);
+                *reinterpret_cast<uint2*>(slot_at(ch, r, jl * 4 + g4) + half * 8) = v2;
+              }
             }
+            drain(ch, [&](int sr) -> uint8_t* {
+              if (__shfl(sid, sr, 64) >= p.numel) return nullptr;
+              const int64_t orow = row0 + wm * WROWS + i * 32 + sr;
+              return reinterpret_cast<uint8_t*>(out + orow * p.n_out + col_base + jp0 * 32);
+            });
           }
         }
       };
@@ -467,16 +526,14 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
       else emit(std::false_type{});
       return;
     }
-  }
 #pragma unroll
-  for (int i = 0; i < RB; ++i) {
-    const int rr = wm * WROWS + i * 32 + (lane & 31);
-    const int r = row0 + rr;
-    const int sid = p.sorted_ids[r];
-    const bool valid = sid < p.numel;
-    if (!valid) continue;  // pad rows: never stored
-    const float sa = INT8 ? p.a_scale[act_row(rr)] : 1.f;
-    if constexpr (GEMM1) {
+    for (int i = 0; i < RB; ++i) {
+      const int rr = wm * WROWS + i * 32 + (lane & 31);
+      const int r = row0 + rr;
+      const int sid = p.sorted_ids[r];
+      const bool valid = sid < p.numel;
+      if (!valid) continue;  // pad rows: never stored
+      const float sa = INT8 ? p.a_scale[act_row(rr)] : 1.f;
       const bool scale = p.weight_on_input != 0;
       const float gamma = scale ? p.topk_w[sid] : 0.f;
       uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
@@ -505,40 +562,76 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
           *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
         }
       }
-    } else if (p.ksplit > 1) {
-      // fp32 partial sums of split ks, reduced in fixed order by moe_sum
-      float* orow = static_cast<float*>(p.out) +
-                    (static_cast<int64_t>(ks) * p.numel + sid) * p.n_out;
+    }
+  } else {
+    const int col_base = tile_n * BNR + wn * WCOLS;
 #pragma unroll
-      for (int j = 0; j < CB; ++j) {
-        const int col0 = tile_n * BNR + wn * WCOLS + j * 32 + csub;
+    for (int i = 0; i < RB; ++i) {
+      if (i >= nlive) break;  // all-pad blocks (wave-uniform)
+      const int rr = wm * WROWS + i * 32 + (lane & 31);
+      const int sid = p.sorted_ids[row0 + rr];
+      const float sa = INT8 ? p.a_scale[act_row(rr)] : 1.f;
+      const int r = lane & 31;
+      if (p.ksplit > 1) {
+        // fp32 partial sums of split ks, reduced in fixed order by moe_sum
+        constexpr int JP = pass_blocks(4, CB);
+        constexpr std::integral_constant<int, JP * 8> ch{};
+        static_assert(32 * JP * 32 * 4 <= REGION, "staging fits");
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const f32x4 sw = wscale4(col0 + 8 * g4);
-          const f32x4 bb = bias4(col0 + 8 * g4);
-          const int v = 4 * g4;
-          *reinterpret_cast<f32x4*>(orow + col0 + 8 * g4) =
-              f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0], value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
-                    value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
-                    value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
+        for (int jp0 = 0; jp0 < CB; jp0 += JP) {
+#pragma unroll
+          for (int jl = 0; jl < JP; ++jl) {
+            const int j = jp0 + jl;
+            const int col0 = col_base + j * 32 + csub;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const f32x4 sw = wscale4(col0 + 8 * g4);
+              const f32x4 bb = bias4(col0 + 8 * g4);
+              const int v = 4 * g4;
+              *reinterpret_cast<f32x4*>(slot_at(ch, r, jl * 8 + g4 * 2 + half)) =
+                  f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0],
+                        value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
+                        value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                        value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
+            }
+          }
+          drain(ch, [&](int sr) -> uint8_t* {
+            const int row_sid = __shfl(sid, sr, 64);
+            if (row_sid >= p.numel) return nullptr;
+            return reinterpret_cast<uint8_t*>(
+                static_cast<float*>(p.out) +
+                (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out + col_base + jp0 * 32);
+          });
         }
-      }
-    } else {
-      uint16_t* orow = out + static_cast<int64_t>(sid) * p.n_out;
+      } else {
+        constexpr int JP = pass_blocks(2, CB);
+        constexpr std::integral_constant<int, JP * 4> ch{};
+        static_assert(32 * JP * 32 * 2 <= REGION, "staging fits");
 #pragma unroll
-      for (int j = 0; j < CB; ++j) {
-        const int col0 = tile_n * BNR + wn * WCOLS + j * 32 + csub;
+        for (int jp0 = 0; jp0 < CB; jp0 += JP) {
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const f32x4 sw = wscale4(col0 + 8 * g4);
-          const f32x4 bb = bias4(col0 + 8 * g4);
-          const int v = 4 * g4;
-          uint2 v2;
-          v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
-                             value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
-          v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
-                             value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
-          *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
+          for (int jl = 0; jl < JP; ++jl) {
+            const int j = jp0 + jl;
+            const int col0 = col_base + j * 32 + csub;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const f32x4 sw = wscale4(col0 + 8 * g4);
+              const f32x4 bb = bias4(col0 + 8 * g4);
+              const int v = 4 * g4;
+              uint2 v2;
+              v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
+                                 value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
+              v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                                 value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
+              *reinterpret_cast<uint2*>(slot_at(ch, r, jl * 4 + g4) + half * 8) = v2;
+            }
+          }
+          drain(ch, [&](int sr) -> uint8_t* {
+            const int row_sid = __shfl(sid, sr, 64);
+            if (row_sid >= p.numel) return nullptr;
+            return reinterpret_cast<uint8_t*>(out + static_cast<int64_t>(row_sid) * p.n_out +
+                                              col_base + jp0 * 32);
+          });
         }
       }
     }

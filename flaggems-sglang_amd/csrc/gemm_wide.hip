@@ -332,15 +332,25 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     }
     mma(fa[1], fb[1]);
 
-    // ---- epilogue (as moe_gemm_tiled_kernel): lane owns token row
+    // ---- epilogue (the tiled kernel's arithmetic): lane owns token row
     // (lane & 31) of each 32-row block and, per 32-column block, columns
-    // 8*q + 4*(lane>>5) + {0..3} (accumulator registers 4q..4q+3).
+    // 8*q + 4*(lane>>5) + {0..3} (accumulator registers 4q..4q+3). A store
+    // straight from that layout would touch 32 output rows per
+    // instruction; instead each 32-row block goes through this wave's
+    // quarter of a free ring slot (stage KT-2's: no wave reads it again and
+    // no refill targets it) and leaves as whole row segments, 16 bytes per
+    // lane. Chunks (16 bytes) of a staged row are XOR-swizzled by the row so
+    // the column-major writes spread over the banks.
     {
       const int ks = cur.ks;
       const int64_t wbase = static_cast<int64_t>(cur.e) * p.nrows_w;
-      uint16_t* out = static_cast<uint16_t*>(p.out);
       const int csub = 4 * (lane >> 5);
+      const int half = lane >> 5;
       const float* wsc = INT8 ? p.w_scale + wbase : nullptr;
+      const int fslot = (KT - 2) % NS;
+      uint8_t* stg = lds + (wave < 2 ? fslot * SLOT + wave * (SLOT / 2)
+                                     : B_OFF + fslot * SLOT + (wave - 2) * (SLOT / 2));
+      static_assert(SLOT / 2 >= 32 * WCOLS * 4, "a 32-row fp32 block fits a wave's staging");
       auto wscale4 = [&](int64_t wrow) -> f32x4 {
         if constexpr (INT8) return *reinterpret_cast<const f32x4*>(wsc + wrow);
         else return f32x4{1.f, 1.f, 1.f, 1.f};
@@ -349,24 +359,34 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
         if constexpr (INT8) return static_cast<float>(a[v]) * sa * sw;
         else return a[v];
       };
+      // orders this wave's staging writes before its reads (and the reads
+      // before the next block's writes)
+      auto stage_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      };
       if constexpr (GEMM1) {
-        // silu, no bias (the launch guarantees both); the router-weight
-        // scaling is a compile-time branch so the common case carries no
-        // per-element select
+        // silu, no bias (the launch guarantees both): 64 output columns per
+        // wave, 128-byte staged rows (8 chunks). The router-weight scaling is
+        // a compile-time branch so the common case carries no per-element
+        // select.
+        constexpr int CH = WCOLS / 2 / 8;  // chunks per staged row
+        uint16_t* out = static_cast<uint16_t*>(p.out);
+        const int col_base = cur.ct * (BNR / 2) + wn * (WCOLS / 2);
         auto emit = [&](auto scale_c) {
           constexpr bool SCALE = decltype(scale_c)::value;
 #pragma unroll
-          for (int i = 0; i < RB; ++i) {
+          for (int i = 0; i < NLIVE; ++i) {
             const int rr = i * 64 + wm * 32 + (lane & 31);
-            const int r = row0 + rr;
-            const int sid = p.sorted_ids[r];
-            if (sid >= p.numel) continue;  // pad rows: never stored
+            const int sid = p.sorted_ids[row0 + rr];
+            const bool ok = sid < p.numel;
             const float sa = INT8 ? p.a_scale[act_row(row0, rr)] : 1.f;
-            const float gamma = SCALE ? p.topk_w[sid] : 1.f;
-            uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
+            const float gamma = SCALE && ok ? p.topk_w[sid] : 1.f;
+            const int r = lane & 31;
 #pragma unroll
             for (int jb = 0; jb < CB / 2; ++jb) {
-              const int col0 = cur.ct * (BNR / 2) + wn * (WCOLS / 2) + jb * 32 + csub;
+              const int col0 = col_base + jb * 32 + csub;
 #pragma unroll
               for (int g4 = 0; g4 < 4; ++g4) {
                 const f32x4 swg = wscale4(col0 + 8 * g4);
@@ -381,9 +401,24 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
                 v2.y = silu_mul_bf16x2<SCALE>(
                     value(ag, v + 2, sa, swg[2]), value(ag, v + 3, sa, swg[3]),
                     value(au, v + 2, sa, swu[2]), value(au, v + 3, sa, swu[3]), gamma);
-                *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
+                const int c = jb * 4 + g4;
+                *reinterpret_cast<uint2*>(stg + r * (CH * 16) + ((c ^ (r % CH)) * 16) + half * 8) = v2;
               }
             }
+            stage_sync();
+            // 8 lanes per row, 8 rows per pass
+#pragma unroll
+            for (int k = 0; k < 32 / (64 / CH); ++k) {
+              const int sr = k * (64 / CH) + lane / CH;
+              const int c = lane % CH;
+              const int row_sid = __shfl(sid, sr, 64);
+              const uint4 val = *reinterpret_cast<const uint4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
+              if (row_sid < p.numel) {
+                const int64_t orow = row0 + i * 64 + wm * 32 + sr;
+                *reinterpret_cast<uint4*>(out + orow * p.n_out + col_base + c * 8) = val;
+              }
+            }
+            stage_sync();
           }
         };
         if (p.weight_on_input) emit(std::true_type{});
@@ -394,36 +429,52 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
           return bias ? *reinterpret_cast<const f32x4*>(bias + col)
                       : f32x4{0.f, 0.f, 0.f, 0.f};
         };
+        const int col_base = cur.ct * BNR + wn * WCOLS;
 #pragma unroll
-        for (int i = 0; i < RB; ++i) {
+        for (int i = 0; i < NLIVE; ++i) {
           const int rr = i * 64 + wm * 32 + (lane & 31);
-          const int r = row0 + rr;
-          const int sid = p.sorted_ids[r];
-          if (sid >= p.numel) continue;  // pad rows: never stored
+          const int sid = p.sorted_ids[row0 + rr];
           const float sa = INT8 ? p.a_scale[act_row(row0, rr)] : 1.f;
+          const int r = lane & 31;
           if (p.ksplit > 1) {
-            float* orow = static_cast<float*>(p.out) +
-                          (static_cast<int64_t>(ks) * p.numel + sid) * p.n_out;
+            // fp32 partials: 512-byte staged rows (32 chunks), 2 rows per pass
+            constexpr int CH = WCOLS * 4 / 16;
 #pragma unroll
             for (int j = 0; j < CB; ++j) {
-              const int col0 = cur.ct * BNR + wn * WCOLS + j * 32 + csub;
+              const int col0 = col_base + j * 32 + csub;
 #pragma unroll
               for (int g4 = 0; g4 < 4; ++g4) {
                 const f32x4 sw = wscale4(col0 + 8 * g4);
                 const f32x4 bb = bias4(col0 + 8 * g4);
                 const int v = 4 * g4;
-                *reinterpret_cast<f32x4*>(orow + col0 + 8 * g4) =
+                const int c = j * 8 + g4 * 2 + half;
+                *reinterpret_cast<f32x4*>(stg + r * (CH * 16) + ((c ^ (r % CH)) * 16)) =
                     f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0],
                           value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
                           value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
                           value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
               }
             }
+            stage_sync();
+            float* outf = static_cast<float*>(p.out);
+#pragma unroll
+            for (int k = 0; k < 32 / (64 / CH); ++k) {
+              const int sr = k * (64 / CH) + lane / CH;
+              const int c = lane % CH;
+              const int row_sid = __shfl(sid, sr, 64);
+              const f32x4 val = *reinterpret_cast<const f32x4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
+              if (row_sid < p.numel)
+                *reinterpret_cast<f32x4*>(outf + (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out +
+                                          col_base + c * 4) = val;
+            }
+            stage_sync();
           } else {
-            uint16_t* orow = out + static_cast<int64_t>(sid) * p.n_out;
+            // bf16 rows: 256-byte staged rows (16 chunks), 4 rows per pass
+            constexpr int CH = WCOLS * 2 / 16;
+            uint16_t* out = static_cast<uint16_t*>(p.out);
 #pragma unroll
             for (int j = 0; j < CB; ++j) {
-              const int col0 = cur.ct * BNR + wn * WCOLS + j * 32 + csub;
+              const int col0 = col_base + j * 32 + csub;
 #pragma unroll
               for (int g4 = 0; g4 < 4; ++g4) {
                 const f32x4 sw = wscale4(col0 + 8 * g4);
@@ -434,9 +485,21 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
                                    value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
                 v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
                                    value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
-                *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
+                const int c = j * 4 + g4;
+                *reinterpret_cast<uint2*>(stg + r * (CH * 16) + ((c ^ (r % CH)) * 16) + half * 8) = v2;
               }
             }
+            stage_sync();
+#pragma unroll
+            for (int k = 0; k < 32 / (64 / CH); ++k) {
+              const int sr = k * (64 / CH) + lane / CH;
+              const int c = lane % CH;
+              const int row_sid = __shfl(sid, sr, 64);
+              const uint4 val = *reinterpret_cast<const uint4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
+              if (row_sid < p.numel)
+                *reinterpret_cast<uint4*>(out + static_cast<int64_t>(row_sid) * p.n_out + col_base + c * 8) = val;
+            }
+            stage_sync();
           }
         }
       }

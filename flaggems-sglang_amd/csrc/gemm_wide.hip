@@ -203,6 +203,24 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
 #pragma unroll
     for (int i = 0; i < NLB; ++i) lds_dma16_buf(rb, s.vb[i], kbyte, b_dst + i * 1024);
   };
+  // One operand's loads of a stage: PART 0 the activation rows, 1 the
+  // weight rows.
+  auto issue_part = [&](const Src& s, int kbyte, int slot, auto part_c) {
+    constexpr int PART = decltype(part_c)::value;
+    kbyte = __builtin_amdgcn_readfirstlane(kbyte);
+    if constexpr (PART == 0) {
+      uint8_t* a_dst = lds + slot * SLOT + wave * NLA * 1024;
+#pragma unroll
+      for (int i = 0; i < NLA; ++i) lds_dma16_buf(ra, s.va[i], kbyte, a_dst + i * 1024);
+    } else {
+      const int e = __builtin_amdgcn_readfirstlane(s.e);
+      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(p.w) + static_cast<int64_t>(e) * w_bytes, 0, w_bytes, kBufWord3);
+      uint8_t* b_dst = lds + B_OFF + slot * SLOT + wave * NLB * 1024;
+#pragma unroll
+      for (int i = 0; i < NLB; ++i) lds_dma16_buf(rb, s.vb[i], kbyte, b_dst + i * 1024);
+    }
+  };
 
   // Fragment reads: lane reads row (lane & 31) of a 32-row block, logical
   // chunk 2*kk + (lane >> 5). Offsets within the wave's A / B region.
@@ -265,69 +283,93 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
         for (int j = 0; j < CB; ++j) acc[i][j] = T::mma(b[j], a[i], acc[i][j]);
     };
     // the next k step's fragment reads, one after each of the first MFMAs
-    // (measured 1.3 % faster than issuing all eight after the first MFMA)
-    auto sched_step = [&]() {
+    // (measured 1.3 % faster than issuing all eight after the first MFMA),
+    // then ND loads one between each pair of the remaining MFMAs
+    auto sched_step = [&](auto nd_c) {
+      constexpr int ND = decltype(nd_c)::value;
       if constexpr (NLIVE > 0) {
 #pragma unroll
         for (int t = 0; t < RB + CB; ++t) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        if constexpr (NLIVE * CB > RB + CB)
-          __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - (RB + CB), 0);
+#pragma unroll
+        for (int t = 0; t < ND; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          if (t < NLIVE * CB - (RB + CB)) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        if constexpr (NLIVE * CB > RB + CB + ND)
+          __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - (RB + CB) - ND, 0);
       }
     };
     // after a stage barrier: one MFMA, the next k step's fragment reads,
-    // then the stage's refill loads one between each pair of MFMAs, so the
-    // wave never stalls on a burst of vector-memory issues
-    auto sched_tail = [&]() {
+    // then ND loads one between each pair of MFMAs, so the wave never
+    // stalls on a burst of vector-memory issues
+    auto sched_tail = [&](auto nd_c) {
+      constexpr int ND = decltype(nd_c)::value;
       if constexpr (NLIVE > 0) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, RB + CB, 0);
 #pragma unroll
-        for (int t = 0; t < NL; ++t) {
+        for (int t = 0; t < ND; ++t) {
           __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
           if (t < NLIVE * CB - 1) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
-        if constexpr (NLIVE * CB - 1 > NL)
-          __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - 1 - NL, 0);
+        if constexpr (NLIVE * CB - 1 > ND)
+          __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - 1 - ND, 0);
       }
     };
     // The barrier before the last k step of stage s publishes stage s+1
-    // (every wave has waited for its own loads of it; later stages may
-    // still be in flight) and frees slot s % NS, which then takes stage
-    // s+NS when there is one.
-    auto stage = [&](int s, bool refill) {
+    // (every wave has waited for its own loads of it) and frees slot s % 2,
+    // which then takes stage s+2 when there is one: its activation rows
+    // right after the barrier, its weight rows during the first k step of
+    // stage s+1 (REFILL / PREV), so a CU's 64 loads of a stage are spread
+    // over two k steps instead of one (measured: Qwen3 M=8192 GEMM1 -6 %,
+    // GEMM2 -4 %, Qwen2 GEMM2 -4.5 %, Mixtral GEMM1 -1 %).
+    static_assert(NS == 2, "the refill schedule assumes a two-slot ring");
+    auto stage = [&](int s, auto refill_c, auto prev_c) {
+      constexpr bool REFILL = decltype(refill_c)::value;
+      constexpr bool PREV = decltype(prev_c)::value;
       const int slot = s % NS;
 #pragma unroll
       for (int kk = 0; kk + 1 < KK; ++kk) {
         read_frags(slot, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+        if (PREV && kk == 0)
+          issue_part(src, (cur.kt0 + s + 1) * SK, (s + 1) % NS, std::integral_constant<int, 1>{});
         mma(fa[kk & 1], fb[kk & 1]);
-        sched_step();
+        if (PREV && kk == 0) sched_step(std::integral_constant<int, NLB>{});
+        else sched_step(std::integral_constant<int, 0>{});
         __builtin_amdgcn_sched_barrier(0);
       }
       wait_lgkm0();
-      if (refill) wait_vmcnt<(NS - 2) * NL>();
-      else wait_vmcnt<0>();
+      wait_vmcnt<0>();
       wave_barrier_all();
       read_frags((s + 1) % NS, 0, fa[0], fb[0]);
-      if (refill) issue(src, (cur.kt0 + s + NS) * SK, slot);
+      if constexpr (REFILL)
+        issue_part(src, (cur.kt0 + s + NS) * SK, slot, std::integral_constant<int, 0>{});
       mma(fa[1], fb[1]);
-      sched_tail();
+      sched_tail(std::integral_constant<int, REFILL ? NLA : 0>{});
       __builtin_amdgcn_sched_barrier(0);
     };
     wait_vmcnt<(NS - 1) * NL>();
     wave_barrier_all();
     read_frags(0, 0, fa[0], fb[0]);
     int s = 0;
-    for (; s + NS < KT; ++s) stage(s, true);
-    for (; s + 1 < KT; ++s) stage(s, false);
+    if (NS < KT) {
+      stage(0, std::true_type{}, std::false_type{});
+      for (s = 1; s + NS < KT; ++s) stage(s, std::true_type{}, std::true_type{});
+      if (s + 1 < KT) {
+        stage(s, std::false_type{}, std::true_type{});
+        ++s;
+      }
+    }
+    for (; s + 1 < KT; ++s) stage(s, std::false_type{}, std::false_type{});
     const int slot = (KT - 1) % NS;
 #pragma unroll
     for (int kk = 0; kk + 1 < KK; ++kk) {
       read_frags(slot, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
       mma(fa[kk & 1], fb[kk & 1]);
-      sched_step();
+      sched_step(std::integral_constant<int, 0>{});
       __builtin_amdgcn_sched_barrier(0);
     }
     mma(fa[1], fb[1]);

@@ -230,6 +230,25 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
       lds_dma16(b_src[i] + koff, base + A_BYTES + (wave * NLB + i) * 1024);
     if constexpr (FP8) lds_dma4(sc_src + kt, base + SC_OFF + wave * 256);
   };
+  // With a two-slot ring (bf16 / int8) a freed slot's refill is split: the
+  // activation rows right after the barrier, the weight rows during the
+  // next stage's first k step, so a CU's loads of a stage are spread over
+  // two k steps.
+  constexpr bool SPLIT = STAGES == 2 && !FP8;
+  auto issue_part = [&](int kt, int slot, auto part_c) {
+    constexpr int PART = decltype(part_c)::value;
+    const int64_t koff = static_cast<int64_t>(kt) * SK;
+    uint8_t* base = lds + slot * STAGE;
+    if constexpr (PART == 0) {
+#pragma unroll
+      for (int i = 0; i < NLA; ++i)
+        lds_dma16(a_src[i] + koff, base + (wave * NLA + i) * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NLB; ++i)
+        lds_dma16(b_src[i] + koff, base + A_BYTES + (wave * NLB + i) * 1024);
+    }
+  };
 
   Acc acc[RB][CB];
 #pragma unroll
@@ -341,6 +360,20 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
       __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - 1, 0);
     };
+    // ... with the weight-row loads of a split refill one between each pair
+    // of the remaining MFMAs
+    auto sched_step_dma = [&]() {
+      constexpr int NR = (RB + CB) * FC;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+      for (int t = 0; t < NLB; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        if (t < NLIVE * CB - 1) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      if constexpr (NLIVE * CB - 1 > NLB)
+        __builtin_amdgcn_sched_group_barrier(0x008, NLIVE * CB - 1 - NLB, 0);
+    };
     auto fold = [&]() {
       if constexpr (FP8) {
 #pragma unroll
@@ -365,18 +398,28 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
     wave_barrier_all();
     read_frags(0, 0, fa[0], fb[0]);
     if constexpr (FP8) read_scales(0, sa_c, sw_c);
-    for (int kt = 0; kt + 1 < KT; ++kt) {
+    // PREV (split refills, from the second stage on): the weight rows of
+    // stage kt+1, whose slot was freed at the previous barrier
+    auto body = [&](int kt, auto prev_c) {
+      constexpr bool PREV = decltype(prev_c)::value;
 #pragma unroll
       for (int kk = 0; kk + 1 < KK; ++kk) {
         read_frags(kt, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+        if constexpr (PREV) {
+          if (kk == 0) issue_part(kt + 1, (kt + 1) % STAGES, std::integral_constant<int, 1>{});
+        }
         mma(kk, fa[kk & 1], fb[kk & 1]);
-        sched_step();
+        if (PREV && kk == 0) sched_step_dma();
+        else sched_step();
         __builtin_amdgcn_sched_barrier(0);
       }
       wait_lgkm0();
       wait_stages(min(STAGES - 2, KT - 2 - kt));
       wave_barrier_all();
-      if (kt + STAGES < KT) issue(kt + STAGES, kt % STAGES);
+      if (kt + STAGES < KT) {
+        if constexpr (SPLIT) issue_part(kt + STAGES, kt % STAGES, std::integral_constant<int, 0>{});
+        else issue(kt + STAGES, kt % STAGES);
+      }
       read_frags(kt + 1, 0, fa[KK & 1], fb[KK & 1]);
       if constexpr (FP8) read_scales(kt + 1, sa_n, sw_n);
       mma(KK - 1, fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
@@ -395,6 +438,14 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
 #pragma unroll
         for (int j = 0; j < CB; ++j) fb[0][j] = fb[1][j];
       }
+    };
+    if constexpr (SPLIT) {
+      // stages 0 and 1 were loaded whole; from stage 1 on each stage
+      // finishes the refill begun at the previous barrier
+      if (KT > 1) body(0, std::false_type{});
+      for (int kt = 1; kt + 1 < KT; ++kt) body(kt, std::true_type{});
+    } else {
+      for (int kt = 0; kt + 1 < KT; ++kt) body(kt, std::false_type{});
     }
 #pragma unroll
     for (int kk = 0; kk + 1 < KK; ++kk) {

@@ -172,11 +172,19 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   // ---- this lane's source of each LDS-DMA load: row lane/CPR, chunk lane%CPR
   const int lrow = lane / C::CPR;
   const int lchunk = lane % C::CPR;
+  // all token slots first: computing a row (GEMM1 divides by topk for real
+  // rows only) compiles to a branch, which would otherwise hold each load
+  // back until the previous row is done
   const uint8_t* a_src[NLA];
+  int a_sid[NLA];
+#pragma unroll
+  for (int i = 0; i < NLA; ++i) a_sid[i] = p.sorted_ids[row0 + (wave * NLA + i) * C::LR + lrow];
 #pragma unroll
   for (int i = 0; i < NLA; ++i) {
     const int r = (wave * NLA + i) * C::LR + lrow;
-    a_src[i] = p.a + act_row(r) * row_bytes + chunk_pos<C>(r, lchunk) * 16;
+    const bool ok = a_sid[i] < p.numel;
+    const int64_t arow = GEMM1 ? (ok ? a_sid[i] / p.topk : 0) : row0 + (ok ? r : 0);
+    a_src[i] = p.a + arow * row_bytes + chunk_pos<C>(r, lchunk) * 16;
   }
   const uint8_t* b_src[NLB];
   const int64_t wbase = static_cast<int64_t>(e) * p.nrows_w;
@@ -278,6 +286,17 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
 #pragma unroll
   for (int i = 0; i < NLB; ++i) b_src[i] += static_cast<int64_t>(kt0) * SK;
   if constexpr (FP8) sc_src += kt0;
+  // the first token slot of each of the wave's 32-row blocks, loaded before
+  // the stage loads: the counter drains in issue order, so waiting on these
+  // never waits on a stage load
+  int first_sid[RB];
+#pragma unroll
+  for (int i = 0; i < RB; ++i) first_sid[i] = p.sorted_ids[row0 + wm * WROWS + i * 32];
+  // activation row (a_scale index) of tile row rr holding slot sid
+  auto act_of = [&](int rr, int sid) -> int64_t {
+    const bool ok = sid < p.numel;
+    return GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? rr : 0);
+  };
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < KT) issue(s, s);
@@ -329,8 +348,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   // last block) skip their MFMAs without branches inside the MFMA stream.
   int nlive = 0;
 #pragma unroll
-  for (int i = 0; i < RB; ++i)
-    nlive += p.sorted_ids[row0 + wm * WROWS + i * 32] < p.numel ? 1 : 0;
+  for (int i = 0; i < RB; ++i) nlive += first_sid[i] < p.numel ? 1 : 0;
 
   Frag fa[2][RB], fb[2][CB];
   auto main_loop = [&](auto nlive_c) {
@@ -538,9 +556,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
           if (i >= nlive) break;  // all-pad blocks (wave-uniform)
           const int rr = wm * WROWS + i * 32 + (lane & 31);
           const int sid = p.sorted_ids[row0 + rr];
-          const bool ok = sid < p.numel;
-          const float sa = INT8 ? p.a_scale[act_row(rr)] : 1.f;
-          const float gamma = SCALE && ok ? p.topk_w[sid] : 1.f;
+          const float sa = INT8 ? p.a_scale[act_of(rr, sid)] : 1.f;
+          const float gamma = SCALE && sid < p.numel ? p.topk_w[sid] : 1.f;
           const int r = lane & 31;
 #pragma unroll
           for (int jp0 = 0; jp0 < CB / 2; jp0 += JP) {
@@ -621,7 +638,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
       if (i >= nlive) break;  // all-pad blocks (wave-uniform)
       const int rr = wm * WROWS + i * 32 + (lane & 31);
       const int sid = p.sorted_ids[row0 + rr];
-      const float sa = INT8 ? p.a_scale[act_row(rr)] : 1.f;
+      const float sa = INT8 ? p.a_scale[act_of(rr, sid)] : 1.f;
       const int r = lane & 31;
       if (p.ksplit > 1) {
         // fp32 partial sums of split ks, reduced in fixed order by moe_sum

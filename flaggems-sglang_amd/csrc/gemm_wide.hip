@@ -154,19 +154,21 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   };
   const int lrow = lane / C::CPR;   // row of a load this lane copies
   const int lchunk = lane % C::CPR;  // its physical chunk
-  auto act_row = [&](int row0, int r) -> int64_t {
-    const int sid = p.sorted_ids[row0 + r];
-    const bool ok = sid < p.numel;
-    return GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? r : 0);
-  };
   auto make_src = [&](const Tile& t, Src& s) {
     const int row0 = t.rb * BM;
     s.e = t.e;
+    // all token slots first: computing a row (GEMM1 divides by topk for
+    // real rows only) compiles to a branch, which would otherwise hold each
+    // load back until the previous row is done
+    int sid[NLA];
+#pragma unroll
+    for (int i = 0; i < NLA; ++i) sid[i] = p.sorted_ids[row0 + (wave * NLA + i) * C::LR + lrow];
 #pragma unroll
     for (int i = 0; i < NLA; ++i) {
       const int r = (wave * NLA + i) * C::LR + lrow;
-      s.va[i] = static_cast<uint32_t>(act_row(row0, r) * row_bytes +
-                                      wide_chunk<C>(r, lchunk) * 16);
+      const bool ok = sid[i] < p.numel;
+      const int64_t arow = GEMM1 ? (ok ? sid[i] / p.topk : 0) : row0 + (ok ? r : 0);
+      s.va[i] = static_cast<uint32_t>(arow * row_bytes + wide_chunk<C>(r, lchunk) * 16);
     }
 #pragma unroll
     for (int i = 0; i < NLB; ++i) {
@@ -238,18 +240,23 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   if (cur.pos >= n_pos || !live_tile(cur.pos, cur)) return;
   Src src;
   make_src(cur, src);
+  const int row0 = cur.rb * BM;
+  // the first token slot of each of the wave's 32-row blocks, loaded before
+  // the stage loads: the counter drains in issue order, so waiting on these
+  // never waits on a stage load
+  int first_sid[RB];
+#pragma unroll
+  for (int i = 0; i < RB; ++i) first_sid[i] = p.sorted_ids[row0 + i * 64 + wm * 32];
   // stage s lives in ring slot s % NS; stages 0..NS-1 load first
   const int KT = cur.KT;
 #pragma unroll
   for (int s = 0; s < NS; ++s) issue(src, (cur.kt0 + s) * SK, s);
 
-  const int row0 = cur.rb * BM;
   // live 32-row blocks of this wave (pad rows are a suffix of the tile, so
   // the wave's live blocks are a prefix of i)
   int nlive = 0;
 #pragma unroll
-  for (int i = 0; i < RB; ++i)
-    nlive += p.sorted_ids[row0 + i * 64 + wm * 32] < p.numel ? 1 : 0;
+  for (int i = 0; i < RB; ++i) nlive += first_sid[i] < p.numel ? 1 : 0;
   nlive = __builtin_amdgcn_readfirstlane(nlive);
 
   // The tile (accumulators, k loop, epilogue) is instantiated per count of
@@ -386,6 +393,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     {
       const int ks = cur.ks;
       const int64_t wbase = static_cast<int64_t>(cur.e) * p.nrows_w;
+
+
       const int csub = 4 * (lane >> 5);
       const int half = lane >> 5;
       const float* wsc = INT8 ? p.w_scale + wbase : nullptr;
@@ -420,10 +429,9 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
           constexpr bool SCALE = decltype(scale_c)::value;
 #pragma unroll
           for (int i = 0; i < NLIVE; ++i) {
-            const int rr = i * 64 + wm * 32 + (lane & 31);
-            const int sid = p.sorted_ids[row0 + rr];
+            const int sid = p.sorted_ids[row0 + i * 64 + wm * 32 + (lane & 31)];
             const bool ok = sid < p.numel;
-            const float sa = INT8 ? p.a_scale[act_row(row0, rr)] : 1.f;
+            const float sa = INT8 ? p.a_scale[ok ? sid / p.topk : 0] : 1.f;
             const float gamma = SCALE && ok ? p.topk_w[sid] : 1.f;
             const int r = lane & 31;
 #pragma unroll
@@ -476,7 +484,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
         for (int i = 0; i < NLIVE; ++i) {
           const int rr = i * 64 + wm * 32 + (lane & 31);
           const int sid = p.sorted_ids[row0 + rr];
-          const float sa = INT8 ? p.a_scale[act_row(row0, rr)] : 1.f;
+          const float sa = INT8 ? p.a_scale[row0 + (sid < p.numel ? rr : 0)] : 1.f;
           const int r = lane & 31;
           if (p.ksplit > 1) {
             // fp32 partials: 512-byte staged rows (32 chunks), 2 rows per pass

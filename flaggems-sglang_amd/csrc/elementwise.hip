@@ -85,6 +85,56 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(
   }
 }
 
+// moe_sum_kernel for a compile-time top-k: a thread issues its TK row loads
+// before any of the dropped-slot checks (a runtime loop with a `continue`
+// keeps each load behind the previous slot's check: TK round trips in
+// series), then sums in slot order with the same roundings. Every slot has a
+// row in `in`, so the loads stay in bounds whatever the ids say.
+template <int TK>
+__global__ __launch_bounds__(256) void moe_sum_tk_kernel(
+    const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int64_t m,
+    int64_t k, const int32_t* __restrict__ ids, int num_experts,
+    const float* __restrict__ weights) {
+  const int64_t vec_per_row = k / 8;
+  const int64_t total = m * vec_per_row;
+  for (int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+       v < total; v += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t t = v / vec_per_row;
+    const int64_t c = (v - t * vec_per_row) * 8;
+    const uint16_t* src = in + t * TK * k + c;
+    u32x4 x[TK];
+#pragma unroll
+    for (int j = 0; j < TK; ++j) x[j] = *reinterpret_cast<const u32x4*>(src + j * k);
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+      if (ids) {
+        const int e = ids[t * TK + j];
+        if (e < 0 || e >= num_experts) continue;
+      }
+      if (weights) {
+        const float w = weights[t * TK + j];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] = __fadd_rn(acc[2 * q], __fmul_rn(w, __uint_as_float(x[j][q] << 16)));
+          acc[2 * q + 1] =
+              __fadd_rn(acc[2 * q + 1], __fmul_rn(w, __uint_as_float(x[j][q] & 0xffff0000u)));
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] += __uint_as_float(x[j][q] << 16);
+          acc[2 * q + 1] += __uint_as_float(x[j][q] & 0xffff0000u);
+        }
+      }
+    }
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
+    *reinterpret_cast<u32x4*>(out + t * k + c) = o;
+  }
+}
+
 // moe_sum over fp32 split-K partials: 4 columns per thread.
 __global__ __launch_bounds__(256) void moe_sum_partials_kernel(
     const float* __restrict__ part, int nsplit, uint16_t* __restrict__ out,
@@ -250,20 +300,32 @@ int launch_silu_and_mul(const void* in, void* out, int64_t rows, int64_t n,
   return check_launch("silu_and_mul_kernel");
 }
 
+int launch_moe_sum_routed(const void* in, void* out, int64_t m, int topk,
+                          int64_t k, const int32_t* ids, int num_experts,
+                          const float* weights, hipStream_t stream);
+
 int launch_moe_sum(const void* in, void* out, int64_t m, int topk, int64_t k,
                    hipStream_t stream) {
-  if (m == 0) return FGS_OK;
-  hipLaunchKernelGGL(moe_sum_kernel, dim3(grid_for(m * (k / 8), 256)),
-                     dim3(256), 0, stream, static_cast<const uint16_t*>(in),
-                     static_cast<uint16_t*>(out), m, topk, k, nullptr, 0,
-                     nullptr);
-  return check_launch("moe_sum_kernel");
+  return launch_moe_sum_routed(in, out, m, topk, k, nullptr, 0, nullptr, stream);
 }
 
 int launch_moe_sum_routed(const void* in, void* out, int64_t m, int topk,
                           int64_t k, const int32_t* ids, int num_experts,
                           const float* weights, hipStream_t stream) {
   if (m == 0) return FGS_OK;
+  const dim3 grid(grid_for(m * (k / 8), 256));
+  const uint16_t* src = static_cast<const uint16_t*>(in);
+  uint16_t* dst = static_cast<uint16_t*>(out);
+  if (topk == 8) {
+    hipLaunchKernelGGL(moe_sum_tk_kernel<8>, grid, dim3(256), 0, stream, src, dst, m, k, ids,
+                       num_experts, weights);
+    return check_launch("moe_sum_tk_kernel");
+  }
+  if (topk == 2) {
+    hipLaunchKernelGGL(moe_sum_tk_kernel<2>, grid, dim3(256), 0, stream, src, dst, m, k, ids,
+                       num_experts, weights);
+    return check_launch("moe_sum_tk_kernel");
+  }
   hipLaunchKernelGGL(moe_sum_kernel, dim3(grid_for(m * (k / 8), 256)),
                      dim3(256), 0, stream, static_cast<const uint16_t*>(in),
                      static_cast<uint16_t*>(out), m, topk, k, ids, num_experts,

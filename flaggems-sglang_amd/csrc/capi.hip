@@ -38,7 +38,8 @@ static int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 constexpr int kMaxExperts = 1024;
 constexpr int kKnownFlags = FGS_FLAG_ROUTER_WEIGHT_ON_INPUT | FGS_FLAG_ACT_GELU |
                             FGS_FLAG_FORCE_DECODE | FGS_FLAG_FORCE_PREFILL |
-                            FGS_FLAG_SEPARATE_SUM | FGS_FLAG_TILE_MASK;
+                            FGS_FLAG_SEPARATE_SUM | FGS_FLAG_FOLD_SUM |
+                            FGS_FLAG_TILE_MASK;
 
 static int max_padded_of(int64_t numel, int e, int block) {
   return static_cast<int>(numel + static_cast<int64_t>(e) * (block - 1));
@@ -93,8 +94,9 @@ static int pick_ksplit(int64_t numel, int e, int bm, int64_t hidden,
 }
 
 // FGS_MOE_DIRECT selects the single-token schedule (a tuning aid; read
-// once): 0 aligned rows, 1 (the default) or 3 direct rows with GEMM2
-// folding the top-k sum, 2 direct rows with moe_sum.
+// once): 0 aligned rows, 1 direct rows with GEMM2 folding the top-k sum
+// for bf16 / int8 outputs of >= 192 column tiles (the default), 2 direct
+// rows with moe_sum, 3 direct rows, always folded.
 static int direct_choice() {
   static const int d = [] {
     const char* v = getenv("FGS_MOE_DIRECT");
@@ -178,12 +180,17 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   p.kw2 = pick_kw(inter, step, 8);
   // One token: its top-k slots go to distinct experts, so the streaming
   // GEMMs take slot j as row tile j (expert topk_ids[j]) and the alignment
-  // is skipped; GEMM2 also folds the weighted top-k sum (no moe_sum).
+  // is skipped; GEMM2 also folds the weighted top-k sum when the output
+  // spans enough column tiles (one workgroup each) to fill the chip.
   const int dc = direct_choice();
   p.direct = !p.tiled && m == 1 && dc != 0;
-  // (measured without per-stage events: Qwen3 -6 %, Qwen2 int8 -10 %,
-  // Mixtral -3 %, DeepSeek fp8 level)
-  p.direct_sum = p.direct && dc != 2 && !(flags & FGS_FLAG_SEPARATE_SUM);
+  // (measured, 3 x 100 flushed calls: folding wins for bf16 / int8 from 192
+  // column tiles -- Qwen2 int8 -6.5 %, Mixtral -2 % -- and loses for Qwen3's
+  // 128 tiles, +1.5 %, and for fp8, whose per-step block scales keep the
+  // unfolded GEMM2 + moe_sum ahead, +3 %)
+  p.direct_sum = p.direct && !(flags & FGS_FLAG_SEPARATE_SUM) &&
+                 ((flags & FGS_FLAG_FOLD_SUM) || dc == 3 ||
+                  (dc == 1 && p.dt != kDtFp8 && hidden / 16 >= 192));
   // the folded GEMM2's waves: as many as keep its grid (one workgroup per
   // 16 output columns) resident in one round at 16 waves per CU
   const int64_t wgs = hidden / 16;
@@ -235,6 +242,8 @@ static int validate(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
       qmode != FGS_QMODE_INT8_CHANNEL)
     return fail(FGS_EINVAL, "unknown qmode");
   if (flags & ~kKnownFlags) return fail(FGS_EINVAL, "unknown flag bits");
+  if ((flags & FGS_FLAG_SEPARATE_SUM) && (flags & FGS_FLAG_FOLD_SUM))
+    return fail(FGS_EINVAL, "FGS_FLAG_SEPARATE_SUM and FGS_FLAG_FOLD_SUM exclude each other");
   if ((flags & FGS_FLAG_FORCE_DECODE) &&
       (flags & (FGS_FLAG_FORCE_PREFILL | FGS_FLAG_TILE_MASK)))
     return fail(FGS_EINVAL, "FORCE_DECODE excludes FORCE_PREFILL / TILE");

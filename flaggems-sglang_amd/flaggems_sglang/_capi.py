@@ -28,6 +28,7 @@ FLAG_ACT_GELU = 0x2
 FLAG_FORCE_DECODE = 0x100
 FLAG_FORCE_PREFILL = 0x200
 FLAG_SEPARATE_SUM = 0x400
+FLAG_FOLD_SUM = 0x800
 TILED_CONFIGS = 4  # row blocks 256, 128, 64, 32
 
 

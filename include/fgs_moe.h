@@ -52,8 +52,10 @@ extern "C" {
 #define FGS_FLAG_FORCE_DECODE 0x100         /* schedule: streaming kernels  */
 #define FGS_FLAG_FORCE_PREFILL 0x200        /* schedule: LDS-tiled kernels  */
 /* schedule: the weighted top-k sum runs as its own kernel (moe_sum); a
- * one-token call otherwise folds it into GEMM2 */
+ * one-token call otherwise folds it into GEMM2 when that is faster */
 #define FGS_FLAG_SEPARATE_SUM 0x400
+/* schedule: a one-token call folds the weighted top-k sum into GEMM2 */
+#define FGS_FLAG_FOLD_SUM 0x800
 /* schedule: LDS-tiled kernels with row-block configuration c (0: 256 rows,
  * 1: 128, 2: 64, 3: 32) instead of the rows-per-expert choice */
 #define FGS_FLAG_TILE(c) ((((c) + 1) & 0x7) << 12)

@@ -59,6 +59,9 @@ def test_align_max_padded():
         ((1, 4096, 14336, 8, 2, 0, 0x100 | 0x1000), _capi.FGS_EINVAL, "excludes"),
         ((1, 4096, 14336, 8, 2, 0, 0x5000), _capi.FGS_EINVAL, "TILE"),
         ((1, 4096, 14336, 8, 2, 0, 0x4000), 0, ""),
+        ((1, 4096, 14336, 8, 2, 0, 0x400), 0, ""),
+        ((1, 4096, 14336, 8, 2, 0, 0x800), 0, ""),
+        ((1, 4096, 14336, 8, 2, 0, 0xC00), _capi.FGS_EINVAL, "exclude each other"),
         ((1, 7168, 2048, 256, 8, 1, 0x1000), 0, ""),
         ((1, 7168, 2048, 256, 8, 1, 0x2000), 0, ""),
         ((1, 4000, 14336, 8, 2, 0, 0), _capi.FGS_EUNSUPPORTED, "multiples"),

@@ -168,8 +168,9 @@ def test_quantised_schedules_agree(gpu, mode):
 
 # ------------------------------------------------------ one-token decode ---
 # M = 1 runs the direct-row schedule: no alignment, slot j is row tile j
-# (its expert topk_ids[j]); GEMM2 folds the weighted top-k sum, or with
-# FLAG_SEPARATE_SUM leaves it to moe_sum. Covered: both GEMM2 forms, top-k
+# (its expert topk_ids[j]); GEMM2 folds the weighted top-k sum
+# (FLAG_FOLD_SUM forces it) or leaves it to moe_sum (FLAG_SEPARATE_SUM).
+# Covered: both GEMM2 forms for every mode, top-k
 # of 2, odd (3: idle waves), above the 16 waves (20: slots dealt round
 # robin), 64 and 192 output column tiles, dropped slots and the router
 # weight on the input.
@@ -189,7 +190,8 @@ def test_single_token(gpu, mode, K, N, E, topk, variant, fold):
             ti[0, -1] = E + 2
     on_input = variant == "on_input"
     res = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, apply_router_weight_on_input=on_input,
-                       _flags=0 if fold else _capi.FLAG_SEPARATE_SUM, **wts.kwargs(mode))
+                       _flags=_capi.FLAG_FOLD_SUM if fold else _capi.FLAG_SEPARATE_SUM,
+                       **wts.kwargs(mode))
     ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=mode, w1_scale=wts.w1_scale,
                             w2_scale=wts.w2_scale, apply_router_weight_on_input=on_input,
                             return_mag=True)

@@ -199,8 +199,20 @@ __global__ __launch_bounds__(kChunkThreads) void moe_align_scatter_kernel(
   const int nchunks = gridDim.x;
 
   for (int e = tid; e < E; e += kChunkThreads) {
+    // 16 chunks' counts in flight at a time (integer sums: any order)
     int before = 0, all = 0;
-    for (int cc = 0; cc < nchunks; ++cc) {
+    int cc = 0;
+    for (; cc + 16 <= nchunks; cc += 16) {
+      int v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = counts[static_cast<int64_t>(cc + u) * E + e];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        if (cc + u < c) before += v[u];
+        all += v[u];
+      }
+    }
+    for (; cc < nchunks; ++cc) {
       const int v = counts[static_cast<int64_t>(cc) * E + e];
       if (cc < c) before += v;
       all += v;

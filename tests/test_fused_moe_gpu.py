@@ -206,6 +206,26 @@ def test_single_token_deterministic(gpu):
         assert torch.equal(fm.fused_moe(x, wts.w1, wts.w2, tw, ti), a)
 
 
+# ------------------------------------------------------------ k-split GEMM2 ---
+@pytest.mark.parametrize("mode", ["bf16", "int8"])
+@pytest.mark.parametrize("shape", [(3328, 1024, 2048, 8, 2), (3328, 1024, 4608, 8, 2),
+                                   (832, 1024, 2048, 8, 8)],
+                         ids=["top2", "top2_long_k", "top8"])
+def test_gemm2_k_split(gpu, shape, mode):
+    """Shapes whose GEMM2 grid (about 30 row blocks x 4 column tiles) is
+    split in two over k: fp32 partials of the 4-wave kernel (k row <= 8 KiB)
+    or of the 8-wave one (bf16 at N=4608), reduced with the top-k sum in
+    fixed order."""
+    M, K, N, E, topk = shape
+    wts = testing.make_weights(K, N, E, mode, 0.1, device=gpu, seed=M + K + N)
+    x, tw, ti = testing.make_tokens(M, K, E, topk, device=gpu, seed=M + K + N)
+    res = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, **wts.kwargs(mode))
+    toks = _sample(M, 32)
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=mode, w1_scale=wts.w1_scale,
+                            w2_scale=wts.w2_scale, tokens=toks, return_mag=True)
+    _check(res.cpu()[toks], ref, mode, f"k-split {shape} {mode}")
+
+
 # ------------------------------------------------- activations and biases ---
 _SCHEDS = [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL]
 

@@ -103,11 +103,13 @@ class Layer:
 def time_layer(layer, steps, warmup, flush, profile_timed=False):
     """Times `steps` calls (after `warmup`), returns (ms/call, stage ms).
 
-    With `profile_timed` the library's stage events are recorded during the
+    With `profile_timed` the library's events around GEMM1 through GEMM2
+    (profile mode 2: the boundaries of stages 2..4) are recorded during the
     timed calls themselves (the headline: its roofline comes from the same
-    launches it times; the events cost a few microseconds per call).
-    Otherwise the timed calls run with the profiler off and a second pass of
-    the same calls with it on gives the per-stage split (the sweep).
+    launches it times; the events cost a few microseconds per call), and a
+    second, untimed pass with every stage boundary gives the other stages.
+    Otherwise the timed calls run with the profiler off and that second pass
+    gives the whole per-stage split (the sweep).
     """
     import ctypes
 
@@ -123,7 +125,7 @@ def time_layer(layer, steps, warmup, flush, profile_timed=False):
 
     def run(n, profile):
         total = 0.0
-        lib.fgs_moe_profile_enable(1 if profile else 0)
+        lib.fgs_moe_profile_enable(profile)
         if flush:
             # cold weights each step: a 512 MiB write evicts L2 and MALL;
             # only the layer call itself is inside the events.
@@ -148,11 +150,14 @@ def time_layer(layer, steps, warmup, flush, profile_timed=False):
 
     stage = (ctypes.c_float * 6)()
     lib.fgs_moe_profile_read(stage, 6)  # drop anything recorded before
-    ms = run(steps, profile_timed)
-    if not profile_timed:
-        run(max(3, min(steps, 10)), True)
+    ms = run(steps, 2 if profile_timed else 0)
+    timed = {}
+    if profile_timed and lib.fgs_moe_profile_read(stage, 6) > 0:
+        timed = {k: float(stage[i]) for i, k in enumerate(_capi.PROFILE_STAGES) if 2 <= i <= 4}
+    run(max(3, min(steps, 10)), 1)
     n = lib.fgs_moe_profile_read(stage, 6)
     stages = dict(zip(_capi.PROFILE_STAGES, [float(v) for v in stage])) if n > 0 else {}
+    stages.update(timed)  # GEMM stages: from the timed calls
     return ms, stages
 
 

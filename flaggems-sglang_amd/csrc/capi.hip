@@ -282,7 +282,8 @@ static int validate(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
 // ------------------------------------------------------ stage profiler ---
 // Per-thread record of HIP events around the stages of each fused call.
 struct StageProfiler {
-  bool on = false;
+  int on = 0;  // 0 off, 1 every boundary, 2 the boundaries of stages 2..4
+  std::vector<int> modes;  // the mode of each recorded call
   std::vector<std::array<hipEvent_t, FGS_PROFILE_STAGES + 1>> calls;
   std::vector<std::array<hipEvent_t, FGS_PROFILE_STAGES + 1>> pool;
   std::array<hipEvent_t, FGS_PROFILE_STAGES + 1>* cur = nullptr;
@@ -305,11 +306,12 @@ struct StageProfiler {
         if (hipEventCreate(&e) != hipSuccess) return false;
     }
     calls.push_back(ev);
+    modes.push_back(on);
     cur = &calls.back();
     return true;
   }
   void mark(int i, hipStream_t s) {
-    if (cur) (void)hipEventRecord((*cur)[i], s);
+    if (cur && (on == 1 || (i >= 2 && i <= 5))) (void)hipEventRecord((*cur)[i], s);
   }
 };
 static thread_local StageProfiler g_prof;
@@ -627,7 +629,8 @@ int32_t fgs_moe_validate(int64_t m, int64_t hidden, int64_t inter,
 }
 
 int32_t fgs_moe_profile_enable(int32_t on) {
-  g_prof.on = on != 0;
+  if (on < 0 || on > 2) return fail(FGS_EINVAL, "profile mode must be 0, 1 or 2");
+  g_prof.on = on;
   return FGS_OK;
 }
 
@@ -636,10 +639,15 @@ int32_t fgs_moe_profile_read(float* stage_ms, int32_t n_stages) {
     return fail(FGS_EINVAL, "stage_ms must hold 1..FGS_PROFILE_STAGES floats");
   for (int i = 0; i < n_stages; ++i) stage_ms[i] = 0.f;
   const int n = static_cast<int>(g_prof.calls.size());
-  for (auto& ev : g_prof.calls) {
-    if (hipEventSynchronize(ev[FGS_PROFILE_STAGES]) != hipSuccess)
+  for (int c = 0; c < n; ++c) {
+    auto& ev = g_prof.calls[c];
+    // stages whose two boundaries this call recorded (pooled events keep
+    // older recordings, which must not be mixed in)
+    const bool all = g_prof.modes[c] == 1;
+    const int lo = all ? 0 : 2, hi = all ? FGS_PROFILE_STAGES : 5;
+    if (hipEventSynchronize(ev[hi]) != hipSuccess)
       return fail(FGS_ELAUNCH, "profile: event synchronisation failed");
-    for (int i = 0; i < n_stages; ++i) {
+    for (int i = lo; i < n_stages && i < hi; ++i) {
       float ms = 0.f;
       if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess)
         stage_ms[i] += ms;
@@ -647,6 +655,7 @@ int32_t fgs_moe_profile_read(float* stage_ms, int32_t n_stages) {
     g_prof.pool.push_back(ev);
   }
   g_prof.calls.clear();
+  g_prof.modes.clear();
   g_prof.cur = nullptr;
   if (n > 0)
     for (int i = 0; i < n_stages; ++i) stage_ms[i] /= n;

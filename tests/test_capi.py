@@ -149,6 +149,16 @@ def test_entry_points_reject_bad_arguments_before_launch():
     assert lib.fgs_moe_validate(4, 256, 128, 4, 2, 0, _capi.FLAG_ACT_GELU, need) == 0
 
 
+def test_profile_modes():
+    """Stage profiler modes 0, 1 and 2 are accepted (host only); others fail."""
+    lib = _capi.load()
+    for mode in (1, 2, 0):
+        assert lib.fgs_moe_profile_enable(mode) == 0
+    assert lib.fgs_moe_profile_enable(3) == _capi.FGS_EINVAL
+    assert "profile mode" in _capi.last_error()
+    assert lib.fgs_moe_profile_enable(-1) == _capi.FGS_EINVAL
+
+
 def test_error_codes_map_to_python_exceptions():
     with pytest.raises(ValueError):
         _capi.check(_capi.FGS_EINVAL, "x")

@@ -416,10 +416,10 @@ static int run_fused(const FusedArgs& a) {
   g1.limit = a.limit;
   g1.bias = a.b13;
   g1.a_rows = a.m;
+  g1.num_experts = a.e;
   if (p.direct) {
     // slot j is row tile j; a2 holds the compact slot rows
     g1.direct_ids = a.topk_ids;
-    g1.num_experts = a.e;
   }
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, static_cast<int>(p.n_launch),
                                    a.stream)

@@ -40,7 +40,8 @@ struct GemmParams {
   int32_t eid_shift;      // tiled: row block rb belongs to alignment block rb >> eid_shift
   const int32_t* direct_ids;  // streaming, one token: topk_ids ([numel] slots) in
                               // place of the alignment; null: aligned rows
-  int32_t num_experts;        // with direct_ids: valid ids are [0, num_experts)
+  int32_t num_experts;        // experts of the layer (with direct_ids: the
+                              // valid ids are [0, num_experts))
 };
 
 // Router gating (scores -> top-k -> renormalise), one wave per token;

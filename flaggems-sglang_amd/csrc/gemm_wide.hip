@@ -578,15 +578,20 @@ bool wide_supported(int dt, bool gemm1, const GemmParams& p) {
   return p.a_rows > 0 && p.a_rows * row_bytes <= kMax && p.nrows_w * row_bytes <= kMax;
 }
 
-// FGS_MOE_WIDE_GROUPN overrides the column-group width of the tile walk
-// (default 8; a tuning aid, read once).
-static int wide_group_n_choice() {
+// Column-group width of the tile walk: 4 for a GEMM1 of >= 16 column tiles
+// over mostly full row blocks (>= 512 rows per expert; measured: Mixtral
+// M=4096 GEMM1 -1.1 %, layer -0.7 %, Qwen2 int8 M=8192 -0.3 %), else 8
+// (half-full blocks -- Mixtral M=512, Qwen2 M=1024 -- and Qwen3's 6-tile
+// GEMM1 are slower at 4). FGS_MOE_WIDE_GROUPN overrides it (a tuning aid,
+// read once).
+static int wide_group_n_choice(bool gemm1, int n_ct, double rows_per_expert) {
   static const int g = [] {
     const char* s = getenv("FGS_MOE_WIDE_GROUPN");
-    const int v = s ? atoi(s) : 8;
-    return (v >= 1 && v <= 64) ? v : 8;
+    const int v = s ? atoi(s) : 0;
+    return (v >= 1 && v <= 64) ? v : 0;
   }();
-  return g;
+  if (g > 0) return g;
+  return gemm1 && n_ct >= 16 && rows_per_expert >= 512 ? 4 : 8;
 }
 
 template <int DT, bool GEMM1>
@@ -604,7 +609,10 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
   GemmParams q = p;
   q.row_blocks = row_blocks;
   if (GEMM1 || q.ksplit < 1) q.ksplit = 1;
-  if (q.group_n < 1) q.group_n = wide_group_n_choice();
+  const int n_ct_walk = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
+  const double rows_per_expert =
+      p.num_experts > 0 ? static_cast<double>(p.numel) / p.num_experts : 0.0;
+  if (q.group_n < 1) q.group_n = wide_group_n_choice(GEMM1, n_ct_walk, rows_per_expert);
   // enough positions for the largest XCD walk the kernel can form from the
   // launched row blocks (it splits the live ones, known on the device)
   const int n_ct = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);

@@ -12,12 +12,22 @@ with every input already resident in HBM. Prints ONE JSON line:
   region) against MI355X's peak;
 * ``sweep``: ms/layer, TFLOP/s, GB/s and roofline fractions at every M of
   the configuration (M = 1 .. 4096), each with its own warmup and timing;
+* ``configs``: the same rows for every other measured configuration
+  (DeepSeek-V3 fp8, Qwen3 bf16 uniform and skewed, Qwen2 int8, the small
+  CPU-sized layer) at each of its M;
 * ``cpu_baseline``: the repo's CPU torch reference (oracle/) on a bounded
   sample of the same workload, on this host's cores.
 
+Each row's ``roofline`` names the dominant kernel (the slower GEMM) with its
+achieved rate against the MI355X peak; where a committed rocprofv3 summary
+covers the shape it also carries ``traffic`` (HBM bytes per launch,
+``profiles/traffic_<cfg>.json``) and ``mfma_busy`` (fraction of SIMD cycles
+the MFMA pipe is busy, ``profiles/mfma_<cfg>.json``).
+
 Options: ``--config`` picks another configuration of
 flaggems_sglang.testing.CONFIGS (its largest M is then the headline),
-``--no-sweep`` / ``--no-cpu`` skip those legs (profiling runs).
+``--no-sweep`` / ``--no-configs`` / ``--no-cpu`` skip those legs
+(profiling runs).
 """
 
 import argparse
@@ -36,6 +46,8 @@ METRIC = ("fused-MoE ms/layer, TFLOP/s & HBM GB/s (% roofline) at M=1..4096, "
 PEAK_HBM_GBS = 8000.0
 PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "int8": 5000.0}
 FLUSH_BYTES = 512 << 20  # > MALL (256 MB): flush between steps when small
+SPIN_CYCLES = 400_000    # ~0.2 ms of GPU spin ahead of each flushed call
+OTHER_CONFIGS = ("deepseek_fp8", "qwen3", "qwen3_skewed", "qwen2_int8", "small")
 
 
 def log(*a):
@@ -50,6 +62,8 @@ def parse():
     ap.add_argument("--config", default="mixtral")
     ap.add_argument("--m", type=int, default=None, help="headline M")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the sweep over the other configurations")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep-steps", type=int, default=10)
     ap.add_argument("--flags", type=lambda v: int(v, 0), default=0,
@@ -128,9 +142,14 @@ def time_layer(layer, steps, warmup, flush, profile_timed=False):
         lib.fgs_moe_profile_enable(profile)
         if flush:
             # cold weights each step: a 512 MiB write evicts L2 and MALL;
-            # only the layer call itself is inside the events.
+            # only the layer call itself is inside the events. A short GPU
+            # spin after the flush keeps the device busy while the host
+            # enqueues the call, so host launch time never shows up as an
+            # idle gap between the events.
             for _ in range(n):
                 scratch.fill_(1)
+                if hasattr(torch.cuda, "_sleep"):
+                    torch.cuda._sleep(SPIN_CYCLES)
                 a = torch.cuda.Event(enable_timing=True)
                 b = torch.cuda.Event(enable_timing=True)
                 a.record()
@@ -161,18 +180,29 @@ def time_layer(layer, steps, warmup, flush, profile_timed=False):
     return ms, stages
 
 
+def _profile_entry(kind, cfg_name, M, stage):
+    """A stage's entry in a committed rocprofv3 summary
+    (profiles/<kind>_<cfg>.json, keyed "<cfg>:<M>:<stage>"), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kind}_{cfg_name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("by_stage", {}).get(f"{cfg_name}:{M}:{stage}") or None
+
+
 def measured_traffic(cfg_name, M, stage):
     """HBM bytes per launch of a stage's kernel, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/traffic_<cfg>.json,
     copy-calibrated), or None when that configuration was not profiled."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
-    if not os.path.exists(path):
-        return None
-    with open(path) as f:
-        entry = json.load(f).get("by_stage", {}).get(f"{cfg_name}:{M}:{stage}")
-    if not entry:
-        return None
-    return entry
+    return _profile_entry("traffic", cfg_name, M, stage)
+
+
+def measured_mfma(cfg_name, M, stage):
+    """MFMA-pipe busy fraction of a stage's kernel from the committed
+    rocprofv3 summary (profiles/mfma_<cfg>.json): SQ_VALU_MFMA_BUSY_CYCLES
+    over the SIMD-cycles of the dispatch (GRBM_GUI_ACTIVE per XCD times the
+    1024 SIMDs), or None when not profiled."""
+    return _profile_entry("mfma", cfg_name, M, stage)
 
 
 def dominant(layer, stages):
@@ -196,11 +226,17 @@ def dominant(layer, stages):
     frac_hbm = gbs / PEAK_HBM_GBS
     meas = measured_traffic(cfg.name, M, name)
     traffic = None if meas is None else round(meas["fetch_bytes"] + meas["write_bytes"])
+    mf = measured_mfma(cfg.name, M, name)
     extra = {"algorithmic_bytes": round(wbytes + io),
              "traffic_source": None if meas is None else
              "profiles/traffic_%s.json: rocprofv3 FETCH_SIZE + WRITE_SIZE per "
              "dispatch, scaled by a 1 GiB copy (profiled avg %.4f ms)"
-             % (cfg.name, meas["avg_ns"] / 1e6)}
+             % (cfg.name, meas["avg_ns"] / 1e6),
+             "mfma_busy": None if mf is None else round(mf["mfma_busy"], 4),
+             "valu_per_mfma": None if mf is None else round(mf["valu_per_mfma"], 2),
+             "mfma_source": None if mf is None else
+             "profiles/mfma_%s.json: rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES / "
+             "(GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs) per dispatch" % cfg.name}
     if frac_mfma >= frac_hbm:
         return {"kernel": f"moe_gemm ({name})", "bound": "mfma",
                 "achieved": round(tflops, 2), "peak": PEAK_TFLOPS[cfg.mode],
@@ -266,6 +302,32 @@ def cpu_baseline(layer, budget_s=25.0):
                       f"best of {reps}"}
 
 
+def sweep_config(cfg, dev, args):
+    """Rows (ms/layer, TFLOP/s, GB/s, roofline fractions, dominant kernel)
+    of one configuration at each of its M; its weights are freed after."""
+    import torch
+
+    from flaggems_sglang import testing
+
+    t0 = time.perf_counter()
+    weights = testing.make_weights(cfg.K, cfg.N, cfg.E, cfg.mode, cfg.w_scale,
+                                   device=dev)
+    torch.cuda.synchronize()
+    log(f"{cfg.name}: weights {weights.nbytes() / 1e9:.2f} GB in "
+        f"{time.perf_counter() - t0:.1f}s")
+    rows = []
+    for m in cfg.Ms:
+        lay = Layer(cfg, weights, m, dev, args.flags)
+        sms, sst = time_layer(lay, args.sweep_steps, 3, lay.bytes < FLUSH_BYTES)
+        r = row(lay, sms, sst)
+        r["roofline"] = dominant(lay, sst)
+        rows.append(r)
+        log(f"{cfg.name} M={m}: {json.dumps(r)}")
+    del weights
+    torch.cuda.empty_cache()
+    return rows
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -299,7 +361,7 @@ def main():
                             profile_timed=True)
     log(f"headline {cfg.name} M={M}: {ms:.4f} ms/layer stages={stages}")
 
-    sweep = []
+    sweep, lay = [], None
     if not args.no_sweep:
         for m in cfg.Ms:
             lay = head if m == M else Layer(cfg, weights, m, dev, args.flags)
@@ -341,8 +403,14 @@ def main():
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "configs": {},
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }
+    if not args.no_configs and args.config == "mixtral" and args.m is None:
+        head = weights = lay = None  # the headline weights go before the next set
+        torch.cuda.empty_cache()
+        for name in OTHER_CONFIGS:
+            out["configs"][name] = sweep_config(testing.CONFIGS[name], dev, args)
     print(json.dumps(out), flush=True)
 
 

@@ -266,9 +266,6 @@ static int validate(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
                                       std::to_string(step));
   if ((inter / 16) > 65535 || (hidden / 16) > 65535)
     return fail(FGS_EUNSUPPORTED, "hidden / inter too large");
-  if (dt == kDtInt8 && (hidden > 512 * kInt8QuantMaxVec || inter > 512 * kInt8QuantMaxVec))
-    return fail(FGS_EUNSUPPORTED, "int8 w8a8: hidden and inter must be <= " +
-                                      std::to_string(512 * kInt8QuantMaxVec));
   if (check_ws) {
     Plan p;
     make_plan(m, hidden, inter, e, topk, qmode, flags, &p);
@@ -543,6 +540,47 @@ int32_t fgs_moe_align_block_size(const int32_t* topk_ids, int64_t numel,
                       expert_ids, num_post_pad, max_padded, as_stream(stream), sc);
 }
 
+int64_t fgs_moe_routing_max_tiles(int64_t numel, int32_t num_experts) {
+  if (numel < 0 || num_experts < 1 || num_experts > kRoutingMaxExperts) return -1;
+  return routing_max_tiles(numel, num_experts);
+}
+
+int64_t fgs_moe_routing_workspace_bytes(int64_t numel, int32_t num_experts) {
+  if (numel < 0 || num_experts < 1 || num_experts > kRoutingMaxExperts) return -1;
+  return routing_workspace_bytes(numel, num_experts);
+}
+
+int32_t fgs_moe_topk_to_routing(const float* topk_weights, const int32_t* topk_ids,
+                                int64_t m, int32_t topk, int32_t num_experts,
+                                float* gate_scal, int32_t* topk_indx, int32_t* gate_indx,
+                                int32_t* hist, int32_t* token_offs_raw,
+                                int32_t* token_offs_pad, int32_t* block_pid_map,
+                                int64_t max_tiles, void* workspace, int64_t ws_bytes,
+                                void* stream) {
+  if (m < 0 || topk < 1) return fail(FGS_EINVAL, "m >= 0 and topk >= 1 required");
+  if (num_experts < 1 || num_experts > kRoutingMaxExperts)
+    return fail(FGS_EINVAL, "num_experts must be in [1, " +
+                                std::to_string(kRoutingMaxExperts) + "]");
+  const int64_t numel = m * topk;
+  if (numel >= (int64_t(1) << 31) / 2)
+    return fail(FGS_EUNSUPPORTED, "m * topk too large for int32 indices");
+  if (max_tiles < routing_max_tiles(numel, num_experts))
+    return fail(FGS_EINVAL, "max_tiles must be >= fgs_moe_routing_max_tiles() = " +
+                                std::to_string(routing_max_tiles(numel, num_experts)));
+  if (ws_bytes < routing_workspace_bytes(numel, num_experts))
+    return fail(FGS_EINVAL, "workspace too small: need " +
+                                std::to_string(routing_workspace_bytes(numel, num_experts)) +
+                                " bytes");
+  if ((numel > 0 && (!topk_weights || !topk_ids || !gate_scal || !topk_indx || !gate_indx)) ||
+      !hist || !token_offs_raw || !token_offs_pad || !block_pid_map || !workspace)
+    return fail(FGS_EINVAL, "null pointer argument");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(FGS_EINVAL, "workspace must be 256-byte aligned");
+  return launch_topk_to_routing(topk_weights, topk_ids, m, topk, num_experts, gate_scal,
+                                topk_indx, gate_indx, hist, token_offs_raw, token_offs_pad,
+                                block_pid_map, max_tiles, workspace, as_stream(stream));
+}
+
 int32_t fgs_moe_silu_and_mul(const void* in, void* out, int64_t rows,
                              int64_t n, void* stream) {
   if (rows < 0 || n <= 0) return fail(FGS_EINVAL, "rows >= 0 and n > 0 required");
@@ -601,9 +639,6 @@ int32_t fgs_moe_quant_int8_token(const void* x, int8_t* q, float* scales,
                                  int64_t rows, int64_t cols, void* stream) {
   if (rows < 0 || cols <= 0) return fail(FGS_EINVAL, "rows >= 0 and cols > 0 required");
   if (cols % 8) return fail(FGS_EUNSUPPORTED, "cols must be a multiple of 8");
-  if (cols > 512 * kInt8QuantMaxVec)
-    return fail(FGS_EUNSUPPORTED,
-                "cols must be <= " + std::to_string(512 * kInt8QuantMaxVec));
   if (rows > 0 && (!x || !q || !scales))
     return fail(FGS_EINVAL, "null pointer argument");
   if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(q) % 8)

@@ -422,11 +422,9 @@ int launch_quant_int8_token(const void* x, int8_t* q, float* scales,
                             const int32_t* rows_dev, const int32_t* sorted_ids,
                             int64_t numel) {
   if (rows == 0) return FGS_OK;
-  if (cols > 512 * kInt8QuantMaxVec)
-    return fail(FGS_EUNSUPPORTED, "int8 token quantiser: more than " +
-                                      std::to_string(512 * kInt8QuantMaxVec) + " columns");
   const uint16_t* xs = static_cast<const uint16_t*>(x);
-  if (rows < kInt8WaveRows) {
+  // rows too wide for a wave's registers take the workgroup-per-row kernel
+  if (rows < kInt8WaveRows || cols > 512 * kInt8QuantMaxVec) {
     hipLaunchKernelGGL(quant_int8_token_wg_kernel, dim3(static_cast<unsigned>(rows)),
                        dim3(256), 0, stream, xs, q, scales, cols, rows_dev, sorted_ids,
                        numel);

@@ -62,21 +62,24 @@ __device__ __forceinline__ float gelu_mul(float g, float u) {
 // swiglu is the activation fused into matmul_ogs by the bias variant
 // (:274-314): gate g and linear u stay fp32 (biases already added);
 // with limit > 0, g = min(g, limit) and u = clamp(u, -limit, limit); out =
-// bf16(g * sigmoid(alpha * g) * (u + 1)).
+// bf16(g * sigmoid(alpha * g) * (u + 1)), times the router weight when it
+// goes on the input (matmul_ogs scales its epilogue's output -- the fused
+// activation's result -- by the gammas).
 __device__ __forceinline__ uint16_t gemm1_epilogue(float g, float u, bool scale,
                                                    float gamma, int act = kActSilu,
                                                    float alpha = 1.f, float limit = 0.f) {
-  if (scale) {
-    g *= gamma;
-    u *= gamma;
-  }
   if (act == kActSwiglu) {
     if (limit > 0.f) {
       g = fminf(g, limit);
       u = fminf(fmaxf(u, -limit), limit);
     }
     const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-alpha * g));
-    return f32_to_bf16_bits(g * sg * (u + 1.0f));
+    const float o = g * sg * (u + 1.0f);
+    return f32_to_bf16_bits(scale ? o * gamma : o);
+  }
+  if (scale) {
+    g *= gamma;
+    u *= gamma;
   }
   g = bf16_bits_to_f32(f32_to_bf16_bits(g));
   u = bf16_bits_to_f32(f32_to_bf16_bits(u));

@@ -62,6 +62,18 @@ int launch_align(const int32_t* ids, int64_t numel, int num_experts,
                  int32_t* num_post_pad, int64_t max_padded, hipStream_t stream,
                  int32_t* scratch = nullptr);
 
+// Routing-format conversion (routing.hip): the triton_kernels routing tuple
+// of _standard_topk_to_triton_kernels, block metadata for block_m in
+// {16, 32, 64, 128}. num_experts <= 1022 (two extra id classes).
+constexpr int kRoutingMaxExperts = 1022;
+int64_t routing_max_tiles(int64_t numel, int num_experts);
+int64_t routing_workspace_bytes(int64_t numel, int num_experts);
+int launch_topk_to_routing(const float* weights, const int32_t* ids, int64_t m, int topk,
+                           int num_experts, float* gate_scal, int32_t* topk_indx,
+                           int32_t* gate_indx, int32_t* hist, int32_t* token_offs_raw,
+                           int32_t* token_offs_pad, int32_t* block_pid_map,
+                           int64_t max_tiles, void* workspace, hipStream_t stream);
+
 int launch_silu_and_mul(const void* in, void* out, int64_t rows, int64_t n,
                         hipStream_t stream);
 int launch_moe_sum(const void* in, void* out, int64_t m, int topk, int64_t k,
@@ -78,7 +90,8 @@ int launch_moe_sum_partials(const float* part, int nsplit, void* out, int64_t m,
 // Activation quantisers; with `rows_dev` given only rows < *rows_dev (a
 // device-side count such as num_tokens_post_padded) are processed, and with
 // `sorted_ids` given the pad rows (sorted_ids[r] >= numel) are skipped.
-// The int8 quantiser takes at most 512 * kInt8QuantMaxVec columns.
+// The int8 quantiser holds a row in a wave's registers up to
+// 512 * kInt8QuantMaxVec columns; wider rows take a workgroup each.
 constexpr int kInt8QuantMaxVec = 16;
 int launch_quant_fp8_group(const void* x, void* q, float* scales, int64_t rows,
                            int64_t cols, int group, hipStream_t stream,

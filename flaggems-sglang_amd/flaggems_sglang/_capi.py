@@ -30,6 +30,7 @@ FLAG_FORCE_PREFILL = 0x200
 FLAG_SEPARATE_SUM = 0x400
 FLAG_FOLD_SUM = 0x800
 TILED_CONFIGS = 4  # row blocks 256, 128, 64, 32
+ROUTING_BLOCK_MS = (16, 32, 64, 128)  # tile tables of fgs_moe_topk_to_routing
 
 
 def flag_tile(cfg: int) -> int:
@@ -53,6 +54,14 @@ SIGNATURES = {
          _c_void_p, _i64, _c_void_p],
     ),
     "fgs_moe_align_scratch_bytes": (_i64, [_i64, _i32]),
+    "fgs_moe_routing_max_tiles": (_i64, [_i64, _i32]),
+    "fgs_moe_routing_workspace_bytes": (_i64, [_i64, _i32]),
+    "fgs_moe_topk_to_routing": (
+        _i32,
+        [_c_void_p, _c_void_p, _i64, _i32, _i32, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64,
+         _c_void_p],
+    ),
     "fgs_moe_silu_and_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "fgs_moe_sum": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _i64, _c_void_p]),
     "fgs_moe_topk_gating": (

@@ -42,36 +42,80 @@ def _require_gpu(name: str, t: torch.Tensor) -> None:
         )
 
 
-_DEINTERLEAVE_CACHE: dict = {}
+class _ConversionCache:
+    """Layout conversions of model weights, made once per live weight.
 
+    An entry belongs to the source's root tensor (a view's ``_base``, else
+    the tensor itself), matched by object identity, and within it to the
+    view's geometry (offset, shape, strides, dtype); it is served while the
+    root's version counter is unchanged (an in-place update converts again).
+    ``weakref.finalize`` on the root drops its entries when the root is
+    garbage-collected, so the cache holds exactly one converted copy per live
+    weight -- a model with any number of MoE layers converts each weight
+    once -- and never a copy of a dead one. A conversion that returns a view
+    of its source (a transposed view that is already contiguous in the other
+    order) costs nothing and is not stored: storing it would keep the root
+    alive.
+    """
 
-def _cached(cache: dict, w: torch.Tensor, fn):
-    """``fn(w)`` cached per weight tensor and version (a model's weights are
-    converted once, not on every call). An entry holds a weak reference to
-    its source and only serves that same tensor object: a freed weight's
-    address can be reused by a new tensor of the same shape."""
-    key = (w.data_ptr(), w._version, tuple(w.shape), tuple(w.stride()), w.dtype)
-    hit = cache.get(key)
-    if hit is not None and hit[0]() is w:
-        return hit[1]
-    if len(cache) > 64:
-        cache.clear()
-    out = fn(w)
-    cache[key] = (weakref.ref(w), out)
-    return out
+    def __init__(self, fn):
+        self._fn = fn
+        self._roots: dict = {}  # id(root) -> {geometry: (version, converted)}
+
+    def __call__(self, w: torch.Tensor) -> torch.Tensor:
+        root = w._base if w._base is not None else w
+        geometry = (w.storage_offset(), tuple(w.shape), tuple(w.stride()), w.dtype)
+        views = self._roots.get(id(root))
+        if views is not None:
+            hit = views.get(geometry)
+            if hit is not None and hit[0] == root._version:
+                return hit[1]
+        out = self._fn(w)
+        if out.untyped_storage().data_ptr() == w.untyped_storage().data_ptr():
+            return out  # zero-copy view of the source
+        if views is None:
+            views = self._roots[id(root)] = {}
+            weakref.finalize(root, self._roots.pop, id(root), None)
+        views[geometry] = (root._version, out)
+        return out
+
+    def __len__(self) -> int:
+        return sum(len(v) for v in self._roots.values())
+
+    def clear(self) -> None:
+        for views in self._roots.values():
+            views.clear()
 
 
 # --------------------------------------------------------------- routing ---
 @dataclass
+class ExptData:
+    """Block metadata of a routing (the fields of ``triton_kernels.routing.
+    ExptData`` that ``compute_expt_data_torch`` fills, ops/fused_moe.py:140):
+    ``hist`` int32 ``[E]``; ``token_offs_raw`` int32 ``[E + 1]`` (exclusive
+    sums of ``hist``); per block_m in (16, 32, 64, 128) ``token_offs_pad
+    [block_m]`` int32 ``[E + 1]`` (exclusive sums of ``ceil(hist /
+    block_m)``, in tiles) and ``block_pid_map[block_m]`` int32
+    ``[max_tiles]`` (``(b << 16) | e`` for expert e's b-th tile, -1 past the
+    last tile)."""
+
+    hist: torch.Tensor
+    token_offs_raw: torch.Tensor
+    token_offs_pad: dict
+    block_pid_map: dict
+
+
+@dataclass
 class RoutingData:
     """Duck-typed stand-in for ``triton_kernels.routing.RoutingData`` with the
-    fields the reference reads (ops/fused_moe.py:141-143, 200-201)."""
+    fields the reference builds and reads (ops/fused_moe.py:141-143,
+    200-201)."""
 
     gate_scal: torch.Tensor
     expt_hist: torch.Tensor
     n_expts_tot: int
     n_expts_act: int
-    expt_data: object = None
+    expt_data: Optional[ExptData] = None
 
 
 @dataclass
@@ -88,25 +132,56 @@ class ScatterIndx:
 
 def standard_topk_to_routing(topk_weights, topk_ids, n_expts_tot):
     """``(topk_weights, topk_ids)`` -> ``(RoutingData, GatherIndx,
-    ScatterIndx)`` in the reference's routing format.
+    ScatterIndx)`` in the reference's routing format, computed on the GPU
+    (``fgs_moe_topk_to_routing``: the stable alignment kernel plus two small
+    kernels).
 
-    Follows ``_standard_topk_to_triton_kernels`` (ops/fused_moe.py:119-146):
-    per-token ascending sort of the ids carrying the weights (:130-131), stable
-    argsort of the flattened ids (:134) and its inverse (:135), gathered gate
-    scales (:136) and the per-expert histogram (:137-139). The block metadata
-    of ``compute_expt_data_torch`` (:140) belongs to ``triton_kernels`` and is
-    not produced (``expt_data=None``); nothing in this package reads it.
+    The result is that of ``_standard_topk_to_triton_kernels``
+    (ops/fused_moe.py:119-146): per-token ascending id sort carrying the
+    weights (:130-131), stable argsort of the flattened ids (``topk_indx``,
+    :134) and its inverse (``gate_indx``, :135), the gathered gate scales
+    (:136), the per-expert histogram (:137-139) and the tile tables of
+    ``compute_expt_data_torch`` (:140) in ``routing_data.expt_data``
+    (:class:`ExptData`). Ids below 0 (slots not routed here) sort ahead of
+    expert 0 and ids >= E behind expert E-1, in slot order.
     """
-    expt_indx_2d, sort_indices = torch.sort(topk_ids, dim=1)
-    expt_scal = torch.gather(topk_weights, 1, sort_indices).reshape(-1)
-    expt_indx = expt_indx_2d.reshape(-1).to(torch.int32)
-    topk_indx = torch.argsort(expt_indx, stable=True).to(torch.int32)
-    gate_indx = torch.argsort(topk_indx, stable=True).to(torch.int32)
-    gate_scal = expt_scal[topk_indx.long()]
-    hist = torch.bincount(expt_indx.long(), minlength=n_expts_tot)[
-        :n_expts_tot
-    ].to(torch.int32)
-    routing = RoutingData(gate_scal, hist, n_expts_tot, topk_ids.shape[1])
+    _require_gpu("topk_ids", topk_ids)
+    _require_gpu("topk_weights", topk_weights)
+    assert topk_ids.ndim == 2 and topk_weights.shape == topk_ids.shape, (
+        "topk_ids / topk_weights must be [M, topk]")
+    lib = _capi.load()
+    M, k = topk_ids.shape
+    E = int(n_expts_tot)
+    numel = M * k
+    max_tiles = lib.fgs_moe_routing_max_tiles(numel, E)
+    ws_bytes = lib.fgs_moe_routing_workspace_bytes(numel, E)
+    if max_tiles < 0 or ws_bytes < 0:
+        raise ValueError(f"standard_topk_to_routing: n_expts_tot={E} not in [1, 1022]")
+    dev = topk_ids.device
+    ids = topk_ids.to(torch.int32).contiguous()
+    wts = topk_weights.to(torch.float32).contiguous()
+    i32 = dict(dtype=torch.int32, device=dev)
+    gate_scal = torch.empty(numel, dtype=torch.float32, device=dev)
+    topk_indx = torch.empty(numel, **i32)
+    gate_indx = torch.empty(numel, **i32)
+    hist = torch.empty(E, **i32)
+    offs_raw = torch.empty(E + 1, **i32)
+    offs_pad = torch.empty((len(_capi.ROUTING_BLOCK_MS), E + 1), **i32)
+    pid_map = torch.empty((len(_capi.ROUTING_BLOCK_MS), max(max_tiles, 1)), **i32)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    _capi.check(
+        lib.fgs_moe_topk_to_routing(
+            wts.data_ptr(), ids.data_ptr(), M, k, E, gate_scal.data_ptr(),
+            topk_indx.data_ptr(), gate_indx.data_ptr(), hist.data_ptr(),
+            offs_raw.data_ptr(), offs_pad.data_ptr(), pid_map.data_ptr(),
+            max_tiles, ws.data_ptr(), ws_bytes, _stream_ptr(ids)),
+        "standard_topk_to_routing",
+    )
+    bms = _capi.ROUTING_BLOCK_MS
+    expt = ExptData(hist, offs_raw,
+                    {bm: offs_pad[i] for i, bm in enumerate(bms)},
+                    {bm: pid_map[i, :max_tiles] for i, bm in enumerate(bms)})
+    routing = RoutingData(gate_scal, hist, E, k, expt)
     return (
         routing,
         GatherIndx(src_indx=topk_indx, dst_indx=gate_indx),
@@ -421,15 +496,11 @@ def fused_moe(
     return out
 
 
-_TRANSPOSE_CACHE: dict = {}
-_TRANSPOSE_DEINTERLEAVE_CACHE: dict = {}
-
-
-def _native_layout(w: torch.Tensor) -> torch.Tensor:
-    """``[E, A, B] -> [E, B, A]`` contiguous, cached per weight version so a
-    model's weights are transposed once, not on every call (the reference
-    plugin transposes on every call, ops/fused_moe.py:342-343)."""
-    return _cached(_TRANSPOSE_CACHE, w, lambda t: t.transpose(-1, -2).contiguous())
+# ``[E, A, B] -> [E, B, A]`` contiguous, once per weight (the reference
+# plugin transposes both weights on every call, ops/fused_moe.py:342-343).
+# A weight passed as a transposed view of a native-layout tensor converts
+# for free.
+_native_layout = _ConversionCache(lambda t: t.transpose(-1, -2).contiguous())
 
 
 def triton_kernel_fused_experts(
@@ -505,6 +576,13 @@ def _deinterleave_rows(w: torch.Tensor) -> torch.Tensor:
     return torch.cat([w[:, 0::2, :], w[:, 1::2, :]], dim=1).contiguous()
 
 
+# interleaved gate/linear weights -> the kernels' [gate block | up block]
+# rows, once per weight: native layout, and the reference's [E, K, 2N]
+_deinterleaved = _ConversionCache(_deinterleave_rows)
+_transposed_deinterleaved = _ConversionCache(
+    lambda w: _deinterleave_rows(w.transpose(-1, -2)))
+
+
 def fused_moe_with_bias(
     hidden_states: torch.Tensor,
     w1: torch.Tensor,
@@ -535,8 +613,9 @@ def fused_moe_with_bias(
         y = bf16(a W2^T + b2);  out = bf16(sum_j w_j * y_j)
 
     ``gemm1_alpha`` defaults to 1.0 and no clamp is applied without
-    ``gemm1_clamp_limit``. The router weight multiplies g and u before the
-    activation when ``apply_router_weight_on_input``.
+    ``gemm1_clamp_limit``. With ``apply_router_weight_on_input`` the router
+    weight multiplies ``a`` before its bf16 rounding (matmul_ogs applies its
+    gammas to the fused activation's output) and ``y`` is not weighted.
     """
     logger.debug("FLAGGEMS_SGLANG FUSED_MOE_WITH_BIAS (gfx950)")
     assert hidden_states.ndim == 2, "hidden_states must be 2D"
@@ -558,7 +637,7 @@ def fused_moe_with_bias(
         "topk_ids / topk_weights must be [M, topk]")
     topk = topk_ids.shape[1]
     if interleaved:
-        w1 = _cached(_DEINTERLEAVE_CACHE, w1, _deinterleave_rows)
+        w1 = _deinterleaved(w1)
         b1 = _deinterleave_rows(b1)
     alpha = 1.0 if gemm1_alpha is None else float(gemm1_alpha)
     limit = 0.0 if gemm1_clamp_limit is None else float(gemm1_clamp_limit)
@@ -633,8 +712,7 @@ def triton_kernel_fused_experts_with_bias(
     num_tokens, hidden = hidden_states.shape
     topk_weights, topk_ids = _routing_to_topk(routing_data, gather_indx,
                                               num_tokens)
-    w13n = _cached(_TRANSPOSE_DEINTERLEAVE_CACHE, w1,
-                   lambda w: _deinterleave_rows(w.transpose(-1, -2)))
+    w13n = _transposed_deinterleaved(w1)
     b1n = _deinterleave_rows(b1)
     w2n = _native_layout(w2)
     kw = dict(apply_router_weight_on_input=apply_router_weight_on_input,
@@ -703,7 +781,7 @@ def fused_moe_flagos(obj, layer, dispatch_output):
             "Bias execution requires both w13_bias and w2_bias")
         if activation != "silu":
             raise ValueError(f"Unsupported FusedMoe activation: {activation}")
-        w13 = _cached(_DEINTERLEAVE_CACHE, layer.w13_weight, _deinterleave_rows)
+        w13 = _deinterleaved(layer.w13_weight)
         b13n = _deinterleave_rows(b13)
 
         def call(x, tw, ti):

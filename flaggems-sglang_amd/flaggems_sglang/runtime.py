@@ -1,11 +1,15 @@
-"""Operator registry of the package.
+"""Operator discovery for the package namespace.
 
-Same contract as the reference's ``OpRegistrar``
-(src/flaggems_sglang/runtime/op_registrar.py:42-118): walk the
-``flaggems_sglang.ops`` package, import each public module and merge every
-plain function its ``__all__`` lists (``inspect.isfunction`` filter, :116).
-The reference's vendor and architecture tiers (:79-94) do not exist here:
-the only implementation is the gfx950 one.
+The public contract is the reference's (src/flaggems_sglang/__init__.py:34-55,
+runtime/op_registrar.py:116): each public module of ``flaggems_sglang.ops``
+exposes its operators through ``__all__``, and only plain Python functions
+(``inspect.isfunction``) are taken. The reference layers vendor and
+architecture overrides on top of the generic modules; this package has a
+single implementation (gfx950 HIP kernels), so discovery is one pass.
+
+``discover_operators`` returns a fresh name -> function table; the package
+``__init__`` publishes it and answers ``all_registered_ops`` / ``get_op``
+from it.
 """
 
 from __future__ import annotations
@@ -13,40 +17,36 @@ from __future__ import annotations
 import importlib
 import inspect
 import pkgutil
-from typing import Callable, Dict, List, Optional
+from types import ModuleType
+from typing import Callable, Dict, Iterator
+
+OPS_PACKAGE = "flaggems_sglang.ops"
 
 
-class OpRegistrar:
-    """Collect operators from the ``ops`` package."""
-
-    def __init__(self, generic_pkg: str = "flaggems_sglang.ops"):
-        self._generic_pkg = generic_pkg
-        self._resolved: Dict[str, Callable] = {}
-
-    def apply(self, target_globals: Optional[Dict] = None) -> Dict[str, Callable]:
-        self._resolved.clear()
-        pkg = importlib.import_module(self._generic_pkg)
-        for mod_info in pkgutil.iter_modules(pkg.__path__):
-            if mod_info.ispkg or mod_info.name.startswith("_"):
-                continue
-            mod = importlib.import_module(f"{self._generic_pkg}.{mod_info.name}")
-            for name in getattr(mod, "__all__", ()):
-                fn = getattr(mod, name, None)
-                if fn is not None and inspect.isfunction(fn):
-                    self._resolved[name] = fn
-        if target_globals is not None:
-            target_globals.update(self._resolved)
-        return dict(self._resolved)
-
-    @property
-    def resolved(self) -> Dict[str, Callable]:
-        return dict(self._resolved)
-
-    def names(self) -> List[str]:
-        return sorted(self._resolved)
-
-    def get(self, name: str) -> Optional[Callable]:
-        return self._resolved.get(name)
+def _operator_modules(package: str) -> Iterator[ModuleType]:
+    """Import and yield the package's public leaf modules (sub-packages and
+    names with a leading underscore are private)."""
+    root = importlib.import_module(package)
+    for info in pkgutil.iter_modules(root.__path__):
+        if info.ispkg or info.name[:1] == "_":
+            continue
+        yield importlib.import_module(package + "." + info.name)
 
 
-__all__ = ["OpRegistrar"]
+def discover_operators(package: str = OPS_PACKAGE) -> Dict[str, Callable]:
+    """Map every function named in a public module's ``__all__`` to itself.
+
+    Names that a module lists but does not define, and listed objects that
+    are not plain functions (classes, constants, builtins), are skipped.
+    A later module wins when two export the same name.
+    """
+    table: Dict[str, Callable] = {}
+    for module in _operator_modules(package):
+        for name in getattr(module, "__all__", None) or ():
+            candidate = getattr(module, name, None)
+            if inspect.isfunction(candidate):
+                table[name] = candidate
+    return table
+
+
+__all__ = ["discover_operators", "OPS_PACKAGE"]

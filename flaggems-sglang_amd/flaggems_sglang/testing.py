@@ -61,6 +61,16 @@ TOL = {
     "int8": dict(atol=5e-2, rtol=2e-2, mean_rel=5e-2),
 }
 
+# Regression bounds of the parity tests: about ten times the largest error
+# measured on MI355X over every parity case of the mode (mean_rel, and the
+# elementwise error in bf16 ulps of the summed terms' magnitude). They catch
+# plausible kernel bugs the tolerance contract above lets through.
+REGRESSION = {
+    "bf16": dict(mean_rel=1e-4, ulp_mag=16.0),
+    "fp8": dict(mean_rel=1e-2, ulp_mag=64.0),
+    "int8": dict(mean_rel=1e-2, ulp_mag=64.0),
+}
+
 
 @dataclasses.dataclass
 class MoEWeights:

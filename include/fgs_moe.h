@@ -100,6 +100,35 @@ int32_t fgs_moe_align_block_size(const int32_t* topk_ids, int64_t numel,
  * reference's conversion runs as torch ops, ops/fused_moe.py:130-139). */
 int64_t fgs_moe_align_scratch_bytes(int64_t numel, int32_t num_experts);
 
+/* Routing-format conversion: (topk_weights, topk_ids) -> the routing tuple
+ * of triton_kernels that _standard_topk_to_triton_kernels builds
+ * (ops/fused_moe.py:119-146), computed on the GPU:
+ *   gate_scal  f32 [numel], topk_indx int32 [numel], gate_indx int32 [numel]:
+ *              the reference's per-token ascending id sort (:130-131), the
+ *              stable argsort of the flattened ids (:134), its inverse
+ *              (:135) and the gathered weights (:136);
+ *   hist       int32 [E] (:137-139, ids outside [0, E) not counted);
+ *   token_offs_raw int32 [E + 1], token_offs_pad int32 [4][E + 1] and
+ *   block_pid_map int32 [4][max_tiles]: the tables of triton_kernels'
+ *              compute_expt_data_torch (:140) for block_m = 16, 32, 64, 128
+ *              (row i of the [4][...] arrays): exclusive sums of hist and of
+ *              ceil(hist / block_m) (the latter in tiles), and per tile
+ *              (b << 16) | e for expert e's b-th tile, -1 past the last.
+ * numel = m * topk; num_experts <= 1022; max_tiles >=
+ * fgs_moe_routing_max_tiles(numel, E) (compute_expt_data_torch's bound);
+ * workspace: fgs_moe_routing_workspace_bytes(numel, E) bytes, 256-aligned.
+ * Ids < 0 (slots not routed) sort ahead of expert 0 and ids >= E behind
+ * expert E-1, each group in slot order. Deterministic (no atomics). */
+int64_t fgs_moe_routing_max_tiles(int64_t numel, int32_t num_experts);
+int64_t fgs_moe_routing_workspace_bytes(int64_t numel, int32_t num_experts);
+int32_t fgs_moe_topk_to_routing(const float* topk_weights, const int32_t* topk_ids,
+                                int64_t m, int32_t topk, int32_t num_experts,
+                                float* gate_scal, int32_t* topk_indx, int32_t* gate_indx,
+                                int32_t* hist, int32_t* token_offs_raw,
+                                int32_t* token_offs_pad, int32_t* block_pid_map,
+                                int64_t max_tiles, void* workspace, int64_t ws_bytes,
+                                void* stream);
+
 /* silu_and_mul: out[r, c] = bf16(silu(f32(in[r, c])) * f32(in[r, n + c])).
  * in bf16 [rows, 2n], out bf16 [rows, n].
  * Replaces _silu_and_mul_triton / _silu_and_mul_kernel
@@ -142,7 +171,7 @@ int32_t fgs_moe_quant_fp8_group(const void* x, void* q, float* scales,
 
 /* Dynamic per-row int8 quantisation: scale = max(amax, 1e-10) / 127,
  * q = clamp(rne(x / scale), -127, 127). x bf16 [rows, cols], q int8,
- * scales f32 [rows]; cols a multiple of 8 and at most 8192 (else -2).
+ * scales f32 [rows]; cols a multiple of 8.
  * No reference counterpart (ops/fused_moe.py:173-175 asserts per-channel
  * quant off); needed by the int8 w8a8 path. */
 int32_t fgs_moe_quant_int8_token(const void* x, int8_t* q, float* scales,
@@ -193,6 +222,8 @@ int32_t fgs_moe_fused_bf16(const void* x, const void* w13, const void* w2,
  *   a = bf16(g * sigmoid(alpha*g) * (u + 1)) with g = x W13g^T + b13g,
  *   u = x W13u^T + b13u and, for limit > 0, g = min(g, limit),
  *   u = clamp(u, -limit, limit); y = bf16(a W2^T + b2); out = bf16(sum_j w_j y_j).
+ *   With FGS_FLAG_ROUTER_WEIGHT_ON_INPUT: a = bf16(w_j * swiglu) and
+ *   out = bf16(sum_j y_j) (matmul_ogs scales its fused activation's output).
  * FGS_FLAG_ACT_GELU is rejected (the reference raises for non-silu,
  * :280-283). */
 int32_t fgs_moe_fused_bf16_bias(const void* x, const void* w13, const float* b13,
@@ -222,8 +253,7 @@ int32_t fgs_moe_fused_fp8_block(const void* x, const void* w13,
 /* Fused MoE, int8 w8a8 with per-output-channel weight scales.
  *   w13 int8 [E, 2*inter, hidden], w13_scale f32 [E, 2*inter]
  *   w2  int8 [E, hidden, inter],   w2_scale  f32 [E, hidden]
- * Activations are quantised dynamically per token (row) inside the call;
- * hidden and inter at most 8192 (else -2).
+ * Activations are quantised dynamically per token (row) inside the call.
  * No reference counterpart (per_channel_quant asserted off,
  * ops/fused_moe.py:173-175). */
 int32_t fgs_moe_fused_int8_channel(const void* x, const void* w13,

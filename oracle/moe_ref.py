@@ -25,13 +25,17 @@ It restates, on the CPU in torch fp32 (plus the C alignment in
   quantisers and dequantising MoE here define them: e4m3fn with 128x128
   weight blocks and 1x128 activation groups (scale = max(amax, 1e-10)/448),
   int8 with per-output-channel weight scales and per-token activation scales
-  (scale = max(amax, 1e-10)/127, round half to even).
+  (scale = max(amax, 1e-10)/127, round half to even);
+* the routing-format conversion of ``_standard_topk_to_triton_kernels``
+  (ops/fused_moe.py:126-139) in Python loops, and the tile tables of
+  ``triton_kernels``' ``compute_expt_data_torch`` (:140; published algorithm
+  restated, version unpinned).
 
 How each function is pinned (closed forms, brute force, library routines,
-invariants) is listed in tests/test_oracle.py. ``_standard_topk_to_triton_kernels``'s
-``compute_expt_data_torch`` metadata and ``matmul_ogs``'s exact accumulation
-order live in the un-vendored ``triton_kernels`` package and are not
-restated: parity of the GEMM arithmetic is to tolerance, not bit-exact.
+invariants) is listed in tests/test_oracle.py. ``matmul_ogs``'s exact
+accumulation order lives in the un-vendored ``triton_kernels`` package and
+is not restated: parity of the GEMM arithmetic is to tolerance, not
+bit-exact.
 """
 
 from __future__ import annotations
@@ -120,6 +124,96 @@ def align(topk_ids, num_experts: int, block_size: int):
     if rc != 0:
         raise ValueError("oracle_align: invalid arguments")
     return sorted_ids, expert_ids[: max_padded // block_size], int(npp[0])
+
+
+# -------------------------------------------------------- routing format ---
+ROUTING_BLOCK_MS = (16, 32, 64, 128)
+
+
+def topk_to_routing(topk_weights, topk_ids, n_expts_tot: int):
+    """The reference's ``_standard_topk_to_triton_kernels`` conversion
+    (src/flaggems_sglang/ops/fused_moe.py:126-139) in plain Python loops:
+
+    * :130-131 sort each token's ids ascending, carrying the weights (ties,
+      which top-k routing never produces, keep slot order);
+    * :133 flatten; :134 stable argsort of the flat ids -> ``topk_indx``;
+    * :135 its inverse -> ``gate_indx``; :136 ``gate_scal`` = weights at
+      ``topk_indx``;
+    * :137-139 ``hist``: ids in ``[0, n_expts_tot)`` counted per expert
+      (``histc`` with ``max = n_expts_tot - 1`` ignores the rest).
+
+    Returns numpy arrays ``(gate_scal f32, topk_indx i32, gate_indx i32,
+    hist i32)``.
+    """
+    w = np.asarray(topk_weights, dtype=np.float32)
+    ids = np.asarray(topk_ids, dtype=np.int64)
+    M, k = ids.shape
+    flat_ids, flat_w = [], []
+    for t in range(M):
+        order = sorted(range(k), key=lambda j: (int(ids[t, j]), j))
+        flat_ids += [int(ids[t, j]) for j in order]
+        flat_w += [w[t, j] for j in order]
+    n = M * k
+    topk_indx = sorted(range(n), key=lambda i: (flat_ids[i], i))
+    gate_indx = [0] * n
+    for p, i in enumerate(topk_indx):
+        gate_indx[i] = p
+    gate_scal = [flat_w[i] for i in topk_indx]
+    hist = [0] * n_expts_tot
+    for v in flat_ids:
+        if 0 <= v < n_expts_tot:
+            hist[v] += 1
+    return (np.array(gate_scal, dtype=np.float32).reshape(n),
+            np.array(topk_indx, dtype=np.int32).reshape(n),
+            np.array(gate_indx, dtype=np.int32).reshape(n),
+            np.array(hist, dtype=np.int32))
+
+
+def routing_max_tiles(n_gates: int, n_expts_tot: int) -> int:
+    """Tile-table length of ``compute_expt_data_torch``: ``n_gates`` when it
+    does not exceed the expert count, else ceil((n_gates - E + 1) / 16) +
+    E - 1 (the bound for the smallest block, 16)."""
+    if n_gates <= n_expts_tot:
+        return n_gates
+    return -((-(n_gates - n_expts_tot + 1)) // min(ROUTING_BLOCK_MS)) + n_expts_tot - 1
+
+
+def expt_data(hist, n_expts_tot: int, n_gates: int):
+    """``compute_expt_data_torch(hist, n_expts_tot, n_gates)`` -- the block
+    metadata the reference stores in ``RoutingData.expt_data``
+    (ops/fused_moe.py:140-143). That function lives in OpenAI's
+    ``triton_kernels`` (python/triton_kernels/triton_kernels/routing.py; no
+    version is pinned by the reference and the package is absent here); its
+    published algorithm, restated:
+
+    * ``token_offs_raw``: [0] + cumulative sum of ``hist`` (E + 1 entries);
+    * for each block_m in (16, 32, 64, 128): ``n_tiles = ceil(hist /
+      block_m)``, ``token_offs_pad[block_m]`` = [0] + cumulative sum of
+      ``n_tiles`` (tile units), and ``block_pid_map[block_m]`` of
+      :func:`routing_max_tiles` entries, -1 except tile ``off_e + b`` of
+      expert ``e`` (``b < n_tiles[e]``), which holds ``(b << 16) + e``.
+
+    Returns ``(token_offs_raw, {block_m: token_offs_pad},
+    {block_m: block_pid_map})`` as int64 numpy arrays.
+    """
+    hist = [int(h) for h in hist]
+    raw = [0]
+    for h in hist:
+        raw.append(raw[-1] + h)
+    max_tiles = routing_max_tiles(n_gates, n_expts_tot)
+    pads, maps = {}, {}
+    for bm in ROUTING_BLOCK_MS:
+        n_tiles = [(h + bm - 1) // bm for h in hist]
+        pad = [0]
+        for nt in n_tiles:
+            pad.append(pad[-1] + nt)
+        pid = [-1] * max_tiles
+        for e in range(n_expts_tot):
+            for b in range(n_tiles[e]):
+                pid[pad[e] + b] = (b << 16) + e
+        pads[bm] = np.array(pad, dtype=np.int64)
+        maps[bm] = np.array(pid, dtype=np.int64)
+    return np.array(raw, dtype=np.int64), pads, maps
 
 
 # --------------------------------------------------------- element-wise ---
@@ -306,11 +400,17 @@ def fused_moe(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
         h = xq[rows] @ w13e.t()
         if b1 is not None:
             h = h + b1[e].cpu().float()
-        if apply_router_weight_on_input:
-            h = h * wts[rows, slots][:, None]
+        gam = wts[rows, slots][:, None]
+        if apply_router_weight_on_input and activation != "swiglu":
+            h = h * gam
         if activation == "swiglu":
+            # matmul_ogs applies the input gammas to its fused activation's
+            # output (parity unpinned: triton_kernels is absent)
             n = h.shape[1] // 2
-            a = swiglu(h[:, :n], h[:, n:], alpha, limit).to(torch.bfloat16)
+            a = swiglu(h[:, :n], h[:, n:], alpha, limit)
+            if apply_router_weight_on_input:
+                a = a * gam
+            a = a.to(torch.bfloat16)
         elif activation == "gelu":
             a = gelu_and_mul(h.to(torch.bfloat16))
         else:

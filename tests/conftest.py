@@ -28,3 +28,18 @@ def gpu():
 
     _capi.load()
     return torch.device("cuda:0")
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """With FGS_PARITY_LOG set, write the per-case parity figures the GPU
+    tests measured (max-abs, ulps, mean_rel) to that JSON file."""
+    path = os.environ.get("FGS_PARITY_LOG")
+    if not path:
+        return
+    mod = sys.modules.get("test_fused_moe_gpu")
+    rows = list(getattr(mod, "PARITY", [])) if mod else []
+    import json
+
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "w") as f:
+        json.dump(rows, f, indent=0)

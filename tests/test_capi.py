@@ -67,7 +67,8 @@ def test_align_max_padded():
         ((1, 4000, 14336, 8, 2, 0, 0), _capi.FGS_EUNSUPPORTED, "multiples"),
         ((1, 3584, 2560, 64, 8, 2, 0), 0, ""),
         ((1, 3584 - 128, 2560, 64, 8, 2, 0), _capi.FGS_EUNSUPPORTED, "multiples"),
-        ((1, 9216, 2560, 64, 8, 2, 0), _capi.FGS_EUNSUPPORTED, "<= 8192"),
+        ((1, 9216, 2560, 64, 8, 2, 0), 0, ""),
+        ((1, 4096, 14336, 8, 2, 2, 0), 0, ""),
         ((1, 9216, 2560, 64, 8, 0, 0), 0, ""),
     ],
 )
@@ -123,8 +124,7 @@ def test_entry_points_reject_bad_arguments_before_launch():
     assert lib.fgs_moe_sum(nul, nul, 4, 0, 16, nul) == -1
     assert lib.fgs_moe_quant_fp8_group(nul, nul, nul, 4, 256, 100, nul) == -2
     assert lib.fgs_moe_quant_int8_token(nul, nul, nul, 4, 12, nul) == -2
-    assert lib.fgs_moe_quant_int8_token(nul, nul, nul, 4, 8200, nul) == -2
-    assert "<= 8192" in _capi.last_error()
+    assert lib.fgs_moe_quant_int8_token(nul, nul, nul, 4, 8200, nul) == -1  # null
     need = lib.fgs_moe_workspace_bytes(4, 256, 128, 4, 2, 0, 0)
     rc = lib.fgs_moe_fused_bf16(nul, nul, nul, nul, nul, 4, 256, 128, 4, 2, 0,
                                 nul, need, nul, nul)
@@ -247,51 +247,85 @@ def test_no_cpu_fallback():
         silu_and_mul(x)
 
 
-def test_standard_topk_to_routing_roundtrip_cpu():
-    """The routing-format converter and its inverse are torch index ops and
-    run on any device; the round trip restores (weights, ids) with ids
-    ascending inside each token (ops/fused_moe.py:130)."""
-    from flaggems_sglang.ops.fused_moe import (_routing_to_topk,
-                                               standard_topk_to_routing)
+def test_standard_topk_to_routing_needs_gpu():
+    """The routing conversion runs on the GPU only (no CPU fallback)."""
+    from flaggems_sglang import standard_topk_to_routing
 
-    g = torch.Generator().manual_seed(0)
-    logits = torch.randn(9, 16, generator=g)
-    w, ids = torch.topk(torch.softmax(logits, -1), 4, dim=-1)
-    w = w / w.sum(-1, keepdim=True)
-    rd, gi, si = standard_topk_to_routing(w, ids.int(), 16)
-    assert rd.n_expts_act == 4 and rd.expt_hist.sum() == 36
-    w2, ids2 = _routing_to_topk(rd, gi, 9)
-    order = torch.argsort(ids, dim=1)
-    assert torch.equal(ids2.long(), torch.gather(ids, 1, order))
-    assert torch.equal(w2, torch.gather(w, 1, order))
-    assert torch.equal(gi.dst_indx[gi.src_indx.long()], torch.arange(36, dtype=torch.int32))
+    w = torch.full((3, 2), 0.5)
+    ids = torch.zeros(3, 2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        standard_topk_to_routing(w, ids, 4)
 
 
-def test_weight_cache_serves_only_its_tensor():
-    """The converted-weight cache (deinterleave / transpose of a model's
-    weights) answers only for the tensor object it converted: a freed weight's
-    address and shape can come back on a new tensor."""
-    import weakref
+def test_routing_conversion_validation():
+    lib = _capi.load()
+    assert lib.fgs_moe_routing_max_tiles(36, 4) == 6
+    assert lib.fgs_moe_routing_max_tiles(2, 3) == 2
+    assert lib.fgs_moe_routing_max_tiles(65536, 128) == (65536 - 128 + 1 + 15) // 16 + 127
+    assert lib.fgs_moe_routing_max_tiles(10, 1023) == -1
+    ws = lib.fgs_moe_routing_workspace_bytes(36, 4)
+    assert ws > 0
+    p = 1 << 20  # never dereferenced: validation fails first
+    rc = lib.fgs_moe_topk_to_routing(p, p, 9, 4, 4, p, p, p, p, p, p, p, 5, p, ws, None)
+    assert rc == _capi.FGS_EINVAL and "max_tiles" in _capi.last_error()
+    rc = lib.fgs_moe_topk_to_routing(p, p, 9, 4, 4, p, p, p, p, p, p, p, 6, p, ws - 1, None)
+    assert rc == _capi.FGS_EINVAL and "workspace too small" in _capi.last_error()
+    rc = lib.fgs_moe_topk_to_routing(p, p, 9, 4, 1023, p, p, p, p, p, p, p, 6, p, ws, None)
+    assert rc == _capi.FGS_EINVAL and "num_experts" in _capi.last_error()
+    rc = lib.fgs_moe_topk_to_routing(p, None, 9, 4, 4, p, p, p, p, p, p, p, 6, p, ws, None)
+    assert rc == _capi.FGS_EINVAL and "null pointer" in _capi.last_error()
+
+
+def test_weight_cache_one_conversion_per_live_weight():
+    """A model with many MoE layers (Qwen3-30B-A3B: 48, DeepSeek-V3: 58, two
+    or three converted weights each) converts every weight once, however
+    many there are; an in-place update converts again; a freed weight's copy
+    is released with it and never served to a new tensor."""
+    import gc
 
     from flaggems_sglang.ops import fused_moe as fm
 
-    cache, calls = {}, []
+    calls = []
 
-    def fn(t):
+    def double(t):
         calls.append(1)
         return t * 2
 
-    a = torch.ones(4, 4)
-    assert fm._cached(cache, a, fn) is fm._cached(cache, a, fn)
-    assert len(calls) == 1
-    # an entry under b's key whose source is gone is not served
-    b = torch.full((4, 4), 3.0)
-    key = (b.data_ptr(), b._version, tuple(b.shape), tuple(b.stride()), b.dtype)
-    gone = torch.zeros(1)
-    cache[key] = (weakref.ref(gone), torch.zeros(4, 4))
-    del gone
-    assert torch.equal(fm._cached(cache, b, fn), b * 2)
+    cache = fm._ConversionCache(double)
+    ws = [torch.full((4, 4), float(i)) for i in range(150)]
+    first = [cache(w) for w in ws]
+    for _ in range(3):
+        for w, f in zip(ws, first):
+            assert cache(w) is f
+    del w  # the loop variable holds the last weight
+    assert len(calls) == 150 and len(cache) == 150
+    # views of one weight are separate conversions of the same root
+    assert torch.equal(cache(ws[1].t()), ws[1].t() * 2)
+    assert len(calls) == 151 and len(cache) == 151
     # an in-place update is a new version
-    a.add_(1)
-    assert torch.equal(fm._cached(cache, a, fn), torch.full((4, 4), 4.0))
-    assert len(calls) == 3
+    ws[0].add_(1)
+    assert torch.equal(cache(ws[0]), torch.full((4, 4), 2.0))
+    assert len(calls) == 152
+    # dropping weights drops their copies
+    del ws[10:]
+    gc.collect()
+    assert len(cache) == 11
+    fresh = [torch.full((4, 4), 7.0) for _ in range(20)]
+    for t in fresh:
+        assert torch.equal(cache(t), torch.full((4, 4), 14.0))
+    assert len(cache) == 31
+
+
+def test_weight_cache_zero_copy_views_not_stored():
+    """A reference-layout weight that is a transposed view of a native-layout
+    tensor converts to that tensor's storage without a copy, and is not held
+    (holding it would keep the source alive)."""
+    from flaggems_sglang.ops import fused_moe as fm
+
+    native = torch.randn(2, 8, 4)
+    ref_layout = native.transpose(-1, -2)
+    out = fm._native_layout(ref_layout)
+    assert out.data_ptr() == native.data_ptr() and torch.equal(out, native)
+    before = len(fm._native_layout)
+    fm._native_layout(ref_layout)
+    assert len(fm._native_layout) == before

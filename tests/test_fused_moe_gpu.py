@@ -28,16 +28,44 @@ from oracle import moe_ref
 pytestmark = pytest.mark.gpu
 
 
+# (case, mode, max_abs, max ulps of |ref|, max ulps of the term magnitude,
+# mean_rel) of every check; conftest writes them out when FGS_PARITY_LOG
+# names a file
+PARITY = []
+
+
+def _ulp_bf16(v):
+    """bf16 unit in the last place of |v| (8 significant bits)."""
+    v = v.abs().clamp(min=2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(v)) - 7)
+
+
 def _check(res, ref, mode, what=""):
-    """``ref`` is the oracle's output or its (output, term magnitude) pair."""
+    """``ref`` is the oracle's output or its (output, term magnitude) pair.
+
+    Two bars: the tolerance contract (elementwise ``atol + rtol * s`` and
+    ``mean_rel``, ``testing.TOL``) and the regression bound
+    (``testing.REGRESSION``: about ten times the error this build measures,
+    so that a plausible kernel bug -- one wrong activation scale among 56
+    k blocks -- fails)."""
     tol = testing.TOL[mode]
+    reg = testing.REGRESSION[mode]
     mag = None
     if isinstance(ref, tuple):
         ref, mag = ref
     ok, max_abs, mean_rel = moe_ref.compare(res, ref, tol["atol"], tol["rtol"], mag)
-    print(f"{what} max_abs={max_abs:.4g} mean_rel={mean_rel:.4g}")
+    diff = (res.float().cpu() - ref.float().cpu()).abs()
+    ulp_ref = float((diff / _ulp_bf16(ref.float().cpu())).max()) if diff.numel() else 0.0
+    scale = ref.float().cpu().abs() if mag is None else mag.float().cpu()
+    ulp_mag = float((diff / _ulp_bf16(scale)).max()) if diff.numel() else 0.0
+    PARITY.append(dict(case=what, mode=mode, max_abs=max_abs, max_ulp_ref=ulp_ref,
+                       max_ulp_mag=ulp_mag, mean_rel=mean_rel))
+    print(f"{what} max_abs={max_abs:.4g} ulp(ref)={ulp_ref:.3g} "
+          f"ulp(mag)={ulp_mag:.3g} mean_rel={mean_rel:.4g}")
     assert ok, f"{what}: elementwise tolerance failed (max_abs={max_abs})"
     assert mean_rel <= tol["mean_rel"], f"{what}: mean_rel={mean_rel}"
+    assert mean_rel <= reg["mean_rel"], f"{what}: mean_rel={mean_rel} (regression bound)"
+    assert ulp_mag <= reg["ulp_mag"], f"{what}: {ulp_mag:.3g} ulps of the term magnitude"
 
 
 def _sample(M, n=24):
@@ -418,13 +446,11 @@ def _weights(cfg, device):
     return _WEIGHTS[key]
 
 
-CONFIG_CASES = [
-    ("small", 64), ("mixtral", 1), ("mixtral", 32), ("mixtral", 512),
-    ("mixtral", 4096), ("qwen3", 1), ("qwen3", 256), ("qwen3", 2048),
-    ("qwen3_skewed", 16), ("qwen3_skewed", 2048), ("qwen3_skewed", 8192),
-    ("qwen2_int8", 1), ("qwen2_int8", 64), ("qwen2_int8", 1024), ("qwen2_int8", 8192),
-    ("deepseek_fp8", 1), ("deepseek_fp8", 32), ("deepseek_fp8", 512),
-    ("deepseek_fp8", 4096),
+# every M the benchmark reports, for every configuration
+CONFIG_CASES = [("small", 64)] + [
+    (name, m) for name in ("mixtral", "qwen3", "qwen3_skewed", "qwen2_int8",
+                           "deepseek_fp8")
+    for m in testing.CONFIGS[name].Ms
 ]
 
 
@@ -446,3 +472,49 @@ def test_fused_moe_configs(gpu, name, M):
 def test_release_config_weights():
     _WEIGHTS.clear()
     torch.cuda.empty_cache()
+
+
+# -------------------------------------------------------- uncombined rows ---
+@pytest.mark.parametrize("M,K,N,E,topk", [(9, 256, 128, 8, 2), (33, 256, 512, 16, 4)])
+def test_uncombined_rows_per_slot(gpu, M, K, N, E, topk):
+    """``scatter_indx=None`` (the adapter's ``no_combine``) returns one row per
+    (token, slot), token-major, a token's slots in ascending expert id (the
+    routing tuple's order): row (t, r) is the r-th smallest expert's gated
+    output, bf16(w * y). Compared row by row with the oracle run on that one
+    slot, so any permutation of the rows fails. matmul_ogs without a scatter
+    index would leave rows in expert-sorted order, but the reference then
+    views them as [num_tokens, hidden] (ops/fused_moe.py:232), which cannot
+    hold M * topk rows: the reference's own order is not observable (parity
+    unpinned)."""
+    x, w1, w2, w, ids = _ref_inputs(M, K, N, E, topk, gpu)
+    w1_ref = w1.transpose(1, 2).contiguous()
+    w2_ref = w2.transpose(1, 2).contiguous()
+    rd, gi, _ = flaggems_sglang.standard_topk_to_routing(w, ids, E)
+    rows = flaggems_sglang.triton_kernel_fused_experts(x, w1_ref, w2_ref, rd, gi, None)
+    assert rows.shape == (M * topk, K)
+    order = torch.argsort(ids.long(), dim=1)
+    sid = torch.gather(ids.long(), 1, order).cpu()
+    sw = torch.gather(w, 1, order).cpu()
+    xr = x.repeat_interleave(topk, dim=0)
+    ref = moe_ref.fused_moe(xr, w1, w2, sw.reshape(-1, 1), sid.reshape(-1, 1).int(),
+                            return_mag=True)
+    _check(rows.cpu(), ref, "bf16", f"uncombined rows {(M, K, N, E, topk)}")
+    # a swap of two slots' rows is caught
+    swapped = rows.view(M, topk, K).flip(1).reshape(M * topk, K).cpu()
+    ok, _, _ = moe_ref.compare(swapped, ref[0], 2e-2, 1e-2, ref[1])
+    assert not ok
+
+
+@pytest.mark.parametrize("sched", [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL, 0],
+                         ids=["decode", "prefill", "auto"])
+def test_int8_wider_than_8192(gpu, sched):
+    """int8 w8a8 with an intermediate wider than a wave's quantiser rows
+    (N = 9216 > 8192: the GEMM2 input quantiser takes a workgroup per row)."""
+    M, K, N, E, topk = 96, 512, 9216, 4, 2
+    wts = testing.make_weights(K, N, E, "int8", 0.05, device=gpu, seed=11)
+    x, tw, ti = testing.make_tokens(M, K, E, topk, device=gpu, seed=11)
+    res = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, _flags=sched, **wts.kwargs("int8"))
+    toks = _sample(M, 16)
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode="int8", w1_scale=wts.w1_scale,
+                            w2_scale=wts.w2_scale, tokens=toks, return_mag=True)
+    _check(res.cpu()[toks], ref, "int8", f"int8 N=9216 sched {sched}")

@@ -200,3 +200,42 @@ def test_topk_gating_feeds_fused_moe(gpu):
     a = fm.fused_moe(x, w1, w2, tw, ti)
     b = fm.fused_moe(x, w1, w2, rw.to(gpu), ri.to(gpu))
     assert (a.float() - b.float()).abs().max() <= 2e-2 * b.float().abs().max()
+
+
+# ------------------------------------------------------- routing format ---
+@pytest.mark.parametrize("M,k,E,drop", [
+    (1, 2, 8, False), (7, 2, 8, False), (33, 4, 16, True), (64, 8, 256, False),
+    (700, 8, 128, True), (1024, 8, 64, False),
+    # >= 4096 slots: the multi-workgroup alignment path
+    (600, 8, 128, False), (4096, 2, 8, True), (2048, 8, 256, False),
+    (0, 2, 8, False), (5, 3, 1022, False),
+])
+def test_standard_topk_to_routing_bit_exact(gpu, M, k, E, drop):
+    """The GPU routing conversion equals the oracle's loop restatement of
+    ops/fused_moe.py:126-139 (gate_scal, topk_indx, gate_indx, hist) and of
+    compute_expt_data_torch (tile tables) bit for bit, and the compat path's
+    inverse rebuilds the per-token routing."""
+    w, ids = _routing(M, E, k, M * 7 + k + E, "cpu")
+    ids = ids.clone()
+    if drop and M:
+        ids[::3, -1] = -1
+    rd, gi, si = fm.standard_topk_to_routing(w.to(gpu), ids.to(gpu), E)
+    gate_scal, topk_indx, gate_indx, hist = moe_ref.topk_to_routing(w, ids, E)
+    assert np.array_equal(rd.gate_scal.cpu().numpy(), gate_scal)
+    assert np.array_equal(gi.src_indx.cpu().numpy(), topk_indx)
+    assert np.array_equal(gi.dst_indx.cpu().numpy(), gate_indx)
+    assert np.array_equal(si.src_indx.cpu().numpy(), gate_indx)
+    assert np.array_equal(rd.expt_hist.cpu().numpy(), hist)
+    assert rd.n_expts_tot == E and rd.n_expts_act == k
+    raw, pad, pid = moe_ref.expt_data(hist, E, M * k)
+    ed = rd.expt_data
+    assert np.array_equal(ed.hist.cpu().numpy(), hist)
+    assert np.array_equal(ed.token_offs_raw.cpu().numpy(), raw)
+    for bm in moe_ref.ROUTING_BLOCK_MS:
+        assert np.array_equal(ed.token_offs_pad[bm].cpu().numpy(), pad[bm])
+        assert np.array_equal(ed.block_pid_map[bm].cpu().numpy(), pid[bm])
+    if M and not drop:
+        tw, ti = fm._routing_to_topk(rd, gi, M)
+        order = torch.argsort(ids.long(), dim=1)
+        assert torch.equal(ti.cpu().long(), torch.gather(ids.long(), 1, order))
+        assert torch.equal(tw.cpu(), torch.gather(w, 1, order))

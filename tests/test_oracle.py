@@ -84,6 +84,65 @@ def test_align_matches_reference_stable_order(M, k, E, B):
     assert (eids[npp // B:] == -1).all()
 
 
+@pytest.mark.parametrize("M,k,E,drop", [(1, 2, 8, False), (9, 4, 16, False),
+                                          (33, 4, 16, True), (100, 8, 128, True),
+                                          (64, 8, 256, False)])
+def test_topk_to_routing_matches_reference_steps(M, k, E, drop):
+    """The loop restatement equals the reference's conversion re-run with
+    torch library ops (sort, stable argsort, gather, histc), including slots
+    marked -1 (not routed), which the reference's stable argsort puts first."""
+    g = torch.Generator().manual_seed(M * 31 + k + E)
+    w, ids = moe_ref.route(torch.randn(M, E, generator=g), k)
+    ids = ids.long()
+    if drop:
+        ids[::3, 0] = -1
+    gate_scal, topk_indx, gate_indx, hist = moe_ref.topk_to_routing(w, ids, E)
+    r_indx, r_scal, r_hist = _reference_routing_steps(w, ids, E)
+    assert np.array_equal(topk_indx, r_indx.numpy())
+    assert np.array_equal(gate_scal, r_scal.numpy())
+    assert np.array_equal(hist, r_hist.numpy())
+    assert np.array_equal(gate_indx, torch.argsort(r_indx, stable=True).numpy())
+
+
+def test_expt_data_known_answer():
+    """Hand-worked tables: hist [3, 0, 17, 16] over 36 gates."""
+    raw, pad, pid = moe_ref.expt_data([3, 0, 17, 16], 4, 36)
+    assert raw.tolist() == [0, 3, 3, 20, 36]
+    # max tiles: ceil((36 - 4 + 1) / 16) + 4 - 1 = 6
+    assert pad[16].tolist() == [0, 1, 1, 3, 4]
+    assert pid[16].tolist() == [0, 2, (1 << 16) + 2, 3, -1, -1]
+    assert pad[32].tolist() == [0, 1, 1, 2, 3]
+    assert pid[32].tolist() == [0, 2, 3, -1, -1, -1]
+    assert pad[128].tolist() == [0, 1, 1, 2, 3]
+    # fewer gates than experts: the table is n_gates long
+    raw, pad, pid = moe_ref.expt_data([1, 0, 1], 3, 2)
+    assert pid[16].tolist() == [0, 2]
+
+
+@pytest.mark.parametrize("M,k,E", [(7, 2, 8), (257, 8, 128), (1024, 8, 64),
+                                   (3, 8, 256)])
+def test_expt_data_agrees_with_alignment(M, k, E):
+    """The tile tables describe the alignment kernel's blocks: for each block
+    size B, token_offs_pad * B are the padded segment offsets of
+    moe_align_block_size(B), the tile -> expert map is its expert_ids, and the
+    table bound holds every tile."""
+    g = torch.Generator().manual_seed(M + k + E)
+    w, ids = moe_ref.route(torch.randn(M, E, generator=g), k)
+    hist = np.bincount(ids.numpy().reshape(-1), minlength=E)
+    raw, pad, pid = moe_ref.expt_data(hist, E, M * k)
+    assert np.array_equal(raw, np.concatenate([[0], np.cumsum(hist)]))
+    for B in moe_ref.ROUTING_BLOCK_MS:
+        s, eids, npp = moe_ref.align(ids.numpy(), E, B)
+        assert pad[B][-1] * B == npp
+        tiles = pad[B][-1]
+        assert tiles <= len(pid[B]) == moe_ref.routing_max_tiles(M * k, E)
+        assert np.array_equal(pid[B][:tiles] & 0xFFFF, eids[:tiles])
+        for t in range(tiles):
+            e, b = pid[B][t] & 0xFFFF, pid[B][t] >> 16
+            assert pad[B][e] + b == t and b * B < hist[e]
+        assert (pid[B][tiles:] == -1).all()
+
+
 # ---------------------------------------------------------------- gating ---
 def test_topk_gating_known_answers():
     logits = torch.tensor([[1.0, 3.0, 3.0, 0.0], [0.5, -1.0, 2.0, 2.0]])
@@ -222,7 +281,7 @@ def test_weight_quantisers():
 
 # ------------------------------------------------------------- fused MoE ---
 def _brute_force_moe(x, w1, w2, tw, tid, act="silu", b1=None, b2=None,
-                     alpha=1.0, limit=0.0):
+                     alpha=1.0, limit=0.0, on_input=False, gamma_first=False):
     """Token-by-token float64 MoE (no intermediate rounding); activations
     written from their textbook definitions with math.erf / exp."""
     x = x.double().numpy()
@@ -236,6 +295,9 @@ def _brute_force_moe(x, w1, w2, tw, tid, act="silu", b1=None, b2=None,
             h = w1[e] @ x[t]
             if b1 is not None:
                 h = h + b1[e].double().numpy()
+            gam = float(tw[t, j])
+            if on_input and (act != "swiglu" or gamma_first):
+                h = h * gam
             gte, up = h[:N], h[N:]
             if act == "gelu":
                 a = np.array([0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))) for v in gte]) * up
@@ -244,12 +306,14 @@ def _brute_force_moe(x, w1, w2, tw, tid, act="silu", b1=None, b2=None,
                     gte = np.minimum(gte, limit)
                     up = np.clip(up, -limit, limit)
                 a = gte / (1.0 + np.exp(-alpha * gte)) * (up + 1.0)
+                if on_input and not gamma_first:
+                    a = a * gam
             else:
                 a = gte / (1.0 + np.exp(-gte)) * up
             y = w2[e] @ a
             if b2 is not None:
                 y = y + b2[e].double().numpy()
-            out[t] += float(tw[t, j]) * y
+            out[t] += (1.0 if on_input else gam) * y
     return out
 
 
@@ -286,6 +350,28 @@ def test_moe_activations_and_biases_match_float64_brute_force(act):
                             **kw).double().numpy()
     want = _brute_force_moe(x, w1, w2, w, ids, act=act, b1=b1, b2=b2, **kw)
     assert np.allclose(got, want, rtol=3e-2, atol=3e-2 * np.abs(want).max())
+
+
+def test_swiglu_router_weight_on_input_after_activation():
+    """With the router weight on the input, the bias variant scales the fused
+    swiglu's output (matmul_ogs's gammas act on its epilogue's result); the
+    brute force with the weight applied to g and u first fails the same
+    tolerance, so the test pins the placement."""
+    M, K, N, E, k = 7, 64, 32, 4, 2
+    x, w1, w2, w, ids = _inputs(M, K, N, E, k, seed=23)
+    g = torch.Generator().manual_seed(24)
+    b1 = torch.randn(E, 2 * N, generator=g) * 0.5
+    b2 = torch.randn(E, K, generator=g) * 0.5
+    kw = dict(alpha=1.702, limit=1.5)
+    got = moe_ref.fused_moe(x, w1, w2, w, ids, activation="swiglu", b1=b1, b2=b2,
+                            apply_router_weight_on_input=True, **kw).double().numpy()
+    want = _brute_force_moe(x, w1, w2, w, ids, act="swiglu", b1=b1, b2=b2,
+                            on_input=True, **kw)
+    other = _brute_force_moe(x, w1, w2, w, ids, act="swiglu", b1=b1, b2=b2,
+                             on_input=True, gamma_first=True, **kw)
+    tol = 3e-2 * np.abs(want).max()
+    assert np.allclose(got, want, rtol=3e-2, atol=tol)
+    assert not np.allclose(got, other, rtol=3e-2, atol=tol)
 
 
 def test_gelu_and_mul_closed_form():

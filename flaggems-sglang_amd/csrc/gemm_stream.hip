@@ -387,7 +387,6 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
   const int kblocks = static_cast<int>(p.kdim / 128);
 
   int j0, jstride, s0, s1;
-  bool lead;  // the slot's first wave: adds its bias once
   if (slots <= KW) {
     const int wps = KW / slots;  // waves per slot
     j0 = wave / wps;             // >= slots: an idle wave (KW % slots != 0)
@@ -395,15 +394,15 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
     const int sub = wave % wps;
     s0 = sub * steps / wps;      // empty for some waves when steps < wps
     s1 = (sub + 1) * steps / wps;
-    lead = sub == 0;
   } else {
     j0 = wave;
     jstride = KW;
     s0 = 0;
     s1 = steps;
-    lead = true;
   }
 
+  // slots <= KW: this wave's partial of slot j0's y (un-weighted);
+  // slots > KW: the weighted sum of this wave's complete slots
   f32x4 tot = {0.f, 0.f, 0.f, 0.f};
   for (int j = j0; j < slots; j += jstride) {
     const int e = p.direct_ids[j];
@@ -443,25 +442,44 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
         }
       }
     }
-    float f = gamma;
+    float f = 1.f;
     if constexpr (DT == kDtInt8)
-      f *= p.a_scale[j] * p.w_scale[static_cast<int64_t>(e) * p.nrows_w + col];
+      f = p.a_scale[j] * p.w_scale[static_cast<int64_t>(e) * p.nrows_w + col];
+    const float b = p.bias ? p.bias[static_cast<int64_t>(e) * p.nrows_w + col] : 0.f;
+    if (slots <= KW) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) tot[i] += static_cast<float>(acc[i]) * f;
-    if (p.bias && lead) {
-      const float b = gamma * p.bias[static_cast<int64_t>(e) * p.nrows_w + col];
+      for (int i = 0; i < 4; ++i) tot[i] = static_cast<float>(acc[i]) * f;
+    } else {
+      // the slot's whole y in this wave: round it to bf16 (the slot row the
+      // unfused GEMM2 writes), then weight it
 #pragma unroll
-      for (int i = 0; i < 4; ++i) tot[i] += b;
+      for (int i = 0; i < 4; ++i)
+        tot[i] += gamma * bf16_bits_to_f32(f32_to_bf16_bits(static_cast<float>(acc[i]) * f + b));
     }
   }
 
-  __shared__ f32x4 red[KW > 1 ? KW - 1 : 1][64];
-  if (KW > 1) {
-    if (wave > 0) red[wave - 1][lane] = tot;
-    __syncthreads();
-    if (wave != 0) return;
+  __shared__ f32x4 red[KW][64];
+  red[wave][lane] = tot;
+  __syncthreads();
+  if (wave != 0) return;
+  if (slots <= KW) {
+    // per slot: its waves' partials in order, the bias, one bf16 rounding,
+    // then the weighted sum over the slots in slot order
+    const int wps = KW / slots;
+    tot = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < slots; ++j) {
+      const int e = p.direct_ids[j];
+      if (e < 0 || e >= p.num_experts) continue;
+      const float gamma = p.weight_on_input ? 1.f : p.topk_w[j];
+      const float b = p.bias ? p.bias[static_cast<int64_t>(e) * p.nrows_w + col] : 0.f;
+      f32x4 y = red[j * wps][lane];
+      for (int w = 1; w < wps; ++w) y += red[j * wps + w][lane];
 #pragma unroll
-    for (int w = 0; w < KW - 1; ++w) tot += red[w][lane];
+      for (int i = 0; i < 4; ++i) tot[i] += gamma * bf16_bits_to_f32(f32_to_bf16_bits(y[i] + b));
+    }
+  } else {
+#pragma unroll
+    for (int w = 1; w < KW; ++w) tot += red[w][lane];
   }
   // row 0 of the tile: lane group 0, register 0
   if (lg == 0) static_cast<uint16_t*>(p.out)[col] = f32_to_bf16_bits(tot[0]);

@@ -529,8 +529,13 @@ def triton_kernel_fused_experts(
     and routing in the reference's format (``routing_data.gate_scal``,
     ``.expt_hist``, ``.n_expts_act``; ``gather_indx.src_indx``).
 
-    ``scatter_indx=None`` returns the un-combined ``[M * topk, K]`` rows in
-    the reference's gate order (the ``no_combine`` case of :371).
+    ``scatter_indx=None`` (the adapter's ``no_combine``, :371) returns the
+    un-combined ``[M * topk, K]`` rows token-major, a token's slots in
+    ascending expert id (the routing tuple's order): row ``(t, r)`` is
+    ``bf16(w * y)`` of token t's r-th slot. The reference's own row order
+    for this case is not observable -- it ends in ``.view(num_tokens,
+    hidden_size)`` (:232), which cannot hold ``M * topk`` rows -- so the
+    order is parity-unpinned.
     """
     logger.debug("FLAGGEMS_SGLANG FUSED_MOE (gfx950)")
     assert use_fp8_w8a8 is False, _UNSUPPORTED_FEATURE_MSG.format(

@@ -354,8 +354,12 @@ def fused_moe(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
     w2 [E, K, N]). Returns bf16 [len(tokens), K] (all tokens by default);
     with ``return_mag`` also the fp32 magnitude sum_j |w_j| * (|y_j| + q_j)
     of the terms each output sums (the scale its rounding errors live on).
-    q_j is 0 for bf16; for fp8 / int8 it is 2^-2 * (|a_q| @ |W2|^T), a
-    quarter of the absolute dot product behind y_j. The GEMM2 input is
+    q_j is 2^-8 * (|a| @ |W2|^T) for bf16: fp32 sums in another order round
+    an element of the bf16 intermediate a to its neighbour now and then, and
+    one such flip moves y_j by up to 2^-8 |a_i W2_ki| whatever the size of
+    y_j (outputs that cancel towards 0 included). For fp8 / int8 it is
+    2^-2 * (|a_q| @ |W2|^T), a quarter of the absolute dot product behind
+    y_j. The GEMM2 input is
     re-quantised from a bf16 intermediate; where the kernel's bf16 value
     differs from this oracle's by an ulp the two round to neighbouring grid
     points, and each such flip moves y_j by one quantisation step (up to
@@ -421,8 +425,9 @@ def fused_moe(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
             ye = ye + b2[e].cpu().float()
         ye = ye.to(torch.bfloat16).float()
         y[rows, slots] = ye
-        if return_mag and mode != "bf16":
-            q[rows, slots] = (aq.abs() @ w2e.abs().t()) * 2.0 ** -2
+        if return_mag:
+            q[rows, slots] = (aq.abs() @ w2e.abs().t()) * (2.0 ** -8 if mode == "bf16"
+                                                           else 2.0 ** -2)
     terms = y if apply_router_weight_on_input else y * wts[:, :, None]
     out = terms.sum(dim=1).to(torch.bfloat16)
     if return_mag:

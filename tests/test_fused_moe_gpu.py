@@ -34,12 +34,6 @@ pytestmark = pytest.mark.gpu
 PARITY = []
 
 
-def _ulp_bf16(v):
-    """bf16 unit in the last place of |v| (8 significant bits)."""
-    v = v.abs().clamp(min=2.0 ** -126)
-    return torch.exp2(torch.floor(torch.log2(v)) - 7)
-
-
 def _check(res, ref, mode, what=""):
     """``ref`` is the oracle's output or its (output, term magnitude) pair.
 
@@ -54,12 +48,9 @@ def _check(res, ref, mode, what=""):
     if isinstance(ref, tuple):
         ref, mag = ref
     ok, max_abs, mean_rel = moe_ref.compare(res, ref, tol["atol"], tol["rtol"], mag)
-    diff = (res.float().cpu() - ref.float().cpu()).abs()
-    ulp_ref = float((diff / _ulp_bf16(ref.float().cpu())).max()) if diff.numel() else 0.0
-    scale = ref.float().cpu().abs() if mag is None else mag.float().cpu()
-    ulp_mag = float((diff / _ulp_bf16(scale)).max()) if diff.numel() else 0.0
-    PARITY.append(dict(case=what, mode=mode, max_abs=max_abs, max_ulp_ref=ulp_ref,
-                       max_ulp_mag=ulp_mag, mean_rel=mean_rel))
+    st = testing.regression_stats(res, ref, mag)
+    ulp_ref, ulp_mag = st["max_ulp_ref"], st["max_ulp_mag"]
+    PARITY.append(dict(case=what, mode=mode, **st))
     print(f"{what} max_abs={max_abs:.4g} ulp(ref)={ulp_ref:.3g} "
           f"ulp(mag)={ulp_mag:.3g} mean_rel={mean_rel:.4g}")
     assert ok, f"{what}: elementwise tolerance failed (max_abs={max_abs})"
@@ -85,6 +76,19 @@ def _ref_inputs(M, K, N, E, topk, device, scale=0.1):
     logits = torch.randn(M, E, generator=g, device=device, dtype=torch.float32)
     w, ids = moe_ref.route(logits.cpu(), topk)
     return x, w1, w2, w.to(device), ids.to(device)
+
+
+def _per_slot_ref(x, w1, w2, w, ids, ascending=False, **kw):
+    """The oracle's rows of an uncombined call: row (t, r) is token t's r-th
+    slot alone (top-1 with its weight), bf16(w * y) -- slots in the given
+    order, or in ascending expert id (the routing tuple's order)."""
+    ids, w = ids.long().cpu(), w.cpu()
+    if ascending:
+        order = torch.argsort(ids, dim=1)
+        ids, w = torch.gather(ids, 1, order), torch.gather(w, 1, order)
+    xr = x.repeat_interleave(ids.shape[1], dim=0)
+    return moe_ref.fused_moe(xr, w1, w2, w.reshape(-1, 1), ids.reshape(-1, 1).int(),
+                             return_mag=True, **kw)
 
 
 @pytest.mark.parametrize("shape", testing.REF_SHAPES_SMALL + testing.REF_SHAPES_LARGE,
@@ -362,7 +366,8 @@ def test_bias_reference_signature(gpu):
         x, w1_ref, None, _interleave_rows(b1), w2_ref, None, b2, routing, gather,
         None, gemm1_alpha=1.702, gemm1_clamp_limit=7.0)
     assert rows.shape == (M * topk, K)
-    _check(rows.view(M, topk, K).float().sum(1).to(torch.bfloat16).cpu(), ref,
+    _check(rows.cpu(), _per_slot_ref(x, w1, w2, w, ids, ascending=True, activation="swiglu",
+                                     b1=b1, b2=b2, alpha=1.702, limit=7.0),
            "bf16", "bias compat uncombined")
     with pytest.raises(ValueError, match="Unsupported FusedMoe activation"):
         flaggems_sglang.triton_kernel_fused_experts_with_bias(
@@ -402,7 +407,7 @@ def test_fused_moe_flagos_adapter(gpu, variant):
         ref, mag = moe_ref.fused_moe(x, w1, w2, w, ids, return_mag=True)
     if variant == "no_combine":
         assert res.shape == (M, topk, K)
-        _check(res.float().sum(1).to(torch.bfloat16).cpu(), (ref, mag), "bf16",
+        _check(res.reshape(M * topk, K).cpu(), _per_slot_ref(x, w1, w2, w, ids), "bf16",
                "flagos no_combine")
     else:
         _check(res.cpu(), ((ref.float() * 2.0).to(torch.bfloat16), mag * 2.0), "bf16",
@@ -492,12 +497,7 @@ def test_uncombined_rows_per_slot(gpu, M, K, N, E, topk):
     rd, gi, _ = flaggems_sglang.standard_topk_to_routing(w, ids, E)
     rows = flaggems_sglang.triton_kernel_fused_experts(x, w1_ref, w2_ref, rd, gi, None)
     assert rows.shape == (M * topk, K)
-    order = torch.argsort(ids.long(), dim=1)
-    sid = torch.gather(ids.long(), 1, order).cpu()
-    sw = torch.gather(w, 1, order).cpu()
-    xr = x.repeat_interleave(topk, dim=0)
-    ref = moe_ref.fused_moe(xr, w1, w2, sw.reshape(-1, 1), sid.reshape(-1, 1).int(),
-                            return_mag=True)
+    ref = _per_slot_ref(x, w1, w2, w, ids, ascending=True)
     _check(rows.cpu(), ref, "bf16", f"uncombined rows {(M, K, N, E, topk)}")
     # a swap of two slots' rows is caught
     swapped = rows.view(M, topk, K).flip(1).reshape(M * topk, K).cpu()

@@ -518,3 +518,48 @@ def test_compare_helper():
     assert ok and abs(mx - 0.01) < 1e-6 and abs(mr - 0.005) < 1e-6
     ok, _, _ = moe_ref.compare(a + 0.5, a, atol=2e-2, rtol=1e-2)
     assert not ok
+
+
+@pytest.mark.parametrize("plant", ["scale_2pct", "neighbour_scale"])
+def test_regression_bound_rejects_one_wrong_scale(monkeypatch, plant):
+    """DeepSeek-shaped contraction (K = 7168: 56 k blocks of 128): the fp8
+    regression bound (testing.REGRESSION) rejects an output computed with one
+    wrong activation scale -- block 17's scale 2 % off, which the tolerance
+    contract (testing.TOL) lets through, or replaced by block 18's -- and
+    still accepts GEMM1 results perturbed at the fp8 MFMA's accumulation
+    precision (W13 scales times 1 + 2^-14). The planted error lives in the
+    oracle."""
+    M, K, N, E, k = 16, 7168, 256, 4, 2
+    x, w1, w2, w, ids = _inputs(M, K, N, E, k, seed=31, scale=0.02)
+    q1 = [moe_ref.quant_weight_fp8_block(w1[e]) for e in range(E)]
+    q2 = [moe_ref.quant_weight_fp8_block(w2[e]) for e in range(E)]
+    W1, S1 = torch.stack([a for a, _ in q1]), torch.stack([b for _, b in q1])
+    W2, S2 = torch.stack([a for a, _ in q2]), torch.stack([b for _, b in q2])
+    kw = dict(mode="fp8", w2_scale=S2)
+    ref, mag = moe_ref.fused_moe(x, W1, W2, w, ids, return_mag=True, w1_scale=S1, **kw)
+    tol, reg = testing.TOL["fp8"], testing.REGRESSION["fp8"]
+
+    noisy = moe_ref.fused_moe(x, W1, W2, w, ids, w1_scale=S1 * (1 + 2.0 ** -14), **kw)
+    assert not torch.equal(noisy, ref)
+    st = testing.regression_stats(noisy, ref, mag)
+    assert st["mean_rel"] <= reg["mean_rel"] and st["max_ulp_mag"] <= reg["ulp_mag"], st
+
+    good = moe_ref.quant_fp8_group
+
+    def wrong_scale(a, group=128):
+        q, sc = good(a, group)
+        if a.shape[-1] == K:  # the GEMM1 input: x
+            sc = sc.clone()
+            if plant == "scale_2pct":
+                sc[:, 17] *= 1.02
+            else:
+                sc[:, 17] = sc[:, 18]
+        return q, sc
+
+    monkeypatch.setattr(moe_ref, "quant_fp8_group", wrong_scale)
+    bad = moe_ref.fused_moe(x, W1, W2, w, ids, w1_scale=S1, **kw)
+    ok, _, mean_rel = moe_ref.compare(bad, ref, tol["atol"], tol["rtol"], mag)
+    if plant == "scale_2pct":
+        assert ok and mean_rel <= tol["mean_rel"]  # the contract alone passes it
+    st = testing.regression_stats(bad, ref, mag)
+    assert st["mean_rel"] > reg["mean_rel"] and st["max_ulp_mag"] > reg["ulp_mag"], st

@@ -334,6 +334,9 @@ struct FusedArgs {
   const float* b2 = nullptr;
   bool swiglu = false;
   float alpha = 1.f, limit = 0.f;
+  // stage events off for this call (the allocation-free entry point: event
+  // creation is a runtime allocation)
+  bool no_profile = false;
 };
 
 static int run_fused(const FusedArgs& a) {
@@ -362,7 +365,8 @@ static int run_fused(const FusedArgs& a) {
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + p.o_y);
   const int64_t numel = a.m * a.topk;
 
-  g_prof.begin();
+  if (a.no_profile) g_prof.cur = nullptr;
+  else g_prof.begin();
   g_prof.mark(0, a.stream);
   if (!p.direct) {
     rc = launch_align(a.topk_ids, numel, a.e, p.block_m, sorted, eids, npp,
@@ -490,6 +494,40 @@ static int run_fused(const FusedArgs& a) {
                                a.stream);
   g_prof.mark(6, a.stream);
   return rc;
+}
+
+// ------------------------------------------ allocation-free entry point ---
+// The workspace of fgs_moe_fused_bf16_noalloc: a file-scope device array,
+// one per GPU, held from library load until the process ends. Host code
+// never uses the array's name as an address (in host code it is only a
+// stand-in for the device symbol): each device's address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+static __device__ __align__(256) uint8_t scratch[FGS_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+
+// Address of this device's `scratch` (nullptr with the error set on failure).
+static void* device_scratch() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(FGS_ELAUNCH, std::string("no-alloc scratch: hipGetDevice: ") + hipGetErrorString(e));
+    return nullptr;
+  }
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(FGS_ELAUNCH, std::string("no-alloc scratch: hipGetSymbolAddress: ") +
+                            hipGetErrorString(e));
+      return nullptr;
+    }
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
 }
 
 }  // namespace fgs
@@ -707,6 +745,32 @@ int32_t fgs_moe_fused_bf16(const void* x, const void* w13, const void* w2,
               nullptr,        topk_weights, topk_ids, m,      hidden,
               inter,          num_experts,  topk,     flags,  workspace,
               ws_bytes,       out,          as_stream(stream)};
+  return run_fused(a);
+}
+
+int32_t fgs_moe_fused_bf16_noalloc(const void* x, const void* w13, const void* w2,
+                                   const float* topk_weights, const int32_t* topk_ids,
+                                   int64_t m, int64_t hidden, int64_t inter,
+                                   int32_t num_experts, int32_t topk, int32_t flags,
+                                   void* out, void* stream) {
+  int rc = validate(m, hidden, inter, num_experts, topk, FGS_QMODE_BF16, flags, 0, false);
+  if (rc) return rc;
+  Plan p;
+  make_plan(m, hidden, inter, num_experts, topk, FGS_QMODE_BF16, flags, &p);
+  if (p.total > FGS_NOALLOC_SCRATCH_BYTES)
+    return fail(FGS_EUNSUPPORTED,
+                "fgs_moe_fused_bf16_noalloc: this problem needs " + std::to_string(p.total) +
+                    " bytes of workspace, more than the " +
+                    std::to_string(static_cast<int64_t>(FGS_NOALLOC_SCRATCH_BYTES)) +
+                    "-byte device scratch (use fgs_moe_fused_bf16 with a workspace)");
+  if (m == 0) return FGS_OK;
+  void* ws = device_scratch();
+  if (!ws) return FGS_ELAUNCH;
+  FusedArgs a{FGS_QMODE_BF16, x,      w13,    w2,          nullptr,
+              nullptr,        topk_weights, topk_ids, m,      hidden,
+              inter,          num_experts,  topk,     flags,  ws,
+              FGS_NOALLOC_SCRATCH_BYTES, out, as_stream(stream)};
+  a.no_profile = true;
   return run_fused(a);
 }
 

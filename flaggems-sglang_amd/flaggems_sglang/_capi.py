@@ -31,6 +31,7 @@ FLAG_SEPARATE_SUM = 0x400
 FLAG_FOLD_SUM = 0x800
 TILED_CONFIGS = 4  # row blocks 256, 128, 64, 32
 ROUTING_BLOCK_MS = (16, 32, 64, 128)  # tile tables of fgs_moe_topk_to_routing
+NOALLOC_SCRATCH_BYTES = 64 << 20  # FGS_NOALLOC_SCRATCH_BYTES
 
 
 def flag_tile(cfg: int) -> int:
@@ -80,6 +81,11 @@ SIGNATURES = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
          _i64, _i32, _i32, _i32, _c_void_p, _i64, _c_void_p, _c_void_p],
+    ),
+    "fgs_moe_fused_bf16_noalloc": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
+         _i64, _i32, _i32, _i32, _c_void_p, _c_void_p],
     ),
     "fgs_moe_fused_bf16_bias": (
         _i32,

@@ -211,6 +211,27 @@ int32_t fgs_moe_fused_bf16(const void* x, const void* w13, const void* w2,
                            void* workspace, int64_t ws_bytes, void* out,
                            void* stream);
 
+/* Allocation-free variant of fgs_moe_fused_bf16. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. Same arguments, kernels and results as fgs_moe_fused_bf16,
+ * without the workspace: the library's own device scratch array of
+ * FGS_NOALLOC_SCRATCH_BYTES per GPU (held from library load until the
+ * process ends) stands in for it, and the call makes no hipMalloc / hipFree
+ * or other allocating runtime call (stage profiling is off for it).
+ * Problems whose workspace (fgs_moe_workspace_bytes) exceeds the scratch
+ * return FGS_EUNSUPPORTED with a message naming the size, before any
+ * launch. Every call on a GPU shares that GPU's scratch, which keeps the
+ * last call's contents (no part of it needs to start at zero): calls that
+ * overlap on one GPU -- on different streams, or from different threads
+ * without ordering -- race. */
+#define FGS_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int32_t fgs_moe_fused_bf16_noalloc(const void* x, const void* w13, const void* w2,
+                                   const float* topk_weights, const int32_t* topk_ids,
+                                   int64_t m, int64_t hidden, int64_t inter,
+                                   int32_t num_experts, int32_t topk, int32_t flags,
+                                   void* out, void* stream);
+
 /* Fused MoE with biases and the swiglu activation, bf16. Replaces
  * triton_kernel_fused_experts_with_bias (ops/fused_moe.py:235-325):
  * GEMM1 with bias b1 and swiglu fused (matmul_ogs(..., bias=b1,

@@ -56,13 +56,15 @@ struct Plan {
   int tile_cfg2;   // GEMM2's configuration (rows per block <= block_m)
   int eid_shift2;  // log2(block_m / GEMM2 block rows)
   int ksplit2;     // GEMM2 k splits (tiled only; > 1 -> fp32 partials)
+  bool tail2;      // GEMM2 on the 4-wave kernel with its last round's tiles
+                   // split over k (partials in the workspace, fixed up)
   bool direct;     // one token, streaming: slots index the GEMM rows directly
                    // (no alignment; distinct experts per token)
   bool direct_sum; // ... and GEMM2 folds the top-k sum (no moe_sum)
   int kwd;         // waves of the folded GEMM2
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
-  int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, total;
+  int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail, total;
 };
 
 // k splits for the tiled GEMM2: its grid (row blocks x hidden/256 column
@@ -115,6 +117,17 @@ static int forced_ksplit() {
     return (x >= 1 && x <= 4) ? x : 0;
   }();
   return k;
+}
+
+// FGS_MOE_TAIL (0 off, 1 default) switches the tail split of the 4-wave
+// GEMM2 (a tuning aid; read once).
+static int tail_choice() {
+  static const int t = [] {
+    const char* v = getenv("FGS_MOE_TAIL");
+    const int x = v ? atoi(v) : 1;
+    return (x == 0 || x == 1) ? x : 1;
+  }();
+  return t;
 }
 
 static int pick_kw(int64_t kdim, int step, int cap) {
@@ -174,6 +187,17 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
     // a forced split still keeps >= 8 LDS stages of k per split
     if (forced_ksplit() > 0 && inter * esz / 128 >= 8 * forced_ksplit())
       p.ksplit2 = forced_ksplit();
+    // GEMM2 of 256-row blocks (bf16 / int8) over 1 to 8 rounds of the CUs:
+    // the 4-wave kernel, whole tiles except the last round's, which are
+    // split over k (instead of splitting every tile: fp32 partials of a few
+    // tiles, not of all). Measured: the 4-wave kernel runs a 256 x 256 x 64
+    // stage in ~1.78 us against the 8-wave kernel's ~2.1 us on the dense
+    // Mixtral GEMM2, but left alone its tiles fill 2.25 rounds.
+    const int64_t rows_est = numel / 256 + std::min<int64_t>(e, numel);
+    const int64_t tiles_est = rows_est * (hidden / 256);
+    p.tail2 = tail_choice() && p.tile_cfg2 == 0 && p.dt != kDtFp8 && forced_ksplit() == 0 &&
+              tiles_est >= kNumCUs && tiles_est <= 8 * kNumCUs;
+    if (p.tail2) p.ksplit2 = 1;
   }
   const int step = stream_step_k(p.dt);
   p.kw1 = pick_kw(hidden, step, 4);
@@ -224,6 +248,7 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
                                   : p.max_padded * 4);
   }
   p.o_y = take(p.ksplit2 > 1 ? p.ksplit2 * numel * hidden * 4 : numel * hidden * 2);
+  p.o_tail = p.tail2 ? take(wide_tail_part_bytes()) : -1;
   p.total = o;
   *pl = p;
   return FGS_OK;
@@ -465,6 +490,8 @@ static int run_fused(const FusedArgs& a) {
   g2.n_out = a.hidden;
   g2.nrows_w = a.hidden;
   g2.ksplit = p.ksplit2;
+  g2.tail_split = p.tail2 ? 1 : 0;
+  g2.tail_part = p.tail2 ? reinterpret_cast<float*>(ws + p.o_tail) : nullptr;
   g2.a_rows = p.max_padded;
   g2.eid_shift = p.tiled ? p.eid_shift2 : 0;
   if (p.direct_sum) {

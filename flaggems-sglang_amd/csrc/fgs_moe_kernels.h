@@ -42,6 +42,10 @@ struct GemmParams {
                               // place of the alignment; null: aligned rows
   int32_t num_experts;        // experts of the layer (with direct_ids: the
                               // valid ids are [0, num_experts))
+  int32_t tail_split;         // 4-wave GEMM2: split the last round's tiles over
+                              // k into pieces (partials in tail_part, fixed up
+                              // into out); needs ksplit 1
+  float* tail_part;           // wide_tail_part_bytes() of fp32 partials
 };
 
 // Router gating (scores -> top-k -> renormalise), one wave per token;
@@ -124,6 +128,9 @@ int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
 // 4-wave kernel of the 256-row configuration (bf16, int8): whether it
 // covers a launch, and the launch.
 bool wide_supported(int dt, bool gemm1, const GemmParams& p);
+// fp32 partial bytes the 4-wave GEMM2's tail split needs (fixed: 32 tiles
+// per XCD of 256 x 256).
+int64_t wide_tail_part_bytes();
 int launch_gemm_wide(int dt, bool gemm1, const GemmParams& p, int row_blocks,
                      hipStream_t stream);
 

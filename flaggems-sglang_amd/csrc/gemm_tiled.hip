@@ -835,7 +835,9 @@ int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
   // the 4-wave one at M=4096). FGS_MOE_WIDE=2 forces it for every GEMM2.
   const int64_t k_row = p.kdim * (dt == kDtBf16 ? 2 : 1);
   const bool wide_gemm =
-      gemm1 ? wide_choice() >= 1 : (wide_choice() >= 2 || (wide_choice() == 1 && k_row <= 8192));
+      gemm1 ? wide_choice() >= 1
+            : (wide_choice() >= 2 ||
+               (wide_choice() == 1 && (k_row <= 8192 || (p.tail_split && p.tail_part))));
   if (cfg == 0 && wide_gemm && wide_supported(dt, gemm1, p))
     return launch_gemm_wide(dt, gemm1, p, row_blocks, stream);
   switch (dt) {

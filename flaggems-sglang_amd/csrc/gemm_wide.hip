@@ -79,6 +79,75 @@ __device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint3
 // gfx9 buffer resource word 3 for raw 32-bit loads.
 constexpr int kBufWord3 = 0x00020000;
 
+// The d-th tile (0-based) of an XCD's range [lo, hi) of the row-block-major
+// tile numbering (tile = rball * n_ct + ct), walked over groups of gn
+// columns, then row blocks, then the columns of the group: the first and
+// last row blocks of a range may hold only some columns, every other row
+// block all columns of each group.
+__device__ __forceinline__ bool wide_walk(int lo, int hi, int n_ct, int gn, int d, int* rball,
+                                          int* ct) {
+  if (d < 0 || lo >= hi) return false;
+  const int rb_lo = lo / n_ct, rb_hi = (hi - 1) / n_ct;
+  const int c_first = lo - rb_lo * n_ct;  // first column of rb_lo in the range
+  const int c_last = hi - 1 - rb_hi * n_ct;  // last column of rb_hi in the range
+  for (int g0 = 0; g0 < n_ct; g0 += gn) {
+    const int g1 = min(n_ct, g0 + gn);
+    if (rb_lo == rb_hi) {
+      const int a = max(g0, c_first), n = max(0, min(g1, c_last + 1) - a);
+      if (d < n) {
+        *rball = rb_lo;
+        *ct = a + d;
+        return true;
+      }
+      d -= n;
+      continue;
+    }
+    const int a = max(g0, c_first), n0 = max(0, g1 - a);
+    if (d < n0) {
+      *rball = rb_lo;
+      *ct = a + d;
+      return true;
+    }
+    d -= n0;
+    const int gs = g1 - g0, ni = (rb_hi - rb_lo - 1) * gs;
+    if (d < ni) {
+      *rball = rb_lo + 1 + d / gs;
+      *ct = g0 + d % gs;
+      return true;
+    }
+    d -= ni;
+    const int n1 = max(0, min(g1, c_last + 1) - g0);
+    if (d < n1) {
+      *rball = rb_hi;
+      *ct = g0 + d;
+      return true;
+    }
+    d -= n1;
+  }
+  return false;
+}
+
+// Tail split of an XCD's walk (GEMM2, p.tail_split): its T tiles run as R =
+// T / 32 full rounds on the XCD's 32 CUs; the rem = T % 32 tiles of the last
+// round are each split over k into S = min(4, 32 / rem) pieces, so the last
+// round holds rem * S pieces instead of rem whole tiles. Piece i of tail
+// tile t writes fp32 partial sums to tail_part slot (xcd * 32 + t * S + i);
+// moe_wide_tail_fixup_kernel adds a tile's pieces in order. S = 1 (no
+// split) when rem is 0 or above 16; a piece keeps >= 2 stages of k (the
+// ring depth), so S <= KT_all / 2.
+struct WideTail {
+  int T, R, rem, S;
+};
+__device__ __forceinline__ WideTail wide_tail(int lo, int hi, bool on, int kt_all) {
+  WideTail w;
+  w.T = hi - lo;
+  w.R = w.T / 32;
+  w.rem = w.T - 32 * w.R;
+  w.S = on && w.rem > 0 ? max(1, min(min(4, 32 / w.rem), kt_all / 2)) : 1;
+  return w;
+}
+constexpr int kWideTailSlots = 8 * 32;  // tail_part slots: 32 per XCD
+
 template <int DT, bool GEMM1, class C>
 __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const GemmParams p) {
   using T = TiledType<DT>;
@@ -119,31 +188,40 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   const int xcd = blockIdx.x % 8;
   const int lo = static_cast<int>(static_cast<int64_t>(total) * xcd / 8);
   const int hi = static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8);
-  const int rb_lo = lo / n_ct;
-  const int n_rb = hi > lo ? (hi - 1) / n_ct - rb_lo + 1 : 0;
-  const int gn = p.group_n;
-  const int n_pos = (n_ct + gn - 1) / gn * n_rb * gn;
+  const WideTail tail = wide_tail(lo, hi, !GEMM1 && p.tail_split, KT_all);
 
   struct Tile {
-    int pos;  // >= n_pos: none
     int rb, ct, e, kt0, KT, ks;
+    int slot;  // tail piece: its tail_part slot; whole tile: -1
   };
+  // Workgroup position pos of the XCD: a whole tile of the walk, or (tail
+  // split) a k piece of one of the last round's tiles.
   auto live_tile = [&](int pos, Tile& t) -> bool {
-    const int span = n_rb * gn;
-    const int group = pos / span;
-    const int idx = pos - group * span;
-    const int gsize = min(gn, n_ct - group * gn);
-    if (idx >= n_rb * gsize) return false;
-    const int rball = rb_lo + idx / gsize;
-    t.ct = group * gn + idx % gsize;
-    const int tile = rball * n_ct + t.ct;
-    if (tile < lo || tile >= hi) return false;
+    int d = pos, piece = -1;
+    if (tail.S > 1 && pos >= 32 * tail.R) {
+      const int q = pos - 32 * tail.R;
+      if (q >= tail.rem * tail.S) return false;
+      d = 32 * tail.R + q / tail.S;
+      piece = q % tail.S;
+    }
+    if (d >= tail.T) return false;
+    int rball, ct;
+    if (!wide_walk(lo, hi, n_ct, p.group_n, d, &rball, &ct)) return false;
+    t.ct = ct;
     t.ks = rball / rb_live;
     t.rb = rball - t.ks * rb_live;
     t.e = __builtin_amdgcn_readfirstlane(p.expert_ids[t.rb]);
     if (t.e < 0) return false;
-    t.kt0 = t.ks * KT_all / p.ksplit;
-    t.KT = (t.ks + 1) * KT_all / p.ksplit - t.kt0;
+    if (piece >= 0) {
+      t.kt0 = piece * KT_all / tail.S;
+      t.KT = (piece + 1) * KT_all / tail.S - t.kt0;
+      t.slot = xcd * 32 + (d - 32 * tail.R) * tail.S + piece;
+      t.ks = piece;  // the bias goes into piece 0's partial
+    } else {
+      t.kt0 = t.ks * KT_all / p.ksplit;
+      t.KT = (t.ks + 1) * KT_all / p.ksplit - t.kt0;
+      t.slot = -1;
+    }
     return true;
   };
 
@@ -236,8 +314,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   }
 
   Tile cur;
-  cur.pos = static_cast<int>(blockIdx.x / 8);
-  if (cur.pos >= n_pos || !live_tile(cur.pos, cur)) return;
+  if (!live_tile(static_cast<int>(blockIdx.x / 8), cur)) return;
   Src src;
   make_src(cur, src);
   const int row0 = cur.rb * BM;
@@ -486,8 +563,9 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
           const int sid = p.sorted_ids[row0 + rr];
           const float sa = INT8 ? p.a_scale[row0 + (sid < p.numel ? rr : 0)] : 1.f;
           const int r = lane & 31;
-          if (p.ksplit > 1) {
-            // fp32 partials: 512-byte staged rows (32 chunks), 2 rows per pass
+          if (p.ksplit > 1 || cur.slot >= 0) {
+            // fp32 partials (k splits, tail pieces): 512-byte staged rows
+            // (32 chunks), 2 rows per pass
             constexpr int CH = WCOLS * 4 / 16;
 #pragma unroll
             for (int j = 0; j < CB; ++j) {
@@ -513,9 +591,14 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
               const int c = lane % CH;
               const int row_sid = __shfl(sid, sr, 64);
               const f32x4 val = *reinterpret_cast<const f32x4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
-              if (row_sid < p.numel)
-                *reinterpret_cast<f32x4*>(outf + (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out +
-                                          col_base + c * 4) = val;
+              if (row_sid >= p.numel) continue;
+              float* dst;
+              if (cur.slot >= 0)  // tail piece: [slot][tile row][tile column]
+                dst = p.tail_part + (static_cast<int64_t>(cur.slot) * BM + i * 64 + wm * 32 + sr) * BNR +
+                      wn * WCOLS + c * 4;
+              else
+                dst = outf + (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out + col_base + c * 4;
+              *reinterpret_cast<f32x4*>(dst) = val;
             }
             stage_sync();
           } else {
@@ -556,6 +639,67 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     }
   };
   dispatch_count<RB>(nlive, tile_body);
+}
+
+// Tail fixup of a tail-split GEMM2: 32 tile rows of one tail tile:
+// y[slot, tile columns] = bf16(sum of the tile's pieces in piece order).
+// Grid: 8 XCDs x 32 tail tiles x 8 blocks of 32 tile rows; 4 waves, a wave
+// per row at a time (64 lanes x 4 fp32 = one 256-column partial row, so
+// every piece read is one contiguous KiB).
+template <int BM, int BNR, int SK, int ESZ>
+__global__ __launch_bounds__(256) void moe_wide_tail_fixup_kernel(const GemmParams p) {
+  static_assert(BNR == 64 * 4, "a wave covers a partial row");
+  const int xcd = blockIdx.x % 8;
+  const int t = (blockIdx.x / 8) % 32;
+  const int rblk = blockIdx.x / (8 * 32);
+  const int npp = p.num_post_pad[0];
+  const int n_ct = static_cast<int>(p.n_out / BNR);
+  const int total = npp / BM * n_ct;  // ksplit is 1 with a tail split
+  const int lo = static_cast<int>(static_cast<int64_t>(total) * xcd / 8);
+  const int hi = static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8);
+  const WideTail tail = wide_tail(lo, hi, true, static_cast<int>(p.kdim * ESZ / SK));
+  if (tail.S < 2 || t >= tail.rem) return;
+  int rb, ct;
+  if (!wide_walk(lo, hi, n_ct, p.group_n, 32 * tail.R + t, &rb, &ct)) return;
+  const int lane = threadIdx.x & 63;
+  const int slot0 = xcd * 32 + t * tail.S;
+  // a wave's 8 rows in two batches of 4, every piece of a batch's rows in
+  // flight at once (the reads, not the adds, set this kernel's time)
+  constexpr int RW = 4;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    int tr[RW], sid[RW];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+      tr[j] = rblk * 32 + (b * RW + j) * 4 + static_cast<int>(threadIdx.x >> 6);
+      sid[j] = p.sorted_ids[rb * BM + tr[j]];
+    }
+    f32x4 part[RW][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < RW; ++j)
+        part[j][i] = i < tail.S && sid[j] < p.numel
+                         ? *reinterpret_cast<const f32x4*>(
+                               p.tail_part + (static_cast<int64_t>(slot0 + i) * BM + tr[j]) * BNR +
+                               lane * 4)
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+      if (sid[j] >= p.numel) continue;
+      // pieces in order: ((p0 + p1) + p2) + p3; absent pieces add zero
+      const f32x4 acc = ((part[j][0] + part[j][1]) + part[j][2]) + part[j][3];
+      uint2 v;
+      v.x = pack_bf16x2(acc[0], acc[1]);
+      v.y = pack_bf16x2(acc[2], acc[3]);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + static_cast<int64_t>(sid[j]) * p.n_out +
+                                ct * BNR + lane * 4) = v;
+    }
+  }
+}
+
+int64_t wide_tail_part_bytes() {
+  return static_cast<int64_t>(kWideTailSlots) * WideRing::BM * WideRing::BNR * 4;
 }
 
 // Whether the 4-wave kernel covers a launch: bf16 / int8, GEMM1 with
@@ -609,19 +753,25 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
   GemmParams q = p;
   q.row_blocks = row_blocks;
   if (GEMM1 || q.ksplit < 1) q.ksplit = 1;
+  if (GEMM1 || !q.tail_part) q.tail_split = 0;
+  if (q.tail_split) q.ksplit = 1;
   const int n_ct_walk = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   const double rows_per_expert =
       p.num_experts > 0 ? static_cast<double>(p.numel) / p.num_experts : 0.0;
   if (q.group_n < 1) q.group_n = wide_group_n_choice(GEMM1, n_ct_walk, rows_per_expert);
   // enough positions for the largest XCD walk the kernel can form from the
-  // launched row blocks (it splits the live ones, known on the device)
+  // launched row blocks (it splits the live ones, known on the device), and
+  // for the tail pieces of its last round
   const int n_ct = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   const int64_t total = static_cast<int64_t>(row_blocks) * q.ksplit * n_ct;
-  const int64_t n_rb = (total + 7) / 8 / n_ct + 2;
-  const int64_t n_pos = (n_ct + q.group_n - 1) / q.group_n * n_rb * q.group_n;
+  const int64_t n_pos = (total + 7) / 8 + (q.tail_split ? 32 : 0);
   const int grid = static_cast<int>(8 * n_pos);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(C::NW * 64), C::LDS_BYTES, stream, q);
-  return check_launch("moe_gemm_wide_kernel");
+  int rc = check_launch("moe_gemm_wide_kernel");
+  if (rc || !q.tail_split) return rc;
+  hipLaunchKernelGGL((moe_wide_tail_fixup_kernel<C::BM, C::BNR, C::SK, TiledType<DT>::ESZ>),
+                     dim3(8 * 32 * (C::BM / 32)), dim3(256), 0, stream, q);
+  return check_launch("moe_wide_tail_fixup_kernel");
 }
 
 int launch_gemm_wide(int dt, bool gemm1, const GemmParams& p, int row_blocks,

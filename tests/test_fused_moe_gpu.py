@@ -285,6 +285,30 @@ def test_gemm2_k_split(gpu, shape, mode):
     _check(res.cpu()[toks], ref, mode, f"k-split {shape} {mode}")
 
 
+@pytest.mark.parametrize("mode", ["bf16", "int8"])
+@pytest.mark.parametrize("shape", [(4096, 4096, 512, 8, 2), (3500, 4096, 1024, 8, 2),
+                                   (2600, 2048, 768, 16, 3)],
+                         ids=["rem8_S4", "rem_S2", "E16_top3"])
+def test_gemm2_tail_split(gpu, shape, mode):
+    """GEMM2 of 256-row blocks over 1 to 8 rounds of the CUs runs on the
+    4-wave kernel with its last round's tiles split over k into pieces whose
+    fp32 partials a fixup kernel adds in order (M=4096 top-2 over 8 experts:
+    about 36 row blocks x 16 column tiles = 72 tiles per XCD, the last 8 in 4
+    pieces each)."""
+    M, K, N, E, topk = shape
+    wts = testing.make_weights(K, N, E, mode, 0.05, device=gpu, seed=M + K + N + 1)
+    x, tw, ti = testing.make_tokens(M, K, E, topk, device=gpu, seed=M + K + N + 1)
+    res = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, **wts.kwargs(mode))
+    toks = _sample(M, 24)
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=mode, w1_scale=wts.w1_scale,
+                            w2_scale=wts.w2_scale, tokens=toks, return_mag=True)
+    _check(res.cpu()[toks], ref, mode, f"tail split {shape} {mode}")
+    # every token: the fixed-up tiles cover whole column ranges, so compare
+    # all rows against a second, deterministic call
+    again = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, **wts.kwargs(mode))
+    assert torch.equal(res, again)
+
+
 # ------------------------------------------------- activations and biases ---
 _SCHEDS = [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL]
 

@@ -72,6 +72,10 @@ def parse():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (the reference "
                          "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--summarize", nargs="+", metavar=("DIR", "CFG:M"),
+                    help="no GPU work: turn the rocprofv3 CSV output under DIR "
+                         "into profiles/moe_kernels_<cfg>_m<M>.md, "
+                         "traffic_<cfg>.json and mfma_<cfg>.json")
     return ap.parse_args()
 
 
@@ -328,6 +332,273 @@ def sweep_config(cfg, dev, args):
     return rows
 
 
+# ---------------------------------------------------------------------------
+# rocprofv3 output -> committed summaries (no GPU work; run after the passes)
+
+PROFILE_TITLES = {
+    "mixtral": "Mixtral-8x7B-shaped bf16 layer",
+    "deepseek_fp8": "DeepSeek-V3-shaped fp8 (128x128 block scales) layer",
+    "qwen3": "Qwen3-30B-A3B-shaped bf16 layer",
+    "qwen3_skewed": "Qwen3-30B-A3B-shaped bf16 layer, skewed routing",
+    "qwen2_int8": "Qwen2-57B-A14B-shaped int8 (per-channel) layer",
+    "small": "small bf16 layer",
+}
+STAGE_ORDER = ("align", "quant_x", "gemm1", "quant_a2", "gemm2", "moe_sum")
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_VALU",
+                 "SQ_INSTS_MFMA", "GRBM_GUI_ACTIVE")
+N_XCD, N_CU, N_SIMD = 8, 256, 1024
+
+
+def _template_args(name):
+    """Top-level template arguments of a demangled kernel name."""
+    inner = name[name.index("<") + 1:]
+    depth, args, cur = 0, [], ""
+    for ch in inner:
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            if depth == 0:
+                args.append(cur.strip())
+                break
+            depth -= 1
+        elif ch == "," and depth == 0:
+            args.append(cur.strip())
+            cur = ""
+            continue
+        cur += ch
+    return args
+
+
+def _kernel_stage(name, after_gemm1):
+    """The layer stage a library kernel belongs to (None: not a layer kernel,
+    e.g. the flush fill). Quantiser launches before GEMM1 in a call quantise
+    x, after it the GEMM1 output."""
+    if "fgs::" not in name:
+        return None
+    if "align" in name:
+        return "align"
+    if "quant_" in name:
+        return "quant_a2" if after_gemm1 else "quant_x"
+    if "gemm2_direct" in name or "tail_fixup" in name:
+        return "gemm2"
+    if "moe_gemm" in name:
+        args = _template_args(name)
+        if "gemm_stream" in name:
+            g1 = args[3] == "true"
+        elif "gemm_wide" in name:
+            g1 = args[1] == "true"
+        else:
+            g1 = args[-1] == "true"
+        return "gemm1" if g1 else "gemm2"
+    if "moe_sum" in name:
+        return "moe_sum"
+    if "silu" in name:
+        return "silu"
+    return None
+
+
+def _csv_rows(src, sub, kind):
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(src, sub, "**", f"*{kind}.csv"), recursive=True)
+    if not files:
+        return None
+    with open(files[0]) as f:
+        return list(csv.DictReader(f))
+
+
+def _dispatches(rows, counters=False):
+    """[(stage, kernel, value)] in dispatch order; value = duration in ns, or
+    {counter: value} for a counter-collection CSV."""
+    per = {}
+    for r in rows:
+        d = per.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
+        if counters:
+            d.setdefault("c", {})[r["Counter_Name"]] = float(r["Counter_Value"])
+        else:
+            d["v"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    out, after_gemm1 = [], False
+    for _, d in sorted(per.items()):
+        st = _kernel_stage(d["name"], after_gemm1)
+        if st is None:
+            continue
+        if st in ("align", "gemm2", "moe_sum"):
+            after_gemm1 = False  # the next quantiser belongs to the next call
+        elif st == "gemm1":
+            after_gemm1 = True
+        out.append((st, d["name"], d["c"] if counters else d["v"]))
+    return out
+
+
+def _merge_json(path, calibration, entries):
+    data = {"by_stage": {}}
+    if os.path.exists(path):
+        with open(path) as f:
+            data = json.load(f)
+    if calibration is not None:
+        data["calibration"] = calibration
+    data.setdefault("by_stage", {}).update(entries)
+    data["by_stage"] = dict(sorted(data["by_stage"].items()))
+    with open(path, "w") as f:
+        json.dump(data, f, indent=1)
+        f.write("\n")
+
+
+def summarize(src, specs, warmup=3):
+    """Writes the committed summaries for each CFG:M from the rocprofv3 runs
+    under `src`: <cfg>_m<M>_kt (kernel trace), <cfg>_m<M>_FETCH_SIZE /
+    _WRITE_SIZE (HBM bytes), <cfg>_m<M>_mfma (MFMA_COUNTERS) and
+    cal_FETCH_SIZE / cal_WRITE_SIZE (the 1 GiB copy of --calibrate-copy).
+    Each kernel's first `warmup` trace dispatches are dropped."""
+    import statistics
+    from collections import OrderedDict, defaultdict
+
+    mean = statistics.mean
+    cal = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        rows = _csv_rows(src, f"cal_{c}", "counter_collection")
+        if rows:
+            vals = [float(r["Counter_Value"]) for r in rows
+                    if "copyBuffer" in r["Kernel_Name"]]
+            cal[c] = mean(vals)
+    calibration = None
+    if len(cal) == 2:
+        calibration = {
+            "kernel": "__amd_rocclr_copyBuffer (torch copy_ of 1 GiB)",
+            "FETCH_SIZE_KiB": cal["FETCH_SIZE"], "WRITE_SIZE_KiB": cal["WRITE_SIZE"],
+            "fetch_factor": (1 << 30) / (cal["FETCH_SIZE"] * 1024),
+            "write_factor": (1 << 30) / (cal["WRITE_SIZE"] * 1024)}
+    for spec in specs:
+        cfg, m = spec.split(":")
+        base = f"{cfg}_m{m}"
+        kt_rows = _csv_rows(src, base + "_kt", "kernel_trace")
+        if kt_rows is None:
+            raise SystemExit(f"no kernel trace under {src}/{base}_kt")
+        agg = OrderedDict()
+        for st, n, v in _dispatches(kt_rows):
+            agg.setdefault((st, n), []).append(v)
+        for k in agg:
+            if len(agg[k]) > warmup:
+                agg[k] = agg[k][warmup:]
+        keys = sorted(agg, key=lambda k: STAGE_ORDER.index(k[0])
+                      if k[0] in STAGE_ORDER else 99)
+        tot = sum(sum(v) for v in agg.values())
+        bench_kt = (f"python3 bench.py --config {cfg} --m {m} --steps 20 "
+                    f"--warmup {warmup} --no-sweep --no-cpu")
+        bench_pmc = (f"python3 bench.py --config {cfg} --m {m} --steps 3 "
+                     f"--warmup 1 --no-sweep --no-cpu")
+        lines = [
+            f"# fused-MoE kernels, {PROFILE_TITLES.get(cfg, cfg)}, M={m}", "",
+            "Kernel time (rocprofv3 kernel trace of the bench run; each kernel's",
+            f"first {warmup} dispatches, the warmup, are left out, leaving the timed",
+            "calls and the calls of the untimed stage-split pass; a quantiser before",
+            "GEMM1 quantises x, one after it the GEMM1 output). Made by",
+            "", f"    rocprofv3 --kernel-trace --stats -f csv -d <dir>/{base}_kt -o run -- {bench_kt}",
+            f"    python3 bench.py --summarize <dir> {cfg}:{m}", "",
+            "| stage | kernel | calls | avg us | min us | max us | % of GPU time |",
+            "|---|---|---|---|---|---|---|"]
+        for k in keys:
+            v = agg[k]
+            lines.append(f"| {k[0]} | `{k[1][:110]}` | {len(v)} | {mean(v) / 1e3:.1f} | "
+                         f"{min(v) / 1e3:.1f} | {max(v) / 1e3:.1f} | "
+                         f"{100 * sum(v) / tot:.1f} |")
+        # per-call stage sums of the kernel trace (several kernels per stage)
+        stage_ns = defaultdict(float)
+        for k in keys:
+            stage_ns[k[0]] += mean(agg[k])
+
+        def by_kernel(sub):
+            rows = _csv_rows(src, sub, "counter_collection")
+            if rows is None:
+                return None
+            d = defaultdict(list)
+            for st, n, c in _dispatches(rows, counters=True):
+                d[(st, n)].append(c)
+            return d
+
+        fe, wr = by_kernel(base + "_FETCH_SIZE"), by_kernel(base + "_WRITE_SIZE")
+        traffic = {}
+        if fe is not None and wr is not None and calibration is not None:
+            ff, wf = calibration["fetch_factor"], calibration["write_factor"]
+            lines += [
+                "", "HBM traffic per dispatch (two counter passes, each scaled by the same",
+                "counter's reading for a plain 1 GiB device copy):", "",
+                f"    rocprofv3 --pmc FETCH_SIZE -f csv -d <dir>/{base}_FETCH_SIZE -o run -- {bench_pmc}",
+                f"    rocprofv3 --pmc WRITE_SIZE -f csv -d <dir>/{base}_WRITE_SIZE -o run -- {bench_pmc}",
+                "    rocprofv3 --pmc FETCH_SIZE -f csv -d <dir>/cal_FETCH_SIZE -o run -- "
+                "python3 bench.py --calibrate-copy   (and WRITE_SIZE)", "",
+                f"Copy calibration: FETCH_SIZE reads {cal['FETCH_SIZE']:.0f} KiB and WRITE_SIZE "
+                f"{cal['WRITE_SIZE']:.0f} KiB for 1 GiB",
+                f"read + 1 GiB written, so fetch bytes = FETCH_SIZE x 1024 x {ff:.3f} and "
+                f"write bytes = WRITE_SIZE x 1024 x {wf:.3f}.", "",
+                "| stage | kernel | fetch MB | write MB | avg us | fetch+write GB/s |",
+                "|---|---|---|---|---|---|"]
+            for k in keys:
+                f = mean(c["FETCH_SIZE"] for c in fe[k]) * 1024 * ff if fe.get(k) else 0.0
+                w = mean(c["WRITE_SIZE"] for c in wr[k]) * 1024 * wf if wr.get(k) else 0.0
+                avg = mean(agg[k])
+                lines.append(f"| {k[0]} | `{k[1][:110]}` | {f / 1e6:.1f} | {w / 1e6:.1f} | "
+                             f"{avg / 1e3:.1f} | {(f + w) / avg:.0f} |")
+                e = traffic.setdefault(f"{cfg}:{m}:{k[0]}", {
+                    "kernel": k[1], "avg_ns": 0.0, "fetch_bytes": 0.0, "write_bytes": 0.0})
+                if e["kernel"] != k[1]:
+                    e["kernel"] += " + " + k[1]
+                e["avg_ns"] += avg
+                e["fetch_bytes"] += f
+                e["write_bytes"] += w
+            _merge_json(os.path.join(ROOT, "profiles", f"traffic_{cfg}.json"),
+                        calibration, traffic)
+        mf = by_kernel(base + "_mfma")
+        if mf is not None:
+            lines += [
+                "", "MFMA utilisation per dispatch (one counter pass):", "",
+                f"    rocprofv3 --pmc {' '.join(MFMA_COUNTERS)} -f csv -d <dir>/{base}_mfma "
+                f"-o run -- {bench_pmc}", "",
+                "mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs):",
+                "the fraction of SIMD cycles the matrix pipe is busy (GRBM_GUI_ACTIVE reads",
+                "as the sum of the 8 XCDs' active cycles; SQ_VALU_MFMA_BUSY_CYCLES sums the",
+                "SIMDs). cu_busy = SQ_BUSY_CU_CYCLES / (GRBM_GUI_ACTIVE / 8 x 256 CUs).",
+                "valu_per_mfma = (SQ_INSTS_VALU - SQ_INSTS_MFMA) / SQ_INSTS_MFMA (SQ_INSTS_VALU",
+                "counts the MFMA instructions too).", "",
+                "| stage | kernel | mfma_busy | cu_busy | valu_per_mfma | MFMA insts | GRBM_GUI_ACTIVE |",
+                "|---|---|---|---|---|---|---|"]
+            stage_c = {}
+            for k in keys:
+                if not mf.get(k):
+                    continue
+                c = {n: mean(d.get(n, 0.0) for d in mf[k]) for n in MFMA_COUNTERS}
+                acc = stage_c.setdefault(k[0], dict.fromkeys(MFMA_COUNTERS, 0.0))
+                for n in MFMA_COUNTERS:
+                    acc[n] += c[n]
+                acc.setdefault("kernels", []).append(k[1])
+                simd = c["GRBM_GUI_ACTIVE"] / N_XCD * N_SIMD
+                busy = c["SQ_VALU_MFMA_BUSY_CYCLES"] / simd if simd else 0.0
+                cu = c["SQ_BUSY_CU_CYCLES"] / (c["GRBM_GUI_ACTIVE"] / N_XCD * N_CU) if simd else 0.0
+                vpm = ((c["SQ_INSTS_VALU"] - c["SQ_INSTS_MFMA"]) / c["SQ_INSTS_MFMA"]
+                       if c["SQ_INSTS_MFMA"] else None)
+                lines.append(f"| {k[0]} | `{k[1][:110]}` | {busy:.3f} | {cu:.3f} | "
+                             f"{'-' if vpm is None else f'{vpm:.2f}'} | "
+                             f"{c['SQ_INSTS_MFMA']:.4g} | {c['GRBM_GUI_ACTIVE']:.4g} |")
+            entries = {}
+            for st, acc in stage_c.items():
+                if not acc["SQ_INSTS_MFMA"]:
+                    continue
+                simd = acc["GRBM_GUI_ACTIVE"] / N_XCD * N_SIMD
+                entries[f"{cfg}:{m}:{st}"] = {
+                    "kernel": " + ".join(acc["kernels"]),
+                    "avg_ns": stage_ns[st],
+                    "mfma_busy": acc["SQ_VALU_MFMA_BUSY_CYCLES"] / simd,
+                    "cu_busy": acc["SQ_BUSY_CU_CYCLES"] / (simd / 4),
+                    "valu_per_mfma": (acc["SQ_INSTS_VALU"] - acc["SQ_INSTS_MFMA"])
+                    / acc["SQ_INSTS_MFMA"],
+                    "counters": {n: acc[n] for n in MFMA_COUNTERS}}
+            _merge_json(os.path.join(ROOT, "profiles", f"mfma_{cfg}.json"), None, entries)
+        with open(os.path.join(ROOT, "profiles", f"moe_kernels_{cfg}_m{m}.md"), "w") as f:
+            f.write("\n".join(lines) + "\n")
+        log(f"summarized {cfg} M={m}")
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -337,6 +608,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.summarize:
+        summarize(args.summarize[0], args.summarize[1:])
         return
     import torch
 

@@ -37,6 +37,7 @@ static int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
 constexpr int kMaxExperts = 1024;
 constexpr int kKnownFlags = FGS_FLAG_ROUTER_WEIGHT_ON_INPUT | FGS_FLAG_ACT_GELU |
+                            FGS_FLAG_SINGLE_FUSED |
                             FGS_FLAG_FORCE_DECODE | FGS_FLAG_FORCE_PREFILL |
                             FGS_FLAG_SEPARATE_SUM | FGS_FLAG_FOLD_SUM |
                             FGS_FLAG_TILE_MASK;
@@ -62,9 +63,13 @@ struct Plan {
                    // (no alignment; distinct experts per token)
   bool direct_sum; // ... and GEMM2 folds the top-k sum (no moe_sum)
   int kwd;         // waves of the folded GEMM2
+  bool fused1;     // one token, bf16: both GEMMs in one launch (decode.hip)
+                   // plus the ordered reduction
+  int chunk1;      // its intermediate columns per workgroup
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
-  int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail, total;
+  int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail, o_part,
+      total;
 };
 
 // k splits for the tiled GEMM2: its grid (row blocks x hidden/256 column
@@ -128,6 +133,16 @@ static int tail_choice() {
     return (x == 0 || x == 1) ? x : 1;
   }();
   return t;
+}
+
+// FGS_MOE_FUSED1=1 makes the single-token fused path of bf16 layers the
+// default (otherwise FGS_FLAG_SINGLE_FUSED selects it; read once).
+static int fused1_choice() {
+  static const int f = [] {
+    const char* v = getenv("FGS_MOE_FUSED1");
+    return v && atoi(v) == 1 ? 1 : 0;
+  }();
+  return f;
 }
 
 static int pick_kw(int64_t kdim, int step, int cap) {
@@ -215,6 +230,16 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   p.direct_sum = p.direct && !(flags & FGS_FLAG_SEPARATE_SUM) &&
                  ((flags & FGS_FLAG_FOLD_SUM) || dc == 3 ||
                   (dc == 1 && p.dt != kDtFp8 && hidden / 16 >= 192));
+  // One bf16 token: GEMM1, the activation and GEMM2 in one launch per
+  // (slot, chunk of intermediate columns), then an ordered reduction (the
+  // schedule flags that pick the unfused sum keep the direct kernels).
+  p.fused1 = p.direct && p.dt == kDtBf16 &&
+             ((flags & FGS_FLAG_SINGLE_FUSED) || fused1_choice()) && topk <= kDecodeMaxSlots &&
+             !(flags & (FGS_FLAG_SEPARATE_SUM | FGS_FLAG_FOLD_SUM)) && hidden % 256 == 0 &&
+             hidden <= kDecodeMaxHidden &&
+             inter % 16 == 0;
+  p.chunk1 = p.fused1 ? decode_chunk(hidden, inter, topk) : 0;
+  if (p.fused1) p.direct_sum = false;
   // the folded GEMM2's waves: as many as keep its grid (one workgroup per
   // 16 output columns) resident in one round at 16 waves per CU
   const int64_t wgs = hidden / 16;
@@ -249,6 +274,7 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   }
   p.o_y = take(p.ksplit2 > 1 ? p.ksplit2 * numel * hidden * 4 : numel * hidden * 2);
   p.o_tail = p.tail2 ? take(wide_tail_part_bytes()) : -1;
+  p.o_part = p.fused1 ? take(static_cast<int64_t>(topk) * (inter / p.chunk1) * hidden * 4) : -1;
   p.total = o;
   *pl = p;
   return FGS_OK;
@@ -421,6 +447,36 @@ static int run_fused(const FusedArgs& a) {
   }
 
   g_prof.mark(2, a.stream);
+  if (p.fused1) {
+    DecodeParams d{};
+    d.x = a.x;
+    d.w13 = a.w13;
+    d.w2 = a.w2;
+    d.b13 = a.b13;
+    d.b2 = a.b2;
+    d.topk_w = a.topk_weights;
+    d.ids = a.topk_ids;
+    d.part = reinterpret_cast<float*>(ws + p.o_part);
+    d.out = a.out;
+    d.hidden = a.hidden;
+    d.inter = a.inter;
+    d.slots = a.topk;
+    d.num_experts = a.e;
+    d.chunk = p.chunk1;
+    d.n_chunks = static_cast<int32_t>(a.inter / p.chunk1);
+    d.weight_on_input = on_input ? 1 : 0;
+    d.act = a.swiglu ? kActSwiglu : (a.flags & FGS_FLAG_ACT_GELU) ? kActGelu : kActSilu;
+    d.alpha = a.alpha;
+    d.limit = a.limit;
+    rc = launch_decode_fused(d, a.stream);
+    if (rc) return rc;
+    g_prof.mark(3, a.stream);
+    g_prof.mark(4, a.stream);
+    rc = launch_decode_reduce(d, a.stream);
+    g_prof.mark(5, a.stream);
+    g_prof.mark(6, a.stream);
+    return rc;
+  }
   GemmParams g1{};
   g1.a = act;
   g1.a_scale = act_scale;
@@ -719,6 +775,32 @@ int64_t fgs_moe_workspace_bytes(int64_t m, int64_t hidden, int64_t inter,
   Plan p;
   make_plan(m, hidden, inter, num_experts, topk, qmode, flags, &p);
   return p.total;
+}
+
+int32_t fgs_moe_schedule(int64_t m, int64_t hidden, int64_t inter, int32_t num_experts,
+                         int32_t topk, int32_t qmode, int32_t flags, char* buf,
+                         int32_t len) {
+  int rc = validate(m, hidden, inter, num_experts, topk, qmode, flags, 0, false);
+  if (rc) return rc;
+  if (!buf || len < 1) return fail(FGS_EINVAL, "buf must hold at least one byte");
+  Plan p;
+  make_plan(m, hidden, inter, num_experts, topk, qmode, flags, &p);
+  std::string s;
+  if (p.fused1) {
+    s = "fused1 chunk=" + std::to_string(p.chunk1);
+  } else if (p.direct) {
+    s = p.direct_sum ? "direct_sum" : "direct";
+  } else if (!p.tiled) {
+    s = "stream mt=" + std::to_string(p.mt);
+  } else {
+    s = "tiled cfg=" + std::to_string(p.tile_cfg) + " cfg2=" + std::to_string(p.tile_cfg2);
+    if (p.ksplit2 > 1) s += " ksplit2=" + std::to_string(p.ksplit2);
+    if (p.tail2) s += " tail2";
+  }
+  const size_t n = std::min(s.size(), static_cast<size_t>(len - 1));
+  memcpy(buf, s.data(), n);
+  buf[n] = 0;
+  return FGS_OK;
 }
 
 int32_t fgs_moe_validate(int64_t m, int64_t hidden, int64_t inter,

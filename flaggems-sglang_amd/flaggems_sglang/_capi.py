@@ -25,6 +25,7 @@ SCORING_SIGMOID = 1
 
 FLAG_ROUTER_WEIGHT_ON_INPUT = 0x1
 FLAG_ACT_GELU = 0x2
+FLAG_SINGLE_FUSED = 0x4
 FLAG_FORCE_DECODE = 0x100
 FLAG_FORCE_PREFILL = 0x200
 FLAG_SEPARATE_SUM = 0x400
@@ -77,6 +78,7 @@ SIGNATURES = {
     ),
     "fgs_moe_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32, _i32]),
     "fgs_moe_validate": (_i32, [_i64, _i64, _i64, _i32, _i32, _i32, _i32, _i64]),
+    "fgs_moe_schedule": (_i32, [_i64, _i64, _i64, _i32, _i32, _i32, _i32, _c_void_p, _i32]),
     "fgs_moe_fused_bf16": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
@@ -160,3 +162,13 @@ def check(rc: int, what: str) -> None:
     if rc == FGS_EUNSUPPORTED:
         raise NotImplementedError(msg)
     raise RuntimeError(msg)
+
+
+def schedule(m: int, hidden: int, inter: int, num_experts: int, topk: int,
+             qmode: int = QMODE_BF16, flags: int = 0) -> str:
+    """The schedule a fused call of this problem runs (``fgs_moe_schedule``):
+    "fused1 chunk=C", "direct", "direct_sum", "stream mt=T" or "tiled ..."."""
+    buf = ctypes.create_string_buffer(96)
+    check(load().fgs_moe_schedule(m, hidden, inter, num_experts, topk, qmode, flags,
+                                  buf, len(buf)), "schedule")
+    return buf.value.decode()

@@ -56,6 +56,13 @@ extern "C" {
 #define FGS_FLAG_SEPARATE_SUM 0x400
 /* schedule: a one-token call folds the weighted top-k sum into GEMM2 */
 #define FGS_FLAG_FOLD_SUM 0x800
+/* schedule: a one-token bf16 call runs GEMM1, the activation and GEMM2 in
+ * one launch per (slot, chunk of intermediate columns), then an ordered
+ * reduction (top-k <= 16, hidden % 256 == 0, hidden <= 16384,
+ * inter % 16 == 0; measured at parity with the default two-GEMM schedule on
+ * Qwen3-shaped layers and slower on Mixtral-shaped ones, so not the default;
+ * the FGS_MOE_FUSED1=1 environment variable makes it the default) */
+#define FGS_FLAG_SINGLE_FUSED 0x4
 /* schedule: LDS-tiled kernels with row-block configuration c (0: 256 rows,
  * 1: 128, 2: 64, 3: 32) instead of the rows-per-expert choice */
 #define FGS_FLAG_TILE(c) ((((c) + 1) & 0x7) << 12)
@@ -183,6 +190,18 @@ int32_t fgs_moe_quant_int8_token(const void* x, int8_t* q, float* scales,
 int64_t fgs_moe_workspace_bytes(int64_t m, int64_t hidden, int64_t inter,
                                 int32_t num_experts, int32_t topk,
                                 int32_t qmode, int32_t flags);
+
+/* The schedule a fused call of this problem runs, as a short text into
+ * buf (NUL-terminated, truncated to len - 1 bytes): "fused1 chunk=C" (one
+ * bf16 token: both GEMMs in one launch, then the ordered reduction),
+ * "direct" / "direct_sum" (one token, two streaming GEMMs, the top-k sum
+ * separate / folded into GEMM2), "stream mt=T" (streaming GEMMs over the
+ * aligned rows) or "tiled cfg=A cfg2=B [ksplit2=S] [tail2]" (LDS-tiled
+ * GEMMs). Host-only. No counterpart in the reference (a diagnostic for
+ * benchmarks and tests). */
+int32_t fgs_moe_schedule(int64_t m, int64_t hidden, int64_t inter, int32_t num_experts,
+                         int32_t topk, int32_t qmode, int32_t flags, char* buf,
+                         int32_t len);
 
 /* Host-only validation of a problem (no device access). Returns FGS_OK or
  * the status and message the fused entry point would return. */

@@ -37,7 +37,7 @@ static int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
 constexpr int kMaxExperts = 1024;
 constexpr int kKnownFlags = FGS_FLAG_ROUTER_WEIGHT_ON_INPUT | FGS_FLAG_ACT_GELU |
-                            FGS_FLAG_SINGLE_FUSED |
+                            FGS_FLAG_SINGLE_FUSED | FGS_FLAG_SEPARATE_QUANT |
                             FGS_FLAG_FORCE_DECODE | FGS_FLAG_FORCE_PREFILL |
                             FGS_FLAG_SEPARATE_SUM | FGS_FLAG_FOLD_SUM |
                             FGS_FLAG_TILE_MASK;
@@ -66,6 +66,9 @@ struct Plan {
   bool fused1;     // one token, bf16: both GEMMs in one launch (decode.hip)
                    // plus the ordered reduction
   int chunk1;      // its intermediate columns per workgroup
+  bool qfold1;     // one token, fp8: GEMM1 quantises x itself
+  bool qfold;      // one token, fp8: GEMM2 quantises the GEMM1 output rows
+                   // itself (no quantiser launch between the GEMMs)
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
   int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail, o_part,
@@ -143,6 +146,16 @@ static int fused1_choice() {
     return v && atoi(v) == 1 ? 1 : 0;
   }();
   return f;
+}
+
+// FGS_MOE_QFOLD (0 off, 1 default) switches the single-token GEMMs'
+// on-the-fly activation quantisation (a tuning aid; read once).
+static int qfold_choice() {
+  static const int q = [] {
+    const char* v = getenv("FGS_MOE_QFOLD");
+    return v && atoi(v) == 0 ? 0 : 1;
+  }();
+  return q;
 }
 
 static int pick_kw(int64_t kdim, int step, int cap) {
@@ -227,6 +240,16 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // column tiles -- Qwen2 int8 -6.5 %, Mixtral -2 % -- and loses for Qwen3's
   // 128 tiles, +1.5 %, and for fp8, whose per-step block scales keep the
   // unfolded GEMM2 + moe_sum ahead, +3 %)
+  // One fp8 token: the GEMMs quantise their activation rows (x, the GEMM1
+  // output) themselves, with the group quantiser's arithmetic. Measured
+  // (DeepSeek fp8 M=1, 3 x 50 flushed calls): 88.4 -> 83.0 us. int8's
+  // per-token scale needs each row's amax before any of it is quantised:
+  // done in the GEMMs (every workgroup reducing the whole row first) it cost
+  // what the quantiser launches cost (Qwen2 int8 M=1: 63.5 -> 63.8 us with
+  // the GEMM2 rows, +5.6 us with x in GEMM1), so int8 keeps the quantisers.
+  p.qfold = p.direct && p.dt == kDtFp8 && qfold_choice() && topk <= kQaMaxSlots &&
+            !(flags & FGS_FLAG_SEPARATE_QUANT);
+  p.qfold1 = p.qfold;
   p.direct_sum = p.direct && !(flags & FGS_FLAG_SEPARATE_SUM) &&
                  ((flags & FGS_FLAG_FOLD_SUM) || dc == 3 ||
                   (dc == 1 && p.dt != kDtFp8 && hidden / 16 >= 192));
@@ -430,7 +453,9 @@ static int run_fused(const FusedArgs& a) {
   const bool on_input = (a.flags & FGS_FLAG_ROUTER_WEIGHT_ON_INPUT) != 0;
   const uint8_t* act = static_cast<const uint8_t*>(a.x);
   const float* act_scale = nullptr;
-  if (p.dt == kDtFp8) {
+  if (p.qfold1) {
+    // GEMM1 quantises x itself
+  } else if (p.dt == kDtFp8) {
     rc = launch_quant_fp8_group(a.x, ws + p.o_xq,
                                 reinterpret_cast<float*>(ws + p.o_xs), a.m,
                                 a.hidden, 128, a.stream);
@@ -503,6 +528,7 @@ static int run_fused(const FusedArgs& a) {
     // slot j is row tile j; a2 holds the compact slot rows
     g1.direct_ids = a.topk_ids;
   }
+  if (p.qfold1) g1.a_src = static_cast<const uint16_t*>(a.x);
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, static_cast<int>(p.n_launch),
                                    a.stream)
                : launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
@@ -518,7 +544,9 @@ static int run_fused(const FusedArgs& a) {
   const int64_t a2_rows = p.direct ? numel : p.max_padded;
   const int32_t* a2_npp = p.direct ? nullptr : npp;
   const int32_t* a2_sorted = p.direct ? nullptr : sorted;
-  if (p.dt == kDtFp8) {
+  if (p.qfold) {
+    // GEMM2 quantises the a2 slot rows itself
+  } else if (p.dt == kDtFp8) {
     rc = launch_quant_fp8_group(a2, ws + p.o_a2q,
                                 reinterpret_cast<float*>(ws + p.o_a2s),
                                 a2_rows, a.inter, 128, a.stream, a2_npp, a2_sorted, numel);
@@ -550,6 +578,7 @@ static int run_fused(const FusedArgs& a) {
   g2.tail_part = p.tail2 ? reinterpret_cast<float*>(ws + p.o_tail) : nullptr;
   g2.a_rows = p.max_padded;
   g2.eid_shift = p.tiled ? p.eid_shift2 : 0;
+  g2.a_src = p.qfold ? a2 : nullptr;
   if (p.direct_sum) {
     // out = the weighted top-k sum, straight from GEMM2
     g2.out = a.out;
@@ -790,6 +819,7 @@ int32_t fgs_moe_schedule(int64_t m, int64_t hidden, int64_t inter, int32_t num_e
     s = "fused1 chunk=" + std::to_string(p.chunk1);
   } else if (p.direct) {
     s = p.direct_sum ? "direct_sum" : "direct";
+    if (p.qfold) s += " qfold";
   } else if (!p.tiled) {
     s = "stream mt=" + std::to_string(p.mt);
   } else {

@@ -13,6 +13,8 @@ enum : int { kDtBf16 = 0, kDtFp8 = 1, kDtInt8 = 2 };
 //          w = w13 [E, 2*n_out, kdim], out = a2 bf16 [rows_pad, n_out].
 //   GEMM2: a = a2 [rows_pad, kdim] (row = padded position),
 //          w = w2 [E, n_out, kdim], out = per-slot y bf16 [numel, n_out].
+constexpr int kQaMaxSlots = 64;  // on-the-fly quantisation: slots per call
+
 struct GemmParams {
   const uint8_t* a;
   const float* a_scale;   // fp8: [rows, kdim/128]; int8: [rows]; else null
@@ -46,6 +48,10 @@ struct GemmParams {
                               // k into pieces (partials in tail_part, fixed up
                               // into out); needs ksplit 1
   float* tail_part;           // wide_tail_part_bytes() of fp32 partials
+  const uint16_t* a_src;      // direct rows, fp8 (at most kQaMaxSlots
+                              // slots): the bf16 activation
+                              // rows ([a_rows, kdim]) the kernel quantises
+                              // itself (a and a_scale unused); null: off
 };
 
 // Router gating (scores -> top-k -> renormalise), one wave per token;
@@ -112,7 +118,8 @@ int stream_step_k(int dt);
 int launch_gemm_stream(int dt, bool gemm1, const GemmParams& p, int mt, int kw,
                        int row_blocks, hipStream_t stream);
 // GEMM2 of one token with the top-k sum folded in (p.direct_ids set, p.out
-// the bf16 [1, n_out] output); kw in {4, 8, 16}.
+// the bf16 [1, n_out] output); kw in {4, 8, 16}. With p.a_src (fp8, at
+// most 64 slots) the slot rows are quantised on the fly.
 int launch_gemm2_direct(int dt, const GemmParams& p, int kw, hipStream_t stream);
 
 // Single-token fused path (decode.hip, bf16): GEMM1 + activation + GEMM2

@@ -114,7 +114,48 @@ __device__ __forceinline__ f32x4 mma_fp8(const u32x4 (&a)[2],
   return mfma16_fp8(av, bv, f32x4{0.f, 0.f, 0.f, 0.f});
 }
 
-template <int DT, int MT, int KW, bool GEMM1, bool DIRECT>
+// ---- on-the-fly activation quantisation (direct rows, fp8) ----
+// With p.a_src set, a direct-row fp8 kernel reads its activation row in bf16
+// and quantises it itself, with the arithmetic of quant_fp8_group_kernel
+// (per 128-column group, scale = max(amax, 1e-10) / 448, q =
+// e4m3fn(clamp(x / scale, +-448))), so the bytes and scales match that
+// kernel's output exactly and the quantiser launches drop out of the
+// single-token path.
+//
+// Every lane quantises 2 consecutive values of the step (one 128-column
+// group) and the bytes go through the wave's LDS slot to lanes (0, lg),
+// whose MFMA row 0 fragments hold the step's 16-byte vectors v*64 + lg*16.
+__device__ __forceinline__ uint32_t load_raw(const uint16_t* row, int64_t k0, int lane) {
+  return *reinterpret_cast<const uint32_t*>(row + k0 + lane * 2);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float quant1_fp8(float f, float scale) {
+  return fminf(fmaxf(f / scale, -448.f), 448.f);
+}
+// fp8 step: the group amax by butterfly over the wave, scale =
+// max(amax, 1e-10) / 448 (returned, the same in every lane); qb is the
+// wave's 128-byte LDS slot.
+__device__ __forceinline__ float quant_step_fp8(uint32_t raw, uint8_t* qb, int lane,
+                                               u32x4 (&f)[2]) {
+  const float a = bf16_lo(raw), b = bf16_hi(raw);
+  float amax = fmaxf(fabsf(a), fabsf(b));
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  const float scale = fmaxf(amax, 1e-10f) / 448.0f;
+  reinterpret_cast<uint16_t*>(qb)[lane] =
+      static_cast<uint16_t>(cvt_pk_fp8(quant1_fp8(a, scale), quant1_fp8(b, scale)));
+  const int lg = lane >> 4;
+  const bool row0 = (lane & 15) == 0;
+#pragma unroll
+  for (int v = 0; v < 2; ++v)
+    f[v] = row0 ? *reinterpret_cast<const u32x4*>(qb + v * 64 + lg * 16) : u32x4{0, 0, 0, 0};
+  return scale;
+}
+
+template <int DT, int MT, int KW, bool GEMM1, bool DIRECT, bool QA>
 __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
     const GemmParams p) {
   typedef StreamTraits<DT> T;
@@ -174,6 +215,13 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
     brow[nb] = p.w + (n * p.kdim) * ESZ + lg * 16;
   }
 
+  // QA: the direct row's bf16 source (the token for GEMM1, slot rb's a2 row
+  // for GEMM2), quantised step by step below
+  static_assert(!QA || (DIRECT && MT == 1 && DT == kDtFp8), "on-the-fly quantisation");
+  const uint16_t* qrow = nullptr;
+  if constexpr (QA) qrow = p.a_src + src_row(rb * BM, rb) * p.kdim;
+  __shared__ __attribute__((aligned(16))) uint8_t qlds[QA ? KW : 1][128];
+
   // fp8 / int8 activation scales of this lane's accumulator rows.
   int64_t crow[MT][4];
   bool cvalid[MT][4];
@@ -201,6 +249,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 
   u32x4 bf[2][NB][NV];
   u32x4 af[2][MT][NV];
+  uint32_t ar[2];  // QA: this lane's two raw bf16 values of the direct row's step
   // fp8 block scales of a step (one 128-k group), fetched with its operands
   float sw[2][NB], sa[2][MT][4];
   auto load_scales = [&](int buf, int kb) {
@@ -211,20 +260,29 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
         sw[buf][nb] = p.w_scale[(static_cast<int64_t>(e) * (p.nrows_w / 128) +
                                  wrow / 128) * kblocks + kb];
       }
+      if constexpr (!QA) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            sa[buf][mt][i] = cvalid[mt][i] ? p.a_scale[crow[mt][i] * kblocks + kb] : 0.f;
+      }
+    }
+  };
+  auto load_a = [&](int buf, int st) {
+    if constexpr (QA) {
+      ar[buf] = load_raw(qrow, static_cast<int64_t>(st) * T::kStepK, lane);
+    } else {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          sa[buf][mt][i] = cvalid[mt][i] ? p.a_scale[crow[mt][i] * kblocks + kb] : 0.f;
+        load_act(af[buf][mt], arow[mt] + st * step_bytes, avalid[mt]);
     }
   };
   if (s0 < s1) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
       load_frag<DT>(bf[0][nb], brow[nb] + s0 * step_bytes, true);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      load_act(af[0][mt], arow[mt] + s0 * step_bytes, avalid[mt]);
+    load_a(0, s0);
     load_scales(0, s0);
   }
   for (int s = s0; s < s1; s += 2) {
@@ -238,10 +296,13 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
           load_frag<DT>(bf[h ^ 1][nb], brow[nb] + nxt * step_bytes, true);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          load_act(af[h ^ 1][mt], arow[mt] + nxt * step_bytes, avalid[mt]);
+        load_a(h ^ 1, nxt);
         load_scales(h ^ 1, nxt);
+      }
+      if constexpr (QA) {
+        const float sc = quant_step_fp8(ar[h], qlds[wave], lane, af[h][0]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sa[h][0][i] = cvalid[0][i] ? sc : 0.f;
       }
       if constexpr (DT == kDtBf16) {
 #pragma unroll
@@ -330,10 +391,10 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
   }
 }
 
-template <int DT, int MT, int KW, bool GEMM1, bool DIRECT>
+template <int DT, int MT, int KW, bool GEMM1, bool DIRECT, bool QA = false>
 static int launch_one(const GemmParams& p, int row_blocks, hipStream_t stream) {
   dim3 grid(row_blocks, static_cast<unsigned>(p.n_out / 16));
-  hipLaunchKernelGGL((moe_gemm_stream_kernel<DT, MT, KW, GEMM1, DIRECT>), grid,
+  hipLaunchKernelGGL((moe_gemm_stream_kernel<DT, MT, KW, GEMM1, DIRECT, QA>), grid,
                      dim3(KW * 64), 0, stream, p);
   return check_launch("moe_gemm_stream_kernel");
 }
@@ -342,7 +403,17 @@ template <int DT, bool GEMM1>
 static int dispatch_kw(const GemmParams& p, int mt, int kw, int row_blocks,
                        hipStream_t stream) {
   if (p.direct_ids) {
-    // direct rows: one slot per 16-row tile
+    // direct rows: one slot per 16-row tile; a_src: quantised on the fly
+    if constexpr (DT == kDtFp8) {
+      if (p.a_src) {
+#define FGS_CASE(KW_)             \
+  if (mt == 1 && kw == KW_)       \
+    return launch_one<DT, 1, KW_, GEMM1, true, true>(p, row_blocks, stream);
+        FGS_CASE(1) FGS_CASE(2) FGS_CASE(4) FGS_CASE(8)
+#undef FGS_CASE
+        return fail(FGS_EUNSUPPORTED, "stream GEMM: no direct-row kernel for this tile");
+      }
+    }
 #define FGS_CASE(KW_) \
   if (mt == 1 && kw == KW_) return launch_one<DT, 1, KW_, GEMM1, true>(p, row_blocks, stream);
     FGS_CASE(1) FGS_CASE(2) FGS_CASE(4) FGS_CASE(8)
@@ -369,7 +440,7 @@ static int dispatch_kw(const GemmParams& p, int mt, int kw, int row_blocks,
 // split its contraction, S > KW deals whole slots to the waves in turn. Only
 // row 0 of the MFMA tile is live (the token; the other activation rows are
 // zero).
-template <int DT, int KW>
+template <int DT, int KW, bool QA>
 __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmParams p) {
   typedef StreamTraits<DT> T;
   typedef typename T::Acc Acc;
@@ -401,6 +472,9 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
     s1 = steps;
   }
 
+  static_assert(!QA || DT == kDtFp8, "on-the-fly quantisation");
+  __shared__ __attribute__((aligned(16))) uint8_t qlds[QA ? KW : 1][128];
+
   // slots <= KW: this wave's partial of slot j0's y (un-weighted);
   // slots > KW: the weighted sum of this wave's complete slots
   f32x4 tot = {0.f, 0.f, 0.f, 0.f};
@@ -418,11 +492,18 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
                            : nullptr;
     Acc acc = {0, 0, 0, 0};
     u32x4 bf[2][NV], af[2][NV];
-    float sc[2];  // fp8: activation x weight block scale of the step
+    uint32_t ar[2];  // QA: this lane's two raw bf16 values of the slot row's step
+    const uint16_t* qrow = QA ? p.a_src + static_cast<int64_t>(j) * p.kdim : nullptr;
+    float sc[2];  // fp8: activation x weight block scale of the step (QA: weight)
     auto load = [&](int buf, int st) {
       load_frag<DT>(bf[buf], brow + st * step_bytes, true);
-      load_act(af[buf], arow + st * step_bytes, avalid);
-      if constexpr (DT == kDtFp8) sc[buf] = p.a_scale[j * kblocks + st] * wsc[st];
+      if constexpr (QA) {
+        ar[buf] = load_raw(qrow, static_cast<int64_t>(st) * T::kStepK, lane);
+        if constexpr (DT == kDtFp8) sc[buf] = wsc[st];
+      } else {
+        load_act(af[buf], arow + st * step_bytes, avalid);
+        if constexpr (DT == kDtFp8) sc[buf] = p.a_scale[j * kblocks + st] * wsc[st];
+      }
     };
     if (s0 < s1) load(0, s0);
     for (int s = s0; s < s1; s += 2) {
@@ -436,9 +517,11 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
         } else if constexpr (DT == kDtInt8) {
           mma_step_i8<DT>(acc, af[h], bf[h]);
         } else {
+          float scl = sc[h];
+          if constexpr (QA) scl = quant_step_fp8(ar[h], qlds[wave], lane, af[h]) * sc[h];
           const f32x4 t = mma_fp8(af[h], bf[h]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] += t[i] * sc[h];
+          for (int i = 0; i < 4; ++i) acc[i] += t[i] * scl;
         }
       }
     }
@@ -451,10 +534,12 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
       for (int i = 0; i < 4; ++i) tot[i] = static_cast<float>(acc[i]) * f;
     } else {
       // the slot's whole y in this wave: round it to bf16 (the slot row the
-      // unfused GEMM2 writes), then weight it
+      // unfused GEMM2 writes), then weight it as moe_sum does (product and
+      // sum rounded separately)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        tot[i] += gamma * bf16_bits_to_f32(f32_to_bf16_bits(static_cast<float>(acc[i]) * f + b));
+        tot[i] = __fadd_rn(tot[i], __fmul_rn(gamma, bf16_bits_to_f32(f32_to_bf16_bits(
+                                                        static_cast<float>(acc[i]) * f + b))));
     }
   }
 
@@ -475,7 +560,8 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
       f32x4 y = red[j * wps][lane];
       for (int w = 1; w < wps; ++w) y += red[j * wps + w][lane];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) tot[i] += gamma * bf16_bits_to_f32(f32_to_bf16_bits(y[i] + b));
+      for (int i = 0; i < 4; ++i)
+        tot[i] = __fadd_rn(tot[i], __fmul_rn(gamma, bf16_bits_to_f32(f32_to_bf16_bits(y[i] + b))));
     }
   } else {
 #pragma unroll
@@ -485,14 +571,14 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
   if (lg == 0) static_cast<uint16_t*>(p.out)[col] = f32_to_bf16_bits(tot[0]);
 }
 
-template <int DT>
+template <int DT, bool QA>
 static int launch_gemm2_direct_t(const GemmParams& p, int kw, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.n_out / 16));
-#define FGS_CASE(KW_)                                                               \
-  if (kw == KW_) {                                                                  \
-    hipLaunchKernelGGL((moe_gemm2_direct_kernel<DT, KW_>), grid, dim3(KW_ * 64), 0, \
-                       stream, p);                                                  \
-    return check_launch("moe_gemm2_direct_kernel");                                 \
+#define FGS_CASE(KW_)                                                                   \
+  if (kw == KW_) {                                                                      \
+    hipLaunchKernelGGL((moe_gemm2_direct_kernel<DT, KW_, QA>), grid, dim3(KW_ * 64), 0, \
+                       stream, p);                                                      \
+    return check_launch("moe_gemm2_direct_kernel");                                     \
   }
   FGS_CASE(4) FGS_CASE(8) FGS_CASE(16)
 #undef FGS_CASE
@@ -502,10 +588,15 @@ static int launch_gemm2_direct_t(const GemmParams& p, int kw, hipStream_t stream
 int launch_gemm2_direct(int dt, const GemmParams& p, int kw, hipStream_t stream) {
   if (!p.direct_ids || p.numel < 1)
     return fail(FGS_EINVAL, "direct GEMM2: needs the slot ids");
+  if (p.a_src && (dt != kDtFp8 || p.numel > kQaMaxSlots))
+    return fail(FGS_EINVAL, "direct GEMM2: on-the-fly quantisation needs fp8 and at most "
+                            "64 slots");
   switch (dt) {
-    case kDtBf16: return launch_gemm2_direct_t<kDtBf16>(p, kw, stream);
-    case kDtFp8: return launch_gemm2_direct_t<kDtFp8>(p, kw, stream);
-    case kDtInt8: return launch_gemm2_direct_t<kDtInt8>(p, kw, stream);
+    case kDtBf16: return launch_gemm2_direct_t<kDtBf16, false>(p, kw, stream);
+    case kDtFp8:
+      return p.a_src ? launch_gemm2_direct_t<kDtFp8, true>(p, kw, stream)
+                     : launch_gemm2_direct_t<kDtFp8, false>(p, kw, stream);
+    case kDtInt8: return launch_gemm2_direct_t<kDtInt8, false>(p, kw, stream);
   }
   return fail(FGS_EUNSUPPORTED, "direct GEMM2: unknown dtype");
 }

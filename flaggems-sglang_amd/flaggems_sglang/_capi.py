@@ -26,6 +26,7 @@ SCORING_SIGMOID = 1
 FLAG_ROUTER_WEIGHT_ON_INPUT = 0x1
 FLAG_ACT_GELU = 0x2
 FLAG_SINGLE_FUSED = 0x4
+FLAG_SEPARATE_QUANT = 0x8
 FLAG_FORCE_DECODE = 0x100
 FLAG_FORCE_PREFILL = 0x200
 FLAG_SEPARATE_SUM = 0x400

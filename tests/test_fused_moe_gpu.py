@@ -283,6 +283,34 @@ def test_single_token_fused_limits(gpu):
     assert not _capi.schedule(1, 3072, 256, 64, 16).startswith("fused1")
 
 
+# An fp8 token's GEMMs quantise x and the GEMM1 output themselves; with
+# FLAG_SEPARATE_QUANT the quantiser kernels do. Same arithmetic, so the
+# outputs are bit-identical (both GEMM2 forms; top-k 20 deals slots to the
+# folded GEMM2's waves in turn, top-k 64 is the on-the-fly limit). int8
+# always runs the quantisers.
+@pytest.mark.parametrize("mode", ["fp8", "int8"])
+@pytest.mark.parametrize("K,N,E,topk", [(3072, 256, 8, 2), (3072, 256, 32, 3),
+                                        (3072, 256, 64, 20), (1024, 512, 16, 4),
+                                        (1024, 256, 64, 64), (7168, 2048, 16, 8)],
+                         ids=lambda v: str(v))
+@pytest.mark.parametrize("fold", [True, False], ids=["folded", "separate"])
+def test_single_token_quant_fold(gpu, mode, K, N, E, topk, fold):
+    sched = _capi.FLAG_FOLD_SUM if fold else _capi.FLAG_SEPARATE_SUM
+    qm = _capi.QMODE_FP8_BLOCK if mode == "fp8" else _capi.QMODE_INT8_CHANNEL
+    assert ("qfold" in _capi.schedule(1, K, N, E, topk, qm, sched)) == (mode == "fp8")
+    assert "qfold" not in _capi.schedule(1, K, N, E, topk, qm,
+                                         sched | _capi.FLAG_SEPARATE_QUANT)
+    wts = testing.make_weights(K, N, E, mode, 0.1, device=gpu, seed=K + N + E + topk + 7)
+    x, tw, ti = testing.make_tokens(1, K, E, topk, device=gpu, seed=K + E + topk + 7)
+    res = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, _flags=sched, **wts.kwargs(mode))
+    sep = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, _flags=sched | _capi.FLAG_SEPARATE_QUANT,
+                       **wts.kwargs(mode))
+    assert torch.equal(res, sep), "on-the-fly quantisation differs from the quantisers"
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=mode, w1_scale=wts.w1_scale,
+                            w2_scale=wts.w2_scale, return_mag=True)
+    _check(res.cpu(), ref, mode, f"M=1 qfold {mode} {(K, N, E, topk)}")
+
+
 def test_single_token_deterministic(gpu):
     wts = testing.make_weights(3072, 256, 8, "bf16", 0.1, device=gpu, seed=5)
     x, tw, ti = testing.make_tokens(1, 3072, 8, 2, device=gpu, seed=5)

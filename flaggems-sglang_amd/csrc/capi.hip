@@ -84,9 +84,11 @@ struct Plan {
 constexpr int kNumCUs = 256;  // MI355X
 
 static int pick_ksplit(int64_t numel, int e, int bm, int64_t hidden,
-                       int64_t k_bytes) {
-  const double blocks = static_cast<double>(numel) / bm +
-                        0.5 * static_cast<double>(std::min<int64_t>(e, numel));
+                       int64_t k_bytes, bool one_block_per_expert = false) {
+  const double blocks = one_block_per_expert
+                            ? static_cast<double>(std::min<int64_t>(e, numel))
+                            : static_cast<double>(numel) / bm +
+                                  0.5 * static_cast<double>(std::min<int64_t>(e, numel));
   const double wgs = blocks * static_cast<double>(hidden / 256);
   int best = 1;
   double best_eff = 0.0;
@@ -211,7 +213,10 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
       p.tile_cfg2 = 1;
       p.eid_shift2 = 1;
     }
-    p.ksplit2 = pick_ksplit(numel, e, tiled_block_m(p.tile_cfg2), hidden, inter * esz);
+    // (the 160-row configuration is chosen below 160 rows per expert: about
+    // one block per touched expert)
+    p.ksplit2 = pick_ksplit(numel, e, tiled_block_m(p.tile_cfg2), hidden, inter * esz,
+                            p.tile_cfg2 == 4 && rows_per_expert < 160);
     // a forced split still keeps >= 8 LDS stages of k per split
     if (forced_ksplit() > 0 && inter * esz / 128 >= 8 * forced_ksplit())
       p.ksplit2 = forced_ksplit();

@@ -153,7 +153,7 @@ int launch_decode_reduce(const DecodeParams& p, hipStream_t stream);
 
 // LDS-tiled MFMA kernels (bf16, fp8, int8): configuration per element type
 // and rows-per-expert regime, its row block, n_out granularity, launch.
-constexpr int kTiledConfigs = 4;
+constexpr int kTiledConfigs = 5;  // row blocks 256, 128, 64, 32, 160
 int tiled_config_supported(int dt, int cfg);
 int tiled_config_for(int dt, double rows_per_expert, int num_experts);
 int tiled_block_m(int cfg);

@@ -760,6 +760,11 @@ using Cfg256 = TileCfg<256, 256, 4, 2, 128, 2>;  // 8 waves of 64x128
 using Cfg128 = TileCfg<128, 256, 2, 4, 128, 3>;  // 8 waves of 64x64
 using Cfg64 = TileCfg<64, 256, 1, 4, 128, 4>;   // 4 waves of 64x64
 using Cfg32 = TileCfg<32, 256, 1, 4, 128, 4>;   // 4 waves of 32x64
+// 160-row blocks for ~100-150 rows per expert (a 256-row block would be
+// half padding): 4 waves of 160x64, a 3-slot ring holding two stages of
+// 256 weight rows in flight (the 256-row configurations hold one or two
+// stages of 128 or 256)
+using Cfg160 = TileCfg<160, 256, 1, 4, 128, 3>;
 // fp8 keeps a second accumulator set per k block (the block-scale fold), so
 // its 256-row configuration has 64x64 wave tiles over 128 weight rows, and
 // the stage scale area costs a stage at 64 and 32 rows.
@@ -768,7 +773,7 @@ using Fp8Cfg64 = TileCfg<64, 256, 1, 4, 128, 3>;
 using Fp8Cfg32 = TileCfg<32, 256, 1, 4, 128, 3>;
 
 static const int kTileRows[kTiledConfigs] = {Cfg256::BM, Cfg128::BM, Cfg64::BM,
-                                             Cfg32::BM};
+                                             Cfg32::BM, Cfg160::BM};
 
 // FGS_MOE_TILE (0..3) forces one configuration (a tuning aid; read once).
 static int forced_tile() {
@@ -801,11 +806,15 @@ int tiled_config_supported(int dt, int cfg) {
 // * the 32-row kernel below that (Mixtral M=32/64, DeepSeek M=32).
 // The 64-row configuration is no longer chosen; it stays for FGS_MOE_TILE.
 int tiled_config_for(int dt, double rows_per_expert, int num_experts) {
-  (void)dt;
   const bool many = num_experts >= 32;
   int c = 3;
   if (rows_per_expert >= 112 || (many && rows_per_expert >= 48)) c = 0;
   else if (rows_per_expert >= 24 || (many && rows_per_expert >= 8)) c = 1;
+  // bf16 with few experts at 96..159 rows each: 160-row blocks, one per
+  // expert (Mixtral M=512: 0.672 -> 0.600 ms; many-expert and fp8 layers
+  // lose with them: their 4-wave 160-row kernel keeps only one wave per
+  // SIMD on a long dependent MFMA / fold chain)
+  if (dt == kDtBf16 && !many && rows_per_expert >= 96 && rows_per_expert < 160) c = 4;
   if (forced_tile() >= 0) c = forced_tile();
   return c;
 }
@@ -846,6 +855,7 @@ int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
         case 0: return launch_cfg<kDtBf16, Cfg256>(gemm1, p, row_blocks, stream);
         case 1: return launch_cfg<kDtBf16, Cfg128>(gemm1, p, row_blocks, stream);
         case 2: return launch_cfg<kDtBf16, Cfg64>(gemm1, p, row_blocks, stream);
+        case 4: return launch_cfg<kDtBf16, Cfg160>(gemm1, p, row_blocks, stream);
         default: return launch_cfg<kDtBf16, Cfg32>(gemm1, p, row_blocks, stream);
       }
     case kDtInt8:
@@ -853,6 +863,7 @@ int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
         case 0: return launch_cfg<kDtInt8, Cfg256>(gemm1, p, row_blocks, stream);
         case 1: return launch_cfg<kDtInt8, Cfg128>(gemm1, p, row_blocks, stream);
         case 2: return launch_cfg<kDtInt8, Cfg64>(gemm1, p, row_blocks, stream);
+        case 4: return launch_cfg<kDtInt8, Cfg160>(gemm1, p, row_blocks, stream);
         default: return launch_cfg<kDtInt8, Cfg32>(gemm1, p, row_blocks, stream);
       }
     case kDtFp8:
@@ -860,6 +871,7 @@ int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
         case 0: return launch_cfg<kDtFp8, Fp8Cfg256>(gemm1, p, row_blocks, stream);
         case 1: return launch_cfg<kDtFp8, Cfg128>(gemm1, p, row_blocks, stream);
         case 2: return launch_cfg<kDtFp8, Fp8Cfg64>(gemm1, p, row_blocks, stream);
+        case 4: return launch_cfg<kDtFp8, Cfg160>(gemm1, p, row_blocks, stream);
         default: return launch_cfg<kDtFp8, Fp8Cfg32>(gemm1, p, row_blocks, stream);
       }
   }

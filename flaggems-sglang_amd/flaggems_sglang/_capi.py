@@ -31,7 +31,7 @@ FLAG_FORCE_DECODE = 0x100
 FLAG_FORCE_PREFILL = 0x200
 FLAG_SEPARATE_SUM = 0x400
 FLAG_FOLD_SUM = 0x800
-TILED_CONFIGS = 4  # row blocks 256, 128, 64, 32
+TILED_CONFIGS = 5  # row blocks 256, 128, 64, 32, 160
 ROUTING_BLOCK_MS = (16, 32, 64, 128)  # tile tables of fgs_moe_topk_to_routing
 NOALLOC_SCRATCH_BYTES = 64 << 20  # FGS_NOALLOC_SCRATCH_BYTES
 

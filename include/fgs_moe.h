@@ -69,7 +69,7 @@ extern "C" {
  * quantiser's arithmetic, so both give the same bytes and scales */
 #define FGS_FLAG_SEPARATE_QUANT 0x8
 /* schedule: LDS-tiled kernels with row-block configuration c (0: 256 rows,
- * 1: 128, 2: 64, 3: 32) instead of the rows-per-expert choice */
+ * 1: 128, 2: 64, 3: 32, 4: 160) instead of the rows-per-expert choice */
 #define FGS_FLAG_TILE(c) ((((c) + 1) & 0x7) << 12)
 #define FGS_FLAG_TILE_MASK 0x7000
 

@@ -57,7 +57,8 @@ def test_align_max_padded():
         ((1, 4096, 14336, 8, 2, 0, 0x40), _capi.FGS_EINVAL, "flag"),
         ((1, 4096, 14336, 8, 2, 0, 0x300), _capi.FGS_EINVAL, "excludes"),
         ((1, 4096, 14336, 8, 2, 0, 0x100 | 0x1000), _capi.FGS_EINVAL, "excludes"),
-        ((1, 4096, 14336, 8, 2, 0, 0x5000), _capi.FGS_EINVAL, "TILE"),
+        ((1, 4096, 14336, 8, 2, 0, 0x6000), _capi.FGS_EINVAL, "TILE"),
+        ((1, 4096, 14336, 8, 2, 0, 0x5000), 0, ""),
         ((1, 4096, 14336, 8, 2, 0, 0x4000), 0, ""),
         ((1, 4096, 14336, 8, 2, 0, 0x400), 0, ""),
         ((1, 4096, 14336, 8, 2, 0, 0x800), 0, ""),

@@ -390,6 +390,45 @@ def test_gemm2_tail_split(gpu, shape, mode):
     assert torch.equal(res, again)
 
 
+def _routing_with_counts(counts, device, seed):
+    """Top-2 routing giving expert e exactly counts[e] slots: token t takes
+    entries t and M + t of the expert-sorted slot list (distinct experts while
+    no count exceeds M), weights from a seeded softmax pair."""
+    total = sum(counts)
+    assert total % 2 == 0 and max(counts) <= total // 2
+    M = total // 2
+    slots = torch.cat([torch.full((c,), e, dtype=torch.int32) for e, c in enumerate(counts)])
+    ids = torch.stack([slots[:M], slots[M:]], 1)
+    g = torch.Generator().manual_seed(seed)
+    w = torch.softmax(torch.randn(M, 2, generator=g), dim=1)
+    return w.to(device), ids.to(device)
+
+
+@pytest.mark.parametrize("mode,N", [("bf16", 256), ("bf16", 128), ("int8", 256)])
+def test_block_remainders(gpu, mode, N):
+    """256-row tiles (the 4-wave kernel) on experts whose last block holds
+    1, 8, 31..33, 63..65 or 200 rows after one or two full blocks -- the
+    partially filled 32-row MFMA blocks and the all-pad ones the kernel
+    skips -- every token checked (N=128: a GEMM2 of two k stages, the ring
+    depth)."""
+    K, E = 512, 10
+    rem = [1, 8, 31, 32, 33, 63, 64, 65, 200, 1]
+    counts = [256 * (1 + e % 2) + r for e, r in enumerate(rem)]
+    w, ids = _routing_with_counts(counts, gpu, seed=N)
+    M = ids.shape[0]
+    wts = testing.make_weights(K, N, E, mode, 0.05, device=gpu, seed=K + N + 7)
+    g = torch.Generator(device=gpu).manual_seed(N + 11)
+    x = torch.randn(M, K, generator=g, device=gpu).to(torch.bfloat16)
+    res = fm.fused_moe(x, wts.w1, wts.w2, w, ids, _flags=_capi.flag_tile(0),
+                       **wts.kwargs(mode))
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, w, ids, mode=mode, w1_scale=wts.w1_scale,
+                            w2_scale=wts.w2_scale, return_mag=True)
+    _check(res.cpu(), ref, mode, f"block remainders N={N} {mode}")
+    again = fm.fused_moe(x, wts.w1, wts.w2, w, ids, _flags=_capi.flag_tile(0),
+                         **wts.kwargs(mode))
+    assert torch.equal(res, again)
+
+
 # ------------------------------------------------- activations and biases ---
 _SCHEDS = [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL]
 

@@ -227,12 +227,18 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
     }
   }
 
-  auto issue = [&](int kt, int slot) {
+  // A wave whose activation-load rows are all padding (they are a suffix of
+  // the block) issues none of its activation loads: those rows' LDS holds
+  // stale bytes, which only the all-pad rows' (discarded) outputs see.
+  const bool a_on = __builtin_amdgcn_readfirstlane(a_sid[0]) < p.numel;
+  auto issue = [&](int kt, int slot, auto a_on_c) {
     const int64_t koff = static_cast<int64_t>(kt) * SK;
     uint8_t* base = lds + slot * STAGE;
+    if constexpr (decltype(a_on_c)::value) {
 #pragma unroll
-    for (int i = 0; i < NLA; ++i)
-      lds_dma16(a_src[i] + koff, base + (wave * NLA + i) * 1024);
+      for (int i = 0; i < NLA; ++i)
+        lds_dma16(a_src[i] + koff, base + (wave * NLA + i) * 1024);
+    }
 #pragma unroll
     for (int i = 0; i < NLB; ++i)
       lds_dma16(b_src[i] + koff, base + A_BYTES + (wave * NLB + i) * 1024);
@@ -243,14 +249,16 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   // next stage's first k step, so a CU's loads of a stage are spread over
   // two k steps.
   constexpr bool SPLIT = STAGES == 2 && !FP8;
-  auto issue_part = [&](int kt, int slot, auto part_c) {
+  auto issue_part = [&](int kt, int slot, auto part_c, auto a_on_c) {
     constexpr int PART = decltype(part_c)::value;
     const int64_t koff = static_cast<int64_t>(kt) * SK;
     uint8_t* base = lds + slot * STAGE;
     if constexpr (PART == 0) {
+      if constexpr (decltype(a_on_c)::value) {
 #pragma unroll
-      for (int i = 0; i < NLA; ++i)
-        lds_dma16(a_src[i] + koff, base + (wave * NLA + i) * 1024);
+        for (int i = 0; i < NLA; ++i)
+          lds_dma16(a_src[i] + koff, base + (wave * NLA + i) * 1024);
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < NLB; ++i)
@@ -298,17 +306,22 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
     return GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? rr : 0);
   };
 #pragma unroll
-  for (int s = 0; s < STAGES; ++s)
-    if (s < KT) issue(s, s);
+  for (int s = 0; s < STAGES; ++s) {
+    if (s >= KT) break;
+    if (a_on) issue(s, s, std::true_type{});
+    else issue(s, s, std::false_type{});
+  }
 
-  // Waits until at most `n` of this wave's later stages are in flight.
-  auto wait_stages = [&](int n) {
-    if (n >= 6) wait_vmcnt<(6 * NL < 64 ? 6 * NL : 0)>();
-    else if (n == 5) wait_vmcnt<(5 * NL < 64 ? 5 * NL : 0)>();
-    else if (n == 4) wait_vmcnt<(4 * NL < 64 ? 4 * NL : 0)>();
-    else if (n == 3) wait_vmcnt<(3 * NL < 64 ? 3 * NL : 0)>();
-    else if (n == 2) wait_vmcnt<2 * NL>();
-    else if (n == 1) wait_vmcnt<NL>();
+  // Waits until at most `n` of this wave's later stages (LPS loads each:
+  // NL, or NL - NLA without activation loads) are in flight.
+  auto wait_stages = [&](int n, auto lps_c) {
+    constexpr int LPS = decltype(lps_c)::value;
+    if (n >= 6) wait_vmcnt<(6 * LPS < 64 ? 6 * LPS : 0)>();
+    else if (n == 5) wait_vmcnt<(5 * LPS < 64 ? 5 * LPS : 0)>();
+    else if (n == 4) wait_vmcnt<(4 * LPS < 64 ? 4 * LPS : 0)>();
+    else if (n == 3) wait_vmcnt<(3 * LPS < 64 ? 3 * LPS : 0)>();
+    else if (n == 2) wait_vmcnt<2 * LPS>();
+    else if (n == 1) wait_vmcnt<LPS>();
     else wait_vmcnt<0>();
   };
   auto load_frag = [&](const uint8_t* p0, int kk) -> Frag {
@@ -351,8 +364,11 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   for (int i = 0; i < RB; ++i) nlive += first_sid[i] < p.numel ? 1 : 0;
 
   Frag fa[2][RB], fb[2][CB];
-  auto main_loop = [&](auto nlive_c) {
+  auto main_loop = [&](auto nlive_c, auto a_on_c) {
     constexpr int NLIVE = decltype(nlive_c)::value;
+    constexpr int LPS = decltype(a_on_c)::value ? NL : NL - NLA;  // loads per stage
+    const auto lps = std::integral_constant<int, LPS>{};
+    const auto aon = a_on_c;
     // fp8: each stage (one k block) accumulates into tmp, which is then
     // added to acc times the block's activation x weight scale.
     Acc tmp[FP8 ? RB : 1][FP8 ? CB : 1];
@@ -412,7 +428,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
     // the DMA of stage kt+STAGES then refills, STAGES-1 stages ahead of its
     // use. The last stage is peeled so the loop body has no branch around
     // LDS reads.
-    wait_stages(min(STAGES - 1, KT - 1));
+    wait_stages(min(STAGES - 1, KT - 1), lps);
     wave_barrier_all();
     read_frags(0, 0, fa[0], fb[0]);
     if constexpr (FP8) read_scales(0, sa_c, sw_c);
@@ -424,7 +440,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
       for (int kk = 0; kk + 1 < KK; ++kk) {
         read_frags(kt, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
         if constexpr (PREV) {
-          if (kk == 0) issue_part(kt + 1, (kt + 1) % STAGES, std::integral_constant<int, 1>{});
+          if (kk == 0)
+            issue_part(kt + 1, (kt + 1) % STAGES, std::integral_constant<int, 1>{}, aon);
         }
         mma(kk, fa[kk & 1], fb[kk & 1]);
         if (PREV && kk == 0) sched_step_dma();
@@ -432,11 +449,13 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
       wait_lgkm0();
-      wait_stages(min(STAGES - 2, KT - 2 - kt));
+      wait_stages(min(STAGES - 2, KT - 2 - kt), lps);
       wave_barrier_all();
       if (kt + STAGES < KT) {
-        if constexpr (SPLIT) issue_part(kt + STAGES, kt % STAGES, std::integral_constant<int, 0>{});
-        else issue(kt + STAGES, kt % STAGES);
+        if constexpr (SPLIT)
+          issue_part(kt + STAGES, kt % STAGES, std::integral_constant<int, 0>{}, aon);
+        else
+          issue(kt + STAGES, kt % STAGES, aon);
       }
       read_frags(kt + 1, 0, fa[KK & 1], fb[KK & 1]);
       if constexpr (FP8) read_scales(kt + 1, sa_n, sw_n);
@@ -473,7 +492,10 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
     mma(KK - 1, fa[(KK - 1) & 1], fb[(KK - 1) & 1]);
     fold();
   };
-  dispatch_count<RB>(nlive, main_loop);
+  if (a_on)
+    dispatch_count<RB>(nlive, [&](auto n) { main_loop(n, std::true_type{}); });
+  else
+    dispatch_count<RB>(nlive, [&](auto n) { main_loop(n, std::false_type{}); });
 
   // ---- epilogue: lane owns token row (lane & 31) of each 32-row block and,
   // in each 32-column block, columns 8*q + 4*(lane>>5) + {0..3}, q = 0..3

@@ -379,6 +379,8 @@ def _kernel_stage(name, after_gemm1):
         return "align"
     if "quant_" in name:
         return "quant_a2" if after_gemm1 else "quant_x"
+    if "scale_gather" in name:  # x's scales into the padded row order
+        return "quant_x"
     if "gemm2_direct" in name or "tail_fixup" in name:
         return "gemm2"
     if "moe_gemm" in name:

@@ -72,6 +72,7 @@ struct Plan {
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
   int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail, o_part,
+      o_xst,
       total;
 };
 
@@ -292,7 +293,7 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   const int64_t alg = align_scratch_bytes(numel, e);
   p.o_alg = alg > 0 ? take(alg) : -1;
   p.o_a2 = take(p.max_padded * inter * 2);
-  p.o_xq = p.o_xs = p.o_a2q = p.o_a2s = -1;
+  p.o_xq = p.o_xs = p.o_a2q = p.o_a2s = p.o_xst = -1;
   if (p.dt != kDtBf16) {
     p.o_xq = take(m * hidden * esz);
     p.o_xs = take(p.dt == kDtFp8 ? m * (hidden / 128) * 4 : m * 4);
@@ -302,6 +303,13 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   }
   p.o_y = take(p.ksplit2 > 1 ? p.ksplit2 * numel * hidden * 4 : numel * hidden * 2);
   p.o_tail = p.tail2 ? take(wide_tail_part_bytes()) : -1;
+  // fp8 on 256-row blocks: x's group scales gathered into the padded row
+  // order, k-block-major, so a GEMM1 wave reads its 64 rows' scales of a k
+  // block as one 256-byte run instead of 64 lines (measured, DeepSeek
+  // M=4096: GEMM1 2.02 -> 1.86 ms for a ~10 us gather; at M <= 512 the
+  // gather costs what it saves)
+  if (p.tiled && p.dt == kDtFp8 && p.tile_cfg == 0)
+    p.o_xst = take((hidden / 128) * p.max_padded * 4);
   p.o_part = p.fused1 ? take(static_cast<int64_t>(topk) * (inter / p.chunk1) * hidden * 4) : -1;
   p.total = o;
   *pl = p;
@@ -467,6 +475,13 @@ static int run_fused(const FusedArgs& a) {
     if (rc) return rc;
     act = ws + p.o_xq;
     act_scale = reinterpret_cast<const float*>(ws + p.o_xs);
+    if (p.o_xst >= 0) {
+      float* xst = reinterpret_cast<float*>(ws + p.o_xst);
+      rc = launch_scale_gather(act_scale, static_cast<int>(a.hidden / 128), sorted, npp, numel,
+                               a.topk, p.block_m, p.max_padded, xst, a.stream);
+      if (rc) return rc;
+      act_scale = xst;
+    }
   } else if (p.dt == kDtInt8) {
     rc = launch_quant_int8_token(a.x, reinterpret_cast<int8_t*>(ws + p.o_xq),
                                  reinterpret_cast<float*>(ws + p.o_xs), a.m,
@@ -529,6 +544,7 @@ static int run_fused(const FusedArgs& a) {
   g1.bias = a.b13;
   g1.a_rows = a.m;
   g1.num_experts = a.e;
+  g1.a_scale_kstride = p.o_xst >= 0 ? p.max_padded : 0;
   if (p.direct) {
     // slot j is row tile j; a2 holds the compact slot rows
     g1.direct_ids = a.topk_ids;
@@ -552,9 +568,11 @@ static int run_fused(const FusedArgs& a) {
   if (p.qfold) {
     // GEMM2 quantises the a2 slot rows itself
   } else if (p.dt == kDtFp8) {
+    // tiled: the scales k-block-major over the padded rows (see o_xst)
     rc = launch_quant_fp8_group(a2, ws + p.o_a2q,
                                 reinterpret_cast<float*>(ws + p.o_a2s),
-                                a2_rows, a.inter, 128, a.stream, a2_npp, a2_sorted, numel);
+                                a2_rows, a.inter, 128, a.stream, a2_npp, a2_sorted, numel,
+                                p.tiled ? p.max_padded : 0);
     if (rc) return rc;
     act2 = ws + p.o_a2q;
     act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
@@ -584,6 +602,7 @@ static int run_fused(const FusedArgs& a) {
   g2.a_rows = p.max_padded;
   g2.eid_shift = p.tiled ? p.eid_shift2 : 0;
   g2.a_src = p.qfold ? a2 : nullptr;
+  g2.a_scale_kstride = p.tiled && p.dt == kDtFp8 ? p.max_padded : 0;
   if (p.direct_sum) {
     // out = the weighted top-k sum, straight from GEMM2
     g2.out = a.out;

@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(
     const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
     float* __restrict__ scales, int64_t rows, int64_t cols, int group,
     const int32_t* __restrict__ rows_dev, const int32_t* __restrict__ sorted_ids,
-    int64_t numel) {
+    int64_t numel, int64_t scale_kstride) {
   const int lane = threadIdx.x & 63;
   const int lanes_per_group = group / 8;
   const int64_t vec_per_row = cols / 8;
@@ -221,7 +221,28 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(
   o.x = lo;
   o.y = hi;
   *reinterpret_cast<uint2*>(q + r * cols + c) = o;
-  if ((lane & (lanes_per_group - 1)) == 0) scales[r * (cols / group) + c / group] = scale;
+  if ((lane & (lanes_per_group - 1)) == 0) {
+    if (scale_kstride > 0) scales[(c / group) * scale_kstride + r] = scale;
+    else scales[r * (cols / group) + c / group] = scale;
+  }
+}
+
+// Activation scales of the padded row order, k-block-major:
+// out[kb * stride + r] = xs[sorted_ids[r] / topk][kb] for the rows below
+// num_tokens_post_padded; a pad row takes the block's first row's scales
+// (any finite value does: pad rows' outputs are never stored). One thread
+// per (padded row, k block): blockIdx.y is the k block, so each k block's
+// writes are contiguous.
+__global__ __launch_bounds__(256) void moe_scale_gather_kernel(
+    const float* __restrict__ xs, int kblocks, const int32_t* __restrict__ sorted_ids,
+    const int32_t* __restrict__ num_post_pad, int64_t numel, int topk, int block,
+    float* __restrict__ out, int64_t stride) {
+  const int64_t r = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (r >= num_post_pad[0]) return;
+  const int kb = blockIdx.y;
+  int sid = sorted_ids[r];
+  if (sid >= numel) sid = sorted_ids[r - r % block];
+  out[kb * stride + r] = xs[static_cast<int64_t>(sid / topk) * kblocks + kb];
 }
 
 // ----------------------------------------------------- int8 token quant ---
@@ -407,14 +428,27 @@ static void dispatch_nv(int n, F&& f) {
 int launch_quant_fp8_group(const void* x, void* q, float* scales,
                            int64_t rows, int64_t cols, int group,
                            hipStream_t stream, const int32_t* rows_dev,
-                           const int32_t* sorted_ids, int64_t numel) {
+                           const int32_t* sorted_ids, int64_t numel,
+                           int64_t scale_kstride) {
   const int64_t vecs = rows * (cols / 8);
   if (vecs == 0) return FGS_OK;
   hipLaunchKernelGGL(quant_fp8_group_kernel, dim3(static_cast<unsigned>((vecs + 255) / 256)),
                      dim3(256), 0, stream, static_cast<const uint16_t*>(x),
                      static_cast<uint8_t*>(q), scales, rows, cols, group, rows_dev,
-                     sorted_ids, numel);
+                     sorted_ids, numel, scale_kstride);
   return check_launch("quant_fp8_group_kernel");
+}
+
+int launch_scale_gather(const float* xs, int kblocks, const int32_t* sorted_ids,
+                        const int32_t* num_post_pad, int64_t numel, int topk, int block,
+                        int64_t max_padded, float* out, hipStream_t stream) {
+  if (max_padded <= 0 || kblocks <= 0) return FGS_OK;
+  hipLaunchKernelGGL(moe_scale_gather_kernel,
+                     dim3(static_cast<unsigned>((max_padded + 255) / 256),
+                          static_cast<unsigned>(kblocks)),
+                     dim3(256), 0, stream,
+                     xs, kblocks, sorted_ids, num_post_pad, numel, topk, block, out, max_padded);
+  return check_launch("moe_scale_gather_kernel");
 }
 
 int launch_quant_int8_token(const void* x, int8_t* q, float* scales,

@@ -52,6 +52,9 @@ struct GemmParams {
                               // slots): the bf16 activation
                               // rows ([a_rows, kdim]) the kernel quantises
                               // itself (a and a_scale unused); null: off
+  int64_t a_scale_kstride;    // tiled fp8: > 0 -> a_scale is k-block-major
+                              // over the padded rows, a_scale[kb * stride +
+                              // padded row]; 0 -> [rows][kblocks]
 };
 
 // Router gating (scores -> top-k -> renormalise), one wave per token;
@@ -103,10 +106,19 @@ int launch_moe_sum_partials(const float* part, int nsplit, void* out, int64_t m,
 // The int8 quantiser holds a row in a wave's registers up to
 // 512 * kInt8QuantMaxVec columns; wider rows take a workgroup each.
 constexpr int kInt8QuantMaxVec = 16;
+// With scale_kstride > 0 the scales are stored k-block-major:
+// scales[g * scale_kstride + row].
 int launch_quant_fp8_group(const void* x, void* q, float* scales, int64_t rows,
                            int64_t cols, int group, hipStream_t stream,
                            const int32_t* rows_dev = nullptr,
-                           const int32_t* sorted_ids = nullptr, int64_t numel = 0);
+                           const int32_t* sorted_ids = nullptr, int64_t numel = 0,
+                           int64_t scale_kstride = 0);
+// Per-token group scales xs [tokens][kblocks] -> k-block-major scales of
+// the padded row order (out[kb * max_padded + r], rows below
+// num_tokens_post_padded; a pad row gets its block's first row's scales).
+int launch_scale_gather(const float* xs, int kblocks, const int32_t* sorted_ids,
+                        const int32_t* num_post_pad, int64_t numel, int topk, int block,
+                        int64_t max_padded, float* out, hipStream_t stream);
 int launch_quant_int8_token(const void* x, int8_t* q, float* scales,
                             int64_t rows, int64_t cols, hipStream_t stream,
                             const int32_t* rows_dev = nullptr,

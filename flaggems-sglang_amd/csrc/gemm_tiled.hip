@@ -209,13 +209,25 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   // fp8 block scales of one k block, staged with the tiles: slot s < BM is
   // padded row s's activation scale, slot BM + b the tile's b-th 128-row
   // weight scale block (GEMM1: b = 0 gate, 1 up); other slots are unused.
+  // Stage kt's scale is sc_src + kt * sc_step: activation scales stored
+  // k-block-major over the padded rows (a_scale_kstride > 0; a pad row
+  // reads the tile's first row) step by the stride, so a wave's 64 rows
+  // are one contiguous 256-byte read; row-major ones and the weight scales
+  // step by one float.
   const int kblocks = static_cast<int>(p.kdim / 128);
   const float* sc_src = nullptr;
+  int64_t sc_step = 1;
   if constexpr (FP8) {
     const int slot = wave * 64 + lane;
     const int64_t wblk0 = static_cast<int64_t>(e) * (p.nrows_w / 128);
     if (slot < BM) {
-      sc_src = p.a_scale + act_row(slot) * kblocks;
+      if (p.a_scale_kstride > 0) {
+        const bool live = p.sorted_ids[row0 + slot] < p.numel;
+        sc_src = p.a_scale + row0 + (live ? slot : 0);
+        sc_step = p.a_scale_kstride;
+      } else {
+        sc_src = p.a_scale + act_row(slot) * kblocks;
+      }
     } else {
       int64_t wb = 0;
       if (slot < BM + (GEMM1 ? 2 : BNR / 128)) {
@@ -242,7 +254,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
 #pragma unroll
     for (int i = 0; i < NLB; ++i)
       lds_dma16(b_src[i] + koff, base + A_BYTES + (wave * NLB + i) * 1024);
-    if constexpr (FP8) lds_dma4(sc_src + kt, base + SC_OFF + wave * 256);
+    if constexpr (FP8) lds_dma4(sc_src + kt * sc_step, base + SC_OFF + wave * 256);
   };
   // With a two-slot ring (bf16 / int8) a freed slot's refill is split: the
   // activation rows right after the barrier, the weight rows during the
@@ -293,7 +305,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   for (int i = 0; i < NLA; ++i) a_src[i] += static_cast<int64_t>(kt0) * SK;
 #pragma unroll
   for (int i = 0; i < NLB; ++i) b_src[i] += static_cast<int64_t>(kt0) * SK;
-  if constexpr (FP8) sc_src += kt0;
+  if constexpr (FP8) sc_src += kt0 * sc_step;
   // the first token slot of each of the wave's 32-row blocks, loaded before
   // the stage loads: the counter drains in issue order, so waiting on these
   // never waits on a stage load

@@ -172,11 +172,14 @@ __global__ __launch_bounds__(256) void moe_sum_partials_kernel(
 // ------------------------------------------------------ fp8 group quant ---
 // Each lane quantises 8 consecutive columns; the group/8 lanes of a group
 // (a power of two <= 64, aligned within the wave) reduce its amax with
-// butterfly shuffles, so a wave covers 512 columns.
+// butterfly shuffles, so a wave covers 512 columns. A workgroup takes
+// 2048 columns of one row (grid: rows x column chunks), so the row and its
+// skip test are uniform and no index is divided.
 // scale = max(amax, 1e-10) / 448; q = e4m3fn(clamp(x / scale, +-448)).
 // With `rows_dev` given, rows >= *rows_dev are skipped (padded-row buffers
 // whose live prefix is only known on the device); with `sorted_ids` given,
 // so are the pad rows (sorted_ids[r] >= numel), which no GEMM reads.
+constexpr int kQuantChunkCols = 256 * 8;  // columns per workgroup
 __global__ __launch_bounds__(256) void quant_fp8_group_kernel(
     const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
     float* __restrict__ scales, int64_t rows, int64_t cols, int group,
@@ -184,12 +187,13 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(
     int64_t numel, int64_t scale_kstride) {
   const int lane = threadIdx.x & 63;
   const int lanes_per_group = group / 8;
-  const int64_t vec_per_row = cols / 8;
-  const int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  const int64_t r = v / vec_per_row;
+  const int64_t r = blockIdx.x;
   const int64_t live_rows = rows_dev ? min(rows, static_cast<int64_t>(*rows_dev)) : rows;
-  const bool active = r < live_rows && (!sorted_ids || sorted_ids[r] < numel);
-  const int64_t c = (v - r * vec_per_row) * 8;
+  if (r >= live_rows) return;
+  if (sorted_ids && sorted_ids[r] >= numel) return;
+  const int64_t c = (static_cast<int64_t>(blockIdx.y) * kQuantChunkCols) + threadIdx.x * 8;
+  // a group lies wholly inside or outside the row (cols % group == 0)
+  const bool active = c < cols;
   float f[8];
   float amax = 0.f;
   if (active) {
@@ -222,8 +226,10 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(
   o.y = hi;
   *reinterpret_cast<uint2*>(q + r * cols + c) = o;
   if ((lane & (lanes_per_group - 1)) == 0) {
-    if (scale_kstride > 0) scales[(c / group) * scale_kstride + r] = scale;
-    else scales[r * (cols / group) + c / group] = scale;
+    const int gshift = __builtin_ctz(group);  // group is a power of two
+    const int64_t g = c >> gshift;
+    if (scale_kstride > 0) scales[g * scale_kstride + r] = scale;
+    else scales[r * (cols >> gshift) + g] = scale;
   }
 }
 
@@ -430,9 +436,12 @@ int launch_quant_fp8_group(const void* x, void* q, float* scales,
                            hipStream_t stream, const int32_t* rows_dev,
                            const int32_t* sorted_ids, int64_t numel,
                            int64_t scale_kstride) {
-  const int64_t vecs = rows * (cols / 8);
-  if (vecs == 0) return FGS_OK;
-  hipLaunchKernelGGL(quant_fp8_group_kernel, dim3(static_cast<unsigned>((vecs + 255) / 256)),
+  if (rows == 0 || cols == 0) return FGS_OK;
+  const int64_t chunks = (cols + kQuantChunkCols - 1) / kQuantChunkCols;
+  if (rows > 0x7fffffff || chunks > 0xffff)
+    return fail(FGS_EUNSUPPORTED, "fp8 group quantiser: too many rows or columns for its grid");
+  hipLaunchKernelGGL(quant_fp8_group_kernel,
+                     dim3(static_cast<unsigned>(rows), static_cast<unsigned>(chunks)),
                      dim3(256), 0, stream, static_cast<const uint16_t*>(x),
                      static_cast<uint8_t*>(q), scales, rows, cols, group, rows_dev,
                      sorted_ids, numel, scale_kstride);

@@ -5,10 +5,11 @@
 // order from moe_align_block_size) and one 16-column output tile. Its KW
 // waves split the contraction; each wave streams its share of the 16 (or,
 // for GEMM1, 16 gate + 16 up) weight rows straight from HBM into MFMA
-// operand registers, with no LDS staging: per step the four lane groups of
-// a row cover 4*LB contiguous bytes, 64 contiguous bytes per load
-// instruction. The MFMA k index is only a label, so activations are read
-// with the identical lane -> k mapping and the contraction is exact. Partial sums meet in LDS; wave 0 runs the epilogue:
+// operand registers, with no LDS staging. Every weight load instruction
+// reads 8 rows x 128 contiguous bytes (whole lines; a 16-rows x 64-byte
+// pattern streams ~20 % slower), and two DPP moves per dword between the
+// halves of each 16-lane row put row n's bytes into the lanes of MFMA row
+// n (lines_to_frag). Partial sums meet in LDS; wave 0 runs the epilogue:
 //   GEMM1 (replaces matmul_ogs with gather + _silu_and_mul_triton,
 //          ops/fused_moe.py:205-218): a2[row, c] = bf16(silu(g) * u)
 //   GEMM2 (replaces matmul_ogs with scatter + gammas, :224-231):
@@ -51,30 +52,54 @@ struct StreamTraits<kDtInt8> {
   typedef i32x4 Acc;
 };
 
-// Lane (n, g) of a step reads 16-byte vector v at byte v*64 + g*16 of its
-// row's step segment: the four lane groups of a row read 64 contiguous
-// bytes per load instruction (whole 64-byte segments for the memory
-// pipeline), and the MFMA k order is the same permutation for weights and
-// activations.
+// Weight rows arrive as whole 128-byte lines. For each 128-byte group q of
+// a step, f[2q] is loaded from row (lane & 7) of the 16-row tile and
+// f[2q + 1] from row 8 + (lane & 7), both at byte (lane >> 3) * 16 of the
+// group: one load instruction covers 8 rows x 128 contiguous bytes. `p` is
+// this lane's row (lane & 7) at its byte of the step, `row8` the byte
+// distance of 8 rows.
 template <int DT, int NV>
-__device__ __forceinline__ void load_frag(u32x4 (&f)[NV], const uint8_t* p,
-                                          bool valid) {
-  if (valid) {
+__device__ __forceinline__ void load_lines(u32x4 (&f)[NV], const uint8_t* p, int64_t row8) {
 #pragma unroll
-    for (int v = 0; v < NV; ++v)
-      f[v] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + v * 64));
-  } else {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) f[v] = u32x4{0, 0, 0, 0};
+  for (int q = 0; q < NV / 2; ++q) {
+    f[2 * q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + q * 128));
+    f[2 * q + 1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + row8 + q * 128));
   }
 }
 
+// Lines -> MFMA fragments. In each 16-lane row, lane n < 8 holds row n's
+// 16-byte chunk 2g of the group (g = lane >> 4) in f[2q] and row n + 8's
+// chunk 2g in f[2q + 1]; lane n >= 8 holds row n - 8's chunk 2g + 1 and
+// row n's chunk 2g + 1. row_ror:8 pairs lane n with n +- 8, and the bank
+// masks write only the half that receives: lanes 8-15 take f[2q + 1] of
+// lane n - 8 into f[2q], lanes 0-7 take f[2q] of lane n + 8 into f[2q + 1].
+// Then lane (n, g) holds row n's bytes 32g .. 32g + 31 of the group in
+// f[2q], f[2q + 1]: the MFMA k index of a lane is the same in every row, so
+// activations read with that mapping (read_act_vec) make the contraction
+// exact.
 template <int NV>
-__device__ __forceinline__ void load_act(u32x4 (&f)[NV], const uint8_t* p,
+__device__ __forceinline__ void lines_to_frag(u32x4 (&f)[NV]) {
+#pragma unroll
+  for (int q = 0; q < NV / 2; ++q)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int a = static_cast<int>(f[2 * q][d]), b = static_cast<int>(f[2 * q + 1][d]);
+      f[2 * q][d] = static_cast<unsigned>(__builtin_amdgcn_update_dpp(a, b, 0x128, 0xF, 0xC, false));
+      f[2 * q + 1][d] = static_cast<unsigned>(__builtin_amdgcn_update_dpp(b, a, 0x128, 0xF, 0x3, false));
+    }
+}
+
+// Byte of an operand vector v within a step for lane group g: group v / 2,
+// chunk 2g + v % 2 (the weight fragments' k mapping).
+__device__ __forceinline__ int frag_byte(int v, int g) { return (v >> 1) * 128 + g * 32 + (v & 1) * 16; }
+
+// Activation fragments (p: the row at this lane's step; lane group g).
+template <int NV>
+__device__ __forceinline__ void load_act(u32x4 (&f)[NV], const uint8_t* p, int g,
                                          bool valid) {
   if (valid) {
 #pragma unroll
-    for (int v = 0; v < NV; ++v) f[v] = *reinterpret_cast<const u32x4*>(p + v * 64);
+    for (int v = 0; v < NV; ++v) f[v] = *reinterpret_cast<const u32x4*>(p + frag_byte(v, g));
   } else {
 #pragma unroll
     for (int v = 0; v < NV; ++v) f[v] = u32x4{0, 0, 0, 0};
@@ -124,7 +149,7 @@ __device__ __forceinline__ f32x4 mma_fp8(const u32x4 (&a)[2],
 //
 // Every lane quantises 2 consecutive values of the step (one 128-column
 // group) and the bytes go through the wave's LDS slot to lanes (0, lg),
-// whose MFMA row 0 fragments hold the step's 16-byte vectors v*64 + lg*16.
+// whose MFMA row 0 fragments hold the step's bytes 32*lg .. 32*lg + 31.
 __device__ __forceinline__ uint32_t load_raw(const uint16_t* row, int64_t k0, int lane) {
   return *reinterpret_cast<const uint32_t*>(row + k0 + lane * 2);
 }
@@ -135,15 +160,36 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float quant1_fp8(float f, float scale) {
   return fminf(fmaxf(f / scale, -448.f), 448.f);
 }
-// fp8 step: the group amax by butterfly over the wave, scale =
-// max(amax, 1e-10) / 448 (returned, the same in every lane); qb is the
-// wave's 128-byte LDS slot.
+// One DPP lane move within each row of 16 lanes (CTRL: a quad permutation
+// or a row mirror; every source lane exists, so no lane keeps `old`).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// Max over the wave, in every lane: quad xor 1 and xor 2, then the row's
+// half mirror (max over 8 lanes) and mirror (over 16), then the four rows'
+// lanes 0, 16, 32, 48 -- VALU lane moves and readlanes instead of six LDS
+// permute round trips. max is exact in any order, so the result is the
+// butterfly's bit for bit.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+  const int b = __float_as_int(v);
+  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 0)),
+                     __int_as_float(__builtin_amdgcn_readlane(b, 16))),
+               fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 32)),
+                     __int_as_float(__builtin_amdgcn_readlane(b, 48))));
+}
+
+// fp8 step: the group amax over the wave, scale = max(amax, 1e-10) / 448
+// (returned, the same in every lane); qb is the wave's 128-byte LDS slot.
 __device__ __forceinline__ float quant_step_fp8(uint32_t raw, uint8_t* qb, int lane,
                                                u32x4 (&f)[2]) {
   const float a = bf16_lo(raw), b = bf16_hi(raw);
-  float amax = fmaxf(fabsf(a), fabsf(b));
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  const float amax = wave_max(fmaxf(fabsf(a), fabsf(b)));
   const float scale = fmaxf(amax, 1e-10f) / 448.0f;
   reinterpret_cast<uint16_t*>(qb)[lane] =
       static_cast<uint16_t>(cvt_pk_fp8(quant1_fp8(a, scale), quant1_fp8(b, scale)));
@@ -151,7 +197,7 @@ __device__ __forceinline__ float quant_step_fp8(uint32_t raw, uint8_t* qb, int l
   const bool row0 = (lane & 15) == 0;
 #pragma unroll
   for (int v = 0; v < 2; ++v)
-    f[v] = row0 ? *reinterpret_cast<const u32x4*>(qb + v * 64 + lg * 16) : u32x4{0, 0, 0, 0};
+    f[v] = row0 ? *reinterpret_cast<const u32x4*>(qb + frag_byte(v, lg)) : u32x4{0, 0, 0, 0};
   return scale;
 }
 
@@ -204,15 +250,16 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
     const int sid = row_sid(r);
     avalid[mt] = sid < p.numel;
     const int64_t src = avalid[mt] ? src_row(r, sid) : 0;
-    arow[mt] = p.a + (src * p.kdim) * ESZ + lg * 16;
+    arow[mt] = p.a + (src * p.kdim) * ESZ;
   }
-  // Weight rows of lane ln.
+  // Weight row (lane & 7) of each row group at this lane's line byte.
   const uint8_t* brow[NB];
   const int64_t wbase = static_cast<int64_t>(e) * p.nrows_w;
+  const int64_t row8 = 8 * p.kdim * ESZ;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int64_t n = wbase + (nb ? p.n_out : 0) + n0 + ln;
-    brow[nb] = p.w + (n * p.kdim) * ESZ + lg * 16;
+    const int64_t n = wbase + (nb ? p.n_out : 0) + n0 + (lane & 7);
+    brow[nb] = p.w + (n * p.kdim) * ESZ + (lane >> 3) * 16;
   }
 
   // QA: the direct row's bf16 source (the token for GEMM1, slot rb's a2 row
@@ -275,13 +322,13 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
     } else {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        load_act(af[buf][mt], arow[mt] + st * step_bytes, avalid[mt]);
+        load_act(af[buf][mt], arow[mt] + st * step_bytes, lg, avalid[mt]);
     }
   };
   if (s0 < s1) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
-      load_frag<DT>(bf[0][nb], brow[nb] + s0 * step_bytes, true);
+      load_lines<DT>(bf[0][nb], brow[nb] + s0 * step_bytes, row8);
     load_a(0, s0);
     load_scales(0, s0);
   }
@@ -295,7 +342,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
       if (nxt < s1) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
-          load_frag<DT>(bf[h ^ 1][nb], brow[nb] + nxt * step_bytes, true);
+          load_lines<DT>(bf[h ^ 1][nb], brow[nb] + nxt * step_bytes, row8);
         load_a(h ^ 1, nxt);
         load_scales(h ^ 1, nxt);
       }
@@ -304,6 +351,8 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) sa[h][0][i] = cvalid[0][i] ? sc : 0.f;
       }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) lines_to_frag(bf[h][nb]);
       if constexpr (DT == kDtBf16) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
@@ -482,9 +531,10 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
     const int e = p.direct_ids[j];
     if (e < 0 || e >= p.num_experts) continue;
     const float gamma = p.weight_on_input ? 1.f : p.topk_w[j];
-    const uint8_t* brow =
-        p.w + ((static_cast<int64_t>(e) * p.nrows_w + col) * p.kdim) * ESZ + lg * 16;
-    const uint8_t* arow = p.a + (static_cast<int64_t>(j) * p.kdim) * ESZ + lg * 16;
+    const uint8_t* brow = p.w + ((static_cast<int64_t>(e) * p.nrows_w + n0 + (lane & 7)) *
+                                 p.kdim) * ESZ + (lane >> 3) * 16;
+    const int64_t row8 = 8 * p.kdim * ESZ;
+    const uint8_t* arow = p.a + (static_cast<int64_t>(j) * p.kdim) * ESZ;
     const bool avalid = ln == 0;  // activation row 0 is the slot's row
     const float* wsc = DT == kDtFp8
                            ? p.w_scale + (static_cast<int64_t>(e) * (p.nrows_w / 128) +
@@ -496,12 +546,12 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
     const uint16_t* qrow = QA ? p.a_src + static_cast<int64_t>(j) * p.kdim : nullptr;
     float sc[2];  // fp8: activation x weight block scale of the step (QA: weight)
     auto load = [&](int buf, int st) {
-      load_frag<DT>(bf[buf], brow + st * step_bytes, true);
+      load_lines<DT>(bf[buf], brow + st * step_bytes, row8);
       if constexpr (QA) {
         ar[buf] = load_raw(qrow, static_cast<int64_t>(st) * T::kStepK, lane);
         if constexpr (DT == kDtFp8) sc[buf] = wsc[st];
       } else {
-        load_act(af[buf], arow + st * step_bytes, avalid);
+        load_act(af[buf], arow + st * step_bytes, lg, avalid);
         if constexpr (DT == kDtFp8) sc[buf] = p.a_scale[j * kblocks + st] * wsc[st];
       }
     };
@@ -512,6 +562,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
         const int cur = s + h;
         if (cur >= s1) break;
         if (cur + 1 < s1) load(h ^ 1, cur + 1);
+        lines_to_frag(bf[h]);
         if constexpr (DT == kDtBf16) {
           mma_step<DT>(acc, af[h], bf[h]);
         } else if constexpr (DT == kDtInt8) {

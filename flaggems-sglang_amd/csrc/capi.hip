@@ -179,14 +179,17 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   p.block_m = 16 * p.mt;
   // LDS-tiled kernels (deep DMA pipeline) or the streaming kernels (weights
   // straight into registers), by the rows per expert at which the tiled
-  // kernels' pipeline fill pays off, measured per contraction length
-  // (kmin: the shorter of the two GEMMs' k rows in bytes):
-  // * fp8 from two tokens (its streaming steps carry 32 bytes per lane:
-  //   DeepSeek M=2..16 tiled -2..-12 %);
-  // * a short k row (< 2 KiB, Qwen3) from 12 rows per expert (streaming
-  //   -14 % at 2 rows, -3 % at 8);
-  // * a long one (>= 8 KiB, Mixtral) from half a row (-2..-4 % at M=2, 3);
-  // * else (Qwen2 int8) from one row (streaming -30 % at a quarter row).
+  // kernels' pipeline fill pays off, measured per element type and
+  // contraction length (kmin: the shorter of the two GEMMs' k rows in
+  // bytes), both schedules forced on the same box:
+  // * fp8 from 1.5 rows per expert (DeepSeek: streaming -3..-12 % at
+  //   M=2..32, level at 48, tiled -5 % at 64, -12 % at 128);
+  // * a short k row (< 2 KiB, Qwen3) from 12 (streaming -13 % at 8 rows,
+  //   tiled -2 % at 12);
+  // * a long one (>= 8 KiB, Mixtral) from 8 (streaming -3..-15 % at
+  //   M=2..24, level at 32, tiled -14 % at 48);
+  // * else (Qwen2 int8) from 4 (streaming -8..-21 % at 1-2 rows, level at
+  //   4, tiled -12 % at 8).
   // One token always streams (its direct-row schedule); shapes the tiled
   // kernels do not cover always stream.
   const int64_t esz = p.dt == kDtBf16 ? 2 : 1;
@@ -194,10 +197,11 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
                         hidden % tiled_n_align(false) == 0;
   const int forced_cfg = ((flags & FGS_FLAG_TILE_MASK) >> 12) - 1;
   const int64_t kmin = std::min(hidden, inter) * esz;
-  double tiled_from = 1.0;
-  if (kmin < 2048) tiled_from = 12.0;
-  else if (kmin >= 8192) tiled_from = 0.5;
-  const bool many_rows = m >= 2 && (p.dt == kDtFp8 || rows_per_expert >= tiled_from);
+  double tiled_from = 4.0;
+  if (p.dt == kDtFp8) tiled_from = 1.5;
+  else if (kmin < 2048) tiled_from = 12.0;
+  else if (kmin >= 8192) tiled_from = 8.0;
+  const bool many_rows = m >= 2 && rows_per_expert >= tiled_from;
   p.tiled = tiled_ok && !(flags & FGS_FLAG_FORCE_DECODE) &&
             ((flags & FGS_FLAG_FORCE_PREFILL) || forced_cfg >= 0 || many_rows);
   p.ksplit2 = 1;
@@ -242,10 +246,9 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // spans enough column tiles (one workgroup each) to fill the chip.
   const int dc = direct_choice();
   p.direct = !p.tiled && m == 1 && dc != 0;
-  // (measured, 3 x 100 flushed calls: folding wins for bf16 / int8 from 192
-  // column tiles -- Qwen2 int8 -6.5 %, Mixtral -2 % -- and loses for Qwen3's
-  // 128 tiles, +1.5 %, and for fp8, whose per-step block scales keep the
-  // unfolded GEMM2 + moe_sum ahead, +3 %)
+  // (measured, 3 x 20 flushed calls, twice: folding wins from 192 column
+  // tiles -- Qwen2 int8 -8 %, Mixtral -1.5 %, DeepSeek fp8 -0.8 % -- and
+  // loses for Qwen3's 128 tiles, +3 %)
   // One fp8 token: the GEMMs quantise their activation rows (x, the GEMM1
   // output) themselves, with the group quantiser's arithmetic. Measured
   // (DeepSeek fp8 M=1, 3 x 50 flushed calls): 88.4 -> 83.0 us. int8's
@@ -258,7 +261,7 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   p.qfold1 = p.qfold;
   p.direct_sum = p.direct && !(flags & FGS_FLAG_SEPARATE_SUM) &&
                  ((flags & FGS_FLAG_FOLD_SUM) || dc == 3 ||
-                  (dc == 1 && p.dt != kDtFp8 && hidden / 16 >= 192));
+                  (dc == 1 && hidden / 16 >= 192));
   // One bf16 token: GEMM1, the activation and GEMM2 in one launch per
   // (slot, chunk of intermediate columns), then an ordered reduction (the
   // schedule flags that pick the unfused sum keep the direct kernels).

@@ -2,7 +2,8 @@
 // expert, the layer is bound by reading every touched expert's weights once).
 //
 // A workgroup owns one row block (16*MT rows of the expert-sorted, padded
-// order from moe_align_block_size) and one 16-column output tile. Its KW
+// order from moe_align_block_size) and one 16-column output tile (grid x:
+// the column tiles, y: the row blocks). Its KW
 // waves split the contraction; each wave streams its share of the 16 (or,
 // for GEMM1, 16 gate + 16 up) weight rows straight from HBM into MFMA
 // operand registers, with no LDS staging. Every weight load instruction
@@ -212,8 +213,11 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
   constexpr int BM = 16 * MT;
   static_assert(!DIRECT || MT == 1, "direct rows: one slot per row tile");
 
-  const int rb = blockIdx.x;
-  const int n0 = blockIdx.y * 16;
+  // column tile fastest: the resident workgroups stream neighbouring tiles
+  // of a few experts (measured: Qwen2 int8 M=8 356 -> 216 us, Mixtral M=8
+  // -15 %, where row-block-fastest had dozens of experts read at one offset)
+  const int rb = blockIdx.y;
+  const int n0 = blockIdx.x * 16;
   int e;
   if constexpr (DIRECT) {
     if (rb >= p.numel) return;
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 
 template <int DT, int MT, int KW, bool GEMM1, bool DIRECT, bool QA = false>
 static int launch_one(const GemmParams& p, int row_blocks, hipStream_t stream) {
-  dim3 grid(row_blocks, static_cast<unsigned>(p.n_out / 16));
+  dim3 grid(static_cast<unsigned>(p.n_out / 16), row_blocks);
   hipLaunchKernelGGL((moe_gemm_stream_kernel<DT, MT, KW, GEMM1, DIRECT, QA>), grid,
                      dim3(KW * 64), 0, stream, p);
   return check_launch("moe_gemm_stream_kernel");
@@ -659,6 +663,8 @@ int stream_step_k(int dt) {
 int launch_gemm_stream(int dt, bool gemm1, const GemmParams& p, int mt, int kw,
                        int row_blocks, hipStream_t stream) {
   if (row_blocks <= 0) return FGS_OK;
+  if (row_blocks > 65535)
+    return fail(FGS_EUNSUPPORTED, "stream GEMM: more than 65535 row blocks (grid y)");
   switch (dt) {
     case kDtBf16:
       return gemm1 ? dispatch_kw<kDtBf16, true>(p, mt, kw, row_blocks, stream)

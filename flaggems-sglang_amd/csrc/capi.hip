@@ -66,8 +66,8 @@ struct Plan {
   bool fused1;     // one token, bf16: both GEMMs in one launch (decode.hip)
                    // plus the ordered reduction
   int chunk1;      // its intermediate columns per workgroup
-  bool qfold1;     // one token, fp8: GEMM1 quantises x itself
-  bool qfold;      // one token, fp8: GEMM2 quantises the GEMM1 output rows
+  bool qfold1;     // one token, fp8 / int8: GEMM1 quantises x itself
+  bool qfold;      // one token, fp8 / int8: GEMM2 quantises the GEMM1 output rows
                    // itself (no quantiser launch between the GEMMs)
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
@@ -151,20 +151,25 @@ static int fused1_choice() {
   return f;
 }
 
-// FGS_MOE_QFOLD (0 off, 1 default) switches the single-token GEMMs'
-// on-the-fly activation quantisation (a tuning aid; read once).
+// FGS_MOE_QFOLD switches the single-token GEMMs' on-the-fly activation
+// quantisation: 0 off, 1 default, and for int8 2 x only (GEMM1), 3 the GEMM1
+// output rows only (GEMM2), 4 both (a tuning aid; read once).
 static int qfold_choice() {
   static const int q = [] {
     const char* v = getenv("FGS_MOE_QFOLD");
-    return v && atoi(v) == 0 ? 0 : 1;
+    if (!v) return 1;
+    const int c = atoi(v);
+    return c >= 0 && c <= 4 ? c : 1;
   }();
   return q;
 }
 
-static int pick_kw(int64_t kdim, int step, int cap) {
+// Waves splitting a streaming GEMM's contraction: the most (a power of two
+// up to cap) that leave each wave at least min_steps k steps.
+static int pick_kw(int64_t kdim, int step, int cap, int min_steps) {
   const int64_t steps = kdim / step;
   int kw = 1;
-  while (kw * 2 <= cap && kw * 2 <= steps) kw *= 2;
+  while (kw * 2 <= cap && steps / (kw * 2) >= min_steps) kw *= 2;
   return kw;
 }
 
@@ -182,14 +187,14 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // kernels' pipeline fill pays off, measured per element type and
   // contraction length (kmin: the shorter of the two GEMMs' k rows in
   // bytes), both schedules forced on the same box:
-  // * fp8 from 1.5 rows per expert (DeepSeek: streaming -3..-12 % at
-  //   M=2..32, level at 48, tiled -5 % at 64, -12 % at 128);
-  // * a short k row (< 2 KiB, Qwen3) from 12 (streaming -13 % at 8 rows,
-  //   tiled -2 % at 12);
-  // * a long one (>= 8 KiB, Mixtral) from 8 (streaming -3..-15 % at
-  //   M=2..24, level at 32, tiled -14 % at 48);
-  // * else (Qwen2 int8) from 4 (streaming -8..-21 % at 1-2 rows, level at
-  //   4, tiled -12 % at 8).
+  // * fp8 from 3 rows per expert (DeepSeek: streaming -6 % at 2 rows,
+  //   level at 3, tiled -1 % at 4);
+  // * a short k row (< 2 KiB, Qwen3) from 16 (streaming -10 % at 12 rows,
+  //   +4 % with skewed routing; tiled -9 % at 16);
+  // * a long one (>= 8 KiB, Mixtral) from 12 (streaming -9 % at 8 rows,
+  //   tiled -6 % at 12);
+  // * else (Qwen2 int8) from 8 (streaming -11 % at 6 rows, level at 8,
+  //   tiled -8 % at 12).
   // One token always streams (its direct-row schedule); shapes the tiled
   // kernels do not cover always stream.
   const int64_t esz = p.dt == kDtBf16 ? 2 : 1;
@@ -197,10 +202,10 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
                         hidden % tiled_n_align(false) == 0;
   const int forced_cfg = ((flags & FGS_FLAG_TILE_MASK) >> 12) - 1;
   const int64_t kmin = std::min(hidden, inter) * esz;
-  double tiled_from = 4.0;
-  if (p.dt == kDtFp8) tiled_from = 1.5;
-  else if (kmin < 2048) tiled_from = 12.0;
-  else if (kmin >= 8192) tiled_from = 8.0;
+  double tiled_from = 8.0;
+  if (p.dt == kDtFp8) tiled_from = 3.0;
+  else if (kmin < 2048) tiled_from = 16.0;
+  else if (kmin >= 8192) tiled_from = 12.0;
   const bool many_rows = m >= 2 && rows_per_expert >= tiled_from;
   p.tiled = tiled_ok && !(flags & FGS_FLAG_FORCE_DECODE) &&
             ((flags & FGS_FLAG_FORCE_PREFILL) || forced_cfg >= 0 || many_rows);
@@ -238,8 +243,14 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
     if (p.tail2) p.ksplit2 = 1;
   }
   const int step = stream_step_k(p.dt);
-  p.kw1 = pick_kw(hidden, step, 4);
-  p.kw2 = pick_kw(inter, step, 8);
+  // GEMM1 on up to 4 waves; GEMM2 on as many as leave each wave 5 steps,
+  // at least 2. Measured (same box, 3 x 20 flushed calls, twice): GEMM2 on
+  // 2 waves instead of 8 -- Qwen2 int8 M=16 -13 %, DeepSeek fp8 M=8 -10 %,
+  // Qwen3 M=16 -2.5 % (2 to 16 steps per wave); Mixtral's 112 steps level
+  // at 4 and 8; GEMM1 on 2 or 1 waves is slower for Mixtral and Qwen3.
+  p.kw1 = pick_kw(hidden, step, 4, 1);
+  const int steps2 = static_cast<int>(inter / step);
+  p.kw2 = std::max(std::min(2, steps2), pick_kw(inter, step, 8, 5));
   // One token: its top-k slots go to distinct experts, so the streaming
   // GEMMs take slot j as row tile j (expert topk_ids[j]) and the alignment
   // is skipped; GEMM2 also folds the weighted top-k sum when the output
@@ -253,12 +264,19 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // output) themselves, with the group quantiser's arithmetic. Measured
   // (DeepSeek fp8 M=1, 3 x 50 flushed calls): 88.4 -> 83.0 us. int8's
   // per-token scale needs each row's amax before any of it is quantised:
-  // done in the GEMMs (every workgroup reducing the whole row first) it cost
-  // what the quantiser launches cost (Qwen2 int8 M=1: 63.5 -> 63.8 us with
-  // the GEMM2 rows, +5.6 us with x in GEMM1), so int8 keeps the quantisers.
-  p.qfold = p.direct && p.dt == kDtFp8 && qfold_choice() && topk <= kQaMaxSlots &&
-            !(flags & FGS_FLAG_SEPARATE_QUANT);
-  p.qfold1 = p.qfold;
+  // every wave reduces its row first (after issuing its first weight loads).
+  // Measured (Qwen2 int8 M=1, 3 x 50 flushed calls, twice): 54.2 us with
+  // both quantisers, 52.7 with GEMM2 quantising the GEMM1 output rows, 56.2
+  // with GEMM1 quantising x (its 1280 workgroups each reduce the row), 54.4
+  // with both -- so int8 folds the GEMM2 side only.
+  const int qc = qfold_choice();
+  const bool qa_ok = p.direct && topk <= kQaMaxSlots && !(flags & FGS_FLAG_SEPARATE_QUANT);
+  if (p.dt == kDtFp8) {
+    p.qfold = p.qfold1 = qa_ok && qc != 0;
+  } else if (p.dt == kDtInt8) {
+    p.qfold1 = qa_ok && (qc == 2 || qc == 4);
+    p.qfold = qa_ok && (qc == 1 || qc == 3 || qc == 4);
+  }
   p.direct_sum = p.direct && !(flags & FGS_FLAG_SEPARATE_SUM) &&
                  ((flags & FGS_FLAG_FOLD_SUM) || dc == 3 ||
                   (dc == 1 && hidden / 16 >= 192));
@@ -846,7 +864,8 @@ int32_t fgs_moe_schedule(int64_t m, int64_t hidden, int64_t inter, int32_t num_e
     s = "fused1 chunk=" + std::to_string(p.chunk1);
   } else if (p.direct) {
     s = p.direct_sum ? "direct_sum" : "direct";
-    if (p.qfold) s += " qfold";
+    if (p.qfold || p.qfold1)
+      s += p.qfold && p.qfold1 ? " qfold" : p.qfold1 ? " qfold_x" : " qfold_a2";
   } else if (!p.tiled) {
     s = "stream mt=" + std::to_string(p.mt);
   } else {

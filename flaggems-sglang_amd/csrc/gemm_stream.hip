@@ -140,13 +140,14 @@ __device__ __forceinline__ f32x4 mma_fp8(const u32x4 (&a)[2],
   return mfma16_fp8(av, bv, f32x4{0.f, 0.f, 0.f, 0.f});
 }
 
-// ---- on-the-fly activation quantisation (direct rows, fp8) ----
+// ---- on-the-fly activation quantisation (direct rows, fp8 / int8) ----
 // With p.a_src set, a direct-row fp8 kernel reads its activation row in bf16
 // and quantises it itself, with the arithmetic of quant_fp8_group_kernel
 // (per 128-column group, scale = max(amax, 1e-10) / 448, q =
 // e4m3fn(clamp(x / scale, +-448))), so the bytes and scales match that
 // kernel's output exactly and the quantiser launches drop out of the
-// single-token path.
+// single-token path; int8 likewise with quant_int8_token_kernel's
+// per-token arithmetic (below).
 //
 // Every lane quantises 2 consecutive values of the step (one 128-column
 // group) and the bytes go through the wave's LDS slot to lanes (0, lg),
@@ -201,6 +202,56 @@ __device__ __forceinline__ float quant_step_fp8(uint32_t raw, uint8_t* qb, int l
     f[v] = row0 ? *reinterpret_cast<const u32x4*>(qb + frag_byte(v, lg)) : u32x4{0, 0, 0, 0};
   return scale;
 }
+
+// int8 (one token, per-token scale like quant_int8_token_kernel): every
+// wave reduces the whole bf16 row's amax itself (16 bytes per lane per
+// 1 KiB of row), scale = max(amax, 1e-10) / 127, then per 256-column step
+// each lane quantises 4 consecutive values, rint(x / scale) clamped to
+// +-127, and the bytes reach the row-0 lanes through the wave's 256-byte
+// LDS slot.
+__device__ __forceinline__ float row_scale_int8(const uint16_t* row, int64_t cols, int lane) {
+  float m = 0.f;
+  for (int64_t c = lane * 8; c < cols; c += 512) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(row + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
+  }
+  return fmaxf(wave_max(m), 1e-10f) / 127.0f;
+}
+
+__device__ __forceinline__ uint32_t quant1_int8(float f, float scale) {
+  const float r = fminf(fmaxf(__builtin_rintf(f / scale), -127.f), 127.f);
+  return static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
+}
+
+__device__ __forceinline__ void quant_step_int8(uint2 raw, float scale, uint8_t* qb, int lane,
+                                                u32x4 (&f)[4]) {
+  reinterpret_cast<uint32_t*>(qb)[lane] =
+      quant1_int8(bf16_lo(raw.x), scale) | quant1_int8(bf16_hi(raw.x), scale) << 8 |
+      quant1_int8(bf16_lo(raw.y), scale) << 16 | quant1_int8(bf16_hi(raw.y), scale) << 24;
+  const int lg = lane >> 4;
+  const bool row0 = (lane & 15) == 0;
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    f[v] = row0 ? *reinterpret_cast<const u32x4*>(qb + frag_byte(v, lg)) : u32x4{0, 0, 0, 0};
+}
+
+// This lane's raw bf16 values of a step: 2 (fp8, 128 columns) or 4 (int8,
+// 256 columns) consecutive ones.
+template <int DT>
+struct QaRaw {
+  typedef uint32_t type;
+  static __device__ __forceinline__ uint32_t load(const uint16_t* row, int64_t k0, int lane) {
+    return load_raw(row, k0, lane);
+  }
+};
+template <>
+struct QaRaw<kDtInt8> {
+  typedef uint2 type;
+  static __device__ __forceinline__ uint2 load(const uint16_t* row, int64_t k0, int lane) {
+    return *reinterpret_cast<const uint2*>(row + k0 + lane * 4);
+  }
+};
 
 template <int DT, int MT, int KW, bool GEMM1, bool DIRECT, bool QA>
 __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
@@ -268,10 +319,10 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 
   // QA: the direct row's bf16 source (the token for GEMM1, slot rb's a2 row
   // for GEMM2), quantised step by step below
-  static_assert(!QA || (DIRECT && MT == 1 && DT == kDtFp8), "on-the-fly quantisation");
+  static_assert(!QA || (DIRECT && MT == 1 && DT != kDtBf16), "on-the-fly quantisation");
   const uint16_t* qrow = nullptr;
   if constexpr (QA) qrow = p.a_src + src_row(rb * BM, rb) * p.kdim;
-  __shared__ __attribute__((aligned(16))) uint8_t qlds[QA ? KW : 1][128];
+  __shared__ __attribute__((aligned(16))) uint8_t qlds[QA ? KW : 1][T::kStepK];
 
   // fp8 / int8 activation scales of this lane's accumulator rows.
   int64_t crow[MT][4];
@@ -300,7 +351,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
 
   u32x4 bf[2][NB][NV];
   u32x4 af[2][MT][NV];
-  uint32_t ar[2];  // QA: this lane's two raw bf16 values of the direct row's step
+  typename QaRaw<DT>::type ar[2];  // QA: this lane's raw bf16 values of the step
   // fp8 block scales of a step (one 128-k group), fetched with its operands
   float sw[2][NB], sa[2][MT][4];
   auto load_scales = [&](int buf, int kb) {
@@ -322,7 +373,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
   };
   auto load_a = [&](int buf, int st) {
     if constexpr (QA) {
-      ar[buf] = load_raw(qrow, static_cast<int64_t>(st) * T::kStepK, lane);
+      ar[buf] = QaRaw<DT>::load(qrow, static_cast<int64_t>(st) * T::kStepK, lane);
     } else {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -336,6 +387,9 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
     load_a(0, s0);
     load_scales(0, s0);
   }
+  // int8 QA: the token's scale (its row loads issued after the first step's)
+  float qscale = 0.f;
+  if constexpr (QA && DT == kDtInt8) qscale = row_scale_int8(qrow, p.kdim, lane);
   for (int s = s0; s < s1; s += 2) {
     // Two-deep register pipeline: fetch s+1 while s is multiplied.
 #pragma unroll
@@ -350,10 +404,12 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
         load_a(h ^ 1, nxt);
         load_scales(h ^ 1, nxt);
       }
-      if constexpr (QA) {
+      if constexpr (QA && DT == kDtFp8) {
         const float sc = quant_step_fp8(ar[h], qlds[wave], lane, af[h][0]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) sa[h][0][i] = cvalid[0][i] ? sc : 0.f;
+      } else if constexpr (QA) {
+        quant_step_int8(ar[h], qscale, qlds[wave], lane, af[h][0]);
       }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) lines_to_frag(bf[h][nb]);
@@ -419,7 +475,8 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
       for (int nb = 0; nb < NB; ++nb) {
         float x;
         if constexpr (DT == kDtInt8) {
-          const float sa = valid ? p.a_scale[crow[mt][i]] : 0.f;
+          float sa = 0.f;
+          if (valid) sa = QA ? qscale : p.a_scale[crow[mt][i]];
           const float sw = p.w_scale[static_cast<int64_t>(e) * p.nrows_w +
                                      (nb ? p.n_out : 0) + col];
           x = static_cast<float>(acc[nb][mt][i]) * sa * sw;
@@ -457,7 +514,7 @@ static int dispatch_kw(const GemmParams& p, int mt, int kw, int row_blocks,
                        hipStream_t stream) {
   if (p.direct_ids) {
     // direct rows: one slot per 16-row tile; a_src: quantised on the fly
-    if constexpr (DT == kDtFp8) {
+    if constexpr (DT != kDtBf16) {
       if (p.a_src) {
 #define FGS_CASE(KW_)             \
   if (mt == 1 && kw == KW_)       \
@@ -525,8 +582,8 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
     s1 = steps;
   }
 
-  static_assert(!QA || DT == kDtFp8, "on-the-fly quantisation");
-  __shared__ __attribute__((aligned(16))) uint8_t qlds[QA ? KW : 1][128];
+  static_assert(!QA || DT != kDtBf16, "on-the-fly quantisation");
+  __shared__ __attribute__((aligned(16))) uint8_t qlds[QA ? KW : 1][T::kStepK];
 
   // slots <= KW: this wave's partial of slot j0's y (un-weighted);
   // slots > KW: the weighted sum of this wave's complete slots
@@ -546,13 +603,13 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
                            : nullptr;
     Acc acc = {0, 0, 0, 0};
     u32x4 bf[2][NV], af[2][NV];
-    uint32_t ar[2];  // QA: this lane's two raw bf16 values of the slot row's step
+    typename QaRaw<DT>::type ar[2];  // QA: this lane's raw bf16 values of the step
     const uint16_t* qrow = QA ? p.a_src + static_cast<int64_t>(j) * p.kdim : nullptr;
     float sc[2];  // fp8: activation x weight block scale of the step (QA: weight)
     auto load = [&](int buf, int st) {
       load_lines<DT>(bf[buf], brow + st * step_bytes, row8);
       if constexpr (QA) {
-        ar[buf] = load_raw(qrow, static_cast<int64_t>(st) * T::kStepK, lane);
+        ar[buf] = QaRaw<DT>::load(qrow, static_cast<int64_t>(st) * T::kStepK, lane);
         if constexpr (DT == kDtFp8) sc[buf] = wsc[st];
       } else {
         load_act(af[buf], arow + st * step_bytes, lg, avalid);
@@ -560,6 +617,9 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
       }
     };
     if (s0 < s1) load(0, s0);
+    // int8 QA: the slot row's per-token scale
+    float qscale = 0.f;
+    if constexpr (QA && DT == kDtInt8) qscale = row_scale_int8(qrow, p.kdim, lane);
     for (int s = s0; s < s1; s += 2) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -570,6 +630,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
         if constexpr (DT == kDtBf16) {
           mma_step<DT>(acc, af[h], bf[h]);
         } else if constexpr (DT == kDtInt8) {
+          if constexpr (QA) quant_step_int8(ar[h], qscale, qlds[wave], lane, af[h]);
           mma_step_i8<DT>(acc, af[h], bf[h]);
         } else {
           float scl = sc[h];
@@ -582,7 +643,7 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm2_direct_kernel(const GemmPar
     }
     float f = 1.f;
     if constexpr (DT == kDtInt8)
-      f = p.a_scale[j] * p.w_scale[static_cast<int64_t>(e) * p.nrows_w + col];
+      f = (QA ? qscale : p.a_scale[j]) * p.w_scale[static_cast<int64_t>(e) * p.nrows_w + col];
     const float b = p.bias ? p.bias[static_cast<int64_t>(e) * p.nrows_w + col] : 0.f;
     if (slots <= KW) {
 #pragma unroll
@@ -643,15 +704,17 @@ static int launch_gemm2_direct_t(const GemmParams& p, int kw, hipStream_t stream
 int launch_gemm2_direct(int dt, const GemmParams& p, int kw, hipStream_t stream) {
   if (!p.direct_ids || p.numel < 1)
     return fail(FGS_EINVAL, "direct GEMM2: needs the slot ids");
-  if (p.a_src && (dt != kDtFp8 || p.numel > kQaMaxSlots))
-    return fail(FGS_EINVAL, "direct GEMM2: on-the-fly quantisation needs fp8 and at most "
-                            "64 slots");
+  if (p.a_src && (dt == kDtBf16 || p.numel > kQaMaxSlots))
+    return fail(FGS_EINVAL, "direct GEMM2: on-the-fly quantisation needs fp8 / int8 and at "
+                            "most 64 slots");
   switch (dt) {
     case kDtBf16: return launch_gemm2_direct_t<kDtBf16, false>(p, kw, stream);
     case kDtFp8:
       return p.a_src ? launch_gemm2_direct_t<kDtFp8, true>(p, kw, stream)
                      : launch_gemm2_direct_t<kDtFp8, false>(p, kw, stream);
-    case kDtInt8: return launch_gemm2_direct_t<kDtInt8, false>(p, kw, stream);
+    case kDtInt8:
+      return p.a_src ? launch_gemm2_direct_t<kDtInt8, true>(p, kw, stream)
+                     : launch_gemm2_direct_t<kDtInt8, false>(p, kw, stream);
   }
   return fail(FGS_EUNSUPPORTED, "direct GEMM2: unknown dtype");
 }

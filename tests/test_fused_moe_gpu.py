@@ -283,11 +283,11 @@ def test_single_token_fused_limits(gpu):
     assert not _capi.schedule(1, 3072, 256, 64, 16).startswith("fused1")
 
 
-# An fp8 token's GEMMs quantise x and the GEMM1 output themselves; with
-# FLAG_SEPARATE_QUANT the quantiser kernels do. Same arithmetic, so the
+# An fp8 token's GEMMs quantise x and the GEMM1 output themselves, an int8
+# token's GEMM2 the GEMM1 output (per-token scales; x keeps its quantiser);
+# with FLAG_SEPARATE_QUANT the quantiser kernels do. Same arithmetic, so the
 # outputs are bit-identical (both GEMM2 forms; top-k 20 deals slots to the
-# folded GEMM2's waves in turn, top-k 64 is the on-the-fly limit). int8
-# always runs the quantisers.
+# folded GEMM2's waves in turn, top-k 64 is the on-the-fly limit).
 @pytest.mark.parametrize("mode", ["fp8", "int8"])
 @pytest.mark.parametrize("K,N,E,topk", [(3072, 256, 8, 2), (3072, 256, 32, 3),
                                         (3072, 256, 64, 20), (1024, 512, 16, 4),
@@ -297,7 +297,8 @@ def test_single_token_fused_limits(gpu):
 def test_single_token_quant_fold(gpu, mode, K, N, E, topk, fold):
     sched = _capi.FLAG_FOLD_SUM if fold else _capi.FLAG_SEPARATE_SUM
     qm = _capi.QMODE_FP8_BLOCK if mode == "fp8" else _capi.QMODE_INT8_CHANNEL
-    assert ("qfold" in _capi.schedule(1, K, N, E, topk, qm, sched)) == (mode == "fp8")
+    expect = " qfold" if mode == "fp8" else " qfold_a2"
+    assert _capi.schedule(1, K, N, E, topk, qm, sched).endswith(expect)
     assert "qfold" not in _capi.schedule(1, K, N, E, topk, qm,
                                          sched | _capi.FLAG_SEPARATE_QUANT)
     wts = testing.make_weights(K, N, E, mode, 0.1, device=gpu, seed=K + N + E + topk + 7)

@@ -63,10 +63,11 @@ extern "C" {
  * Qwen3-shaped layers and slower on Mixtral-shaped ones, so not the default;
  * the FGS_MOE_FUSED1=1 environment variable makes it the default) */
 #define FGS_FLAG_SINGLE_FUSED 0x4
-/* schedule: a one-token fp8 call quantises its activations with the
- * separate quantiser kernel; by default (top-k <= 64) its GEMMs quantise
- * their bf16 activation rows (x, the GEMM1 output) themselves, with the
- * quantiser's arithmetic, so both give the same bytes and scales */
+/* schedule: a one-token fp8 / int8 call quantises its activations with the
+ * separate quantiser kernels; by default (top-k <= 64) its GEMMs quantise
+ * their bf16 activation rows themselves (fp8: x and the GEMM1 output; int8:
+ * the GEMM1 output, per-token scales), with the quantisers' arithmetic, so
+ * both give the same bytes and scales */
 #define FGS_FLAG_SEPARATE_QUANT 0x8
 /* schedule: LDS-tiled kernels with row-block configuration c (0: 256 rows,
  * 1: 128, 2: 64, 3: 32, 4: 160) instead of the rows-per-expert choice */

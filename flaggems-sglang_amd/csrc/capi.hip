@@ -63,6 +63,7 @@ struct Plan {
                    // (no alignment; distinct experts per token)
   bool direct_sum; // ... and GEMM2 folds the top-k sum (no moe_sum)
   int kwd;         // waves of the folded GEMM2
+  bool pair2;      // ... two slots per MFMA (moe_gemm2_pair_kernel)
   bool fused1;     // one token, bf16: both GEMMs in one launch (decode.hip)
                    // plus the ordered reduction
   int chunk1;      // its intermediate columns per workgroup
@@ -143,6 +144,17 @@ static int tail_choice() {
 
 // FGS_MOE_FUSED1=1 makes the single-token fused path of bf16 layers the
 // default (otherwise FGS_FLAG_SINGLE_FUSED selects it; read once).
+// FGS_MOE_PAIR (0 never, 1 always, unset: by output width) runs the folded
+// single-token GEMM2 with two slots per MFMA (a tuning aid; read once).
+static int pair_choice() {
+  static const int f = [] {
+    const char* v = getenv("FGS_MOE_PAIR");
+    if (!v) return -1;
+    return atoi(v) == 1 ? 1 : atoi(v) == 0 ? 0 : -1;
+  }();
+  return f;
+}
+
 static int fused1_choice() {
   static const int f = [] {
     const char* v = getenv("FGS_MOE_FUSED1");
@@ -257,9 +269,10 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // spans enough column tiles (one workgroup each) to fill the chip.
   const int dc = direct_choice();
   p.direct = !p.tiled && m == 1 && dc != 0;
-  // (measured, 3 x 20 flushed calls, twice: folding wins from 192 column
-  // tiles -- Qwen2 int8 -8 %, Mixtral -1.5 %, DeepSeek fp8 -0.8 % -- and
-  // loses for Qwen3's 128 tiles, +3 %)
+  // (measured, 3 x 20 flushed calls, twice: folding on one workgroup per 16
+  // columns wins from 192 of them -- Qwen2 int8 -3 %, Mixtral -1.5 %,
+  // DeepSeek fp8 -4 % -- and loses for Qwen3's 128, +3 %; see below for the
+  // paired form)
   // One fp8 token: the GEMMs quantise their activation rows (x, the GEMM1
   // output) themselves, with the group quantiser's arithmetic. Measured
   // (DeepSeek fp8 M=1, 3 x 50 flushed calls): 88.4 -> 83.0 us. int8's
@@ -277,9 +290,19 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
     p.qfold1 = qa_ok && (qc == 2 || qc == 4);
     p.qfold = qa_ok && (qc == 1 || qc == 3 || qc == 4);
   }
+  // Folding needs about 192 workgroups: one per 16 output columns, or with
+  // two slots per MFMA one per 8 (moe_gemm2_pair_kernel; it quantises two
+  // rows per step, so it is the slower one where 16-column workgroups
+  // suffice: Qwen2 int8 M=1 +5 %, DeepSeek fp8 +9 %, Mixtral +2 %; Qwen3's
+  // 128 sixteen-column tiles fold only paired: 24.7 us against 27.3 for
+  // GEMM2 + moe_sum and 28.0 for the one-slot fold)
+  const int pairs = (topk + 1) / 2;
+  const bool pair_ok = pairs <= 16 && hidden % 8 == 0;
+  const bool fold_wide = hidden / 16 >= 192;
+  const bool fold_pair = !fold_wide && hidden / 8 >= 192 && pair_ok;
   p.direct_sum = p.direct && !(flags & FGS_FLAG_SEPARATE_SUM) &&
                  ((flags & FGS_FLAG_FOLD_SUM) || dc == 3 ||
-                  (dc == 1 && hidden / 16 >= 192));
+                  (dc == 1 && (fold_wide || fold_pair)));
   // One bf16 token: GEMM1, the activation and GEMM2 in one launch per
   // (slot, chunk of intermediate columns), then an ordered reduction (the
   // schedule flags that pick the unfused sum keep the direct kernels).
@@ -294,6 +317,16 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // 16 output columns) resident in one round at 16 waves per CU
   const int64_t wgs = hidden / 16;
   p.kwd = wgs * 16 <= kNumCUs * 16 ? 16 : wgs * 8 <= kNumCUs * 16 ? 8 : 4;
+  // paired: (topk + 1) / 2 pairs, each on the most waves (<= 16 in all)
+  // that keep 3 k steps per wave
+  const int pc = pair_choice();
+  p.pair2 = p.direct_sum && pair_ok && (pc == 1 || (pc == -1 && !fold_wide));
+  if (p.pair2) {
+    int wps = 1;
+    while (pairs * wps * 2 <= 16 && steps2 / (wps * 2) >= 3) wps *= 2;
+    p.kwd = 4;
+    while (p.kwd < pairs * wps) p.kwd *= 2;
+  }
   p.max_padded = max_padded_of(numel, e, p.block_m);
   p.n_blocks = p.max_padded / p.block_m;
   // Blocks that can hold rows: each touched expert pads at most one partial
@@ -627,7 +660,8 @@ static int run_fused(const FusedArgs& a) {
   if (p.direct_sum) {
     // out = the weighted top-k sum, straight from GEMM2
     g2.out = a.out;
-    rc = launch_gemm2_direct(p.dt, g2, p.kwd, a.stream);
+    rc = p.pair2 ? launch_gemm2_pair(p.dt, g2, p.kwd, a.stream)
+                 : launch_gemm2_direct(p.dt, g2, p.kwd, a.stream);
     if (rc) return rc;
     g_prof.mark(5, a.stream);
     g_prof.mark(6, a.stream);
@@ -863,7 +897,7 @@ int32_t fgs_moe_schedule(int64_t m, int64_t hidden, int64_t inter, int32_t num_e
   if (p.fused1) {
     s = "fused1 chunk=" + std::to_string(p.chunk1);
   } else if (p.direct) {
-    s = p.direct_sum ? "direct_sum" : "direct";
+    s = p.direct_sum ? (p.pair2 ? "direct_sum pair" : "direct_sum") : "direct";
     if (p.qfold || p.qfold1)
       s += p.qfold && p.qfold1 ? " qfold" : p.qfold1 ? " qfold_x" : " qfold_a2";
   } else if (!p.tiled) {

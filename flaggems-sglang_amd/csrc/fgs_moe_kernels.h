@@ -133,6 +133,9 @@ int launch_gemm_stream(int dt, bool gemm1, const GemmParams& p, int mt, int kw,
 // the bf16 [1, n_out] output); kw in {4, 8, 16}. With p.a_src (fp8, at
 // most 64 slots) the slot rows are quantised on the fly.
 int launch_gemm2_direct(int dt, const GemmParams& p, int kw, hipStream_t stream);
+// The same with two slots per MFMA (8 output columns per workgroup, twice
+// the workgroups); needs (numel + 1) / 2 <= kw and n_out % 8 == 0.
+int launch_gemm2_pair(int dt, const GemmParams& p, int kw, hipStream_t stream);
 
 // Single-token fused path (decode.hip, bf16): GEMM1 + activation + GEMM2
 // per (slot, chunk of `chunk` intermediate columns) in one launch, fp32

@@ -701,6 +701,216 @@ static int launch_gemm2_direct_t(const GemmParams& p, int kw, hipStream_t stream
   return fail(FGS_EUNSUPPORTED, "direct GEMM2: no kernel for this wave count");
 }
 
+// GEMM2 of one token with the top-k sum folded in, two slots per MFMA: a
+// workgroup owns 8 output columns; slot pair q (slots 2q, 2q+1) puts those
+// columns' weight rows of expert topk_ids[2q] in MFMA rows 0-7 and of
+// topk_ids[2q+1] in rows 8-15 (one whole-line load instruction each) and the
+// two slots' activation rows in A rows 0 and 1, so C[0][c] is slot 2q's
+// column c and C[1][8 + c] slot 2q+1's. The same bytes as
+// moe_gemm2_direct_kernel on twice the workgroups. pairs <= KW: each pair's
+// KW / pairs waves split its contraction; the sum over slots is the same as
+// moe_gemm2_direct_kernel's (per slot its waves' partials in order, the
+// bias, one bf16 rounding, then gamma-weighted in slot order).
+template <int DT>
+__device__ __forceinline__ float quant_pair_fp8(uint32_t ra, uint32_t rb, uint8_t* qb, int lane,
+                                                u32x4 (&f)[2], float& sb) {
+  const float a0 = bf16_lo(ra), a1 = bf16_hi(ra), b0 = bf16_lo(rb), b1 = bf16_hi(rb);
+  const float sa = fmaxf(wave_max(fmaxf(fabsf(a0), fabsf(a1))), 1e-10f) / 448.0f;
+  sb = fmaxf(wave_max(fmaxf(fabsf(b0), fabsf(b1))), 1e-10f) / 448.0f;
+  reinterpret_cast<uint16_t*>(qb)[lane] =
+      static_cast<uint16_t>(cvt_pk_fp8(quant1_fp8(a0, sa), quant1_fp8(a1, sa)));
+  reinterpret_cast<uint16_t*>(qb + 128)[lane] =
+      static_cast<uint16_t>(cvt_pk_fp8(quant1_fp8(b0, sb), quant1_fp8(b1, sb)));
+  const int lg = lane >> 4, ln = lane & 15;
+#pragma unroll
+  for (int v = 0; v < 2; ++v) {
+    const u32x4 x = *reinterpret_cast<const u32x4*>(qb + (ln == 1 ? 128 : 0) + frag_byte(v, lg));
+    f[v] = ln < 2 ? x : u32x4{0, 0, 0, 0};
+  }
+  return sa;
+}
+
+__device__ __forceinline__ void quant_pair_int8(uint2 ra, uint2 rb, float sa, float sb, uint8_t* qb,
+                                                int lane, u32x4 (&f)[4]) {
+  reinterpret_cast<uint32_t*>(qb)[lane] =
+      quant1_int8(bf16_lo(ra.x), sa) | quant1_int8(bf16_hi(ra.x), sa) << 8 |
+      quant1_int8(bf16_lo(ra.y), sa) << 16 | quant1_int8(bf16_hi(ra.y), sa) << 24;
+  reinterpret_cast<uint32_t*>(qb + 256)[lane] =
+      quant1_int8(bf16_lo(rb.x), sb) | quant1_int8(bf16_hi(rb.x), sb) << 8 |
+      quant1_int8(bf16_lo(rb.y), sb) << 16 | quant1_int8(bf16_hi(rb.y), sb) << 24;
+  const int lg = lane >> 4, ln = lane & 15;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const u32x4 x = *reinterpret_cast<const u32x4*>(qb + (ln == 1 ? 256 : 0) + frag_byte(v, lg));
+    f[v] = ln < 2 ? x : u32x4{0, 0, 0, 0};
+  }
+}
+
+template <int DT, int KW, bool QA>
+__global__ __launch_bounds__(KW * 64) void moe_gemm2_pair_kernel(const GemmParams p) {
+  typedef StreamTraits<DT> T;
+  typedef typename T::Acc Acc;
+  constexpr int NV = T::kVecs;
+  constexpr int ESZ = (DT == kDtBf16) ? 2 : 1;
+  static_assert(!QA || DT != kDtBf16, "on-the-fly quantisation");
+  const int n0 = blockIdx.x * 8;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15;
+  const int lg = lane >> 4;
+  const int c8 = ln & 7;   // this lane's output column n0 + c8 (rows c8 and 8 + c8)
+  const int slots = static_cast<int>(p.numel);
+  const int pairs = (slots + 1) / 2;  // <= KW (the launcher checks)
+  const int wps = KW / pairs;         // waves per pair
+  const int q = wave / wps;           // >= pairs: an idle wave
+  const int sub = wave % wps;
+  const int steps = static_cast<int>(p.kdim / T::kStepK);
+  const int s0 = sub * steps / wps, s1 = (sub + 1) * steps / wps;
+  const int64_t step_bytes = static_cast<int64_t>(T::kStepK) * ESZ;
+  const int kblocks = static_cast<int>(p.kdim / 128);
+  __shared__ __attribute__((aligned(16))) uint8_t qlds[QA ? KW : 1][2 * T::kStepK];
+  __shared__ float2 red[KW][64];
+
+  float2 part = {0.f, 0.f};  // (slot 2q, column c8) and (slot 2q + 1, column c8)
+  if (q < pairs) {
+    const int ja = 2 * q, jb = 2 * q + 1;
+    const int ea = p.direct_ids[ja];
+    const int eb = jb < slots ? p.direct_ids[jb] : -1;
+    const bool va = ea >= 0 && ea < p.num_experts;
+    const bool vb = eb >= 0 && eb < p.num_experts;
+    if (va || vb) {
+      // a dropped (or absent) slot reads the other slot's rows with a zero
+      // activation row and is skipped in the sum
+      const int xa = va ? ea : eb, xb = vb ? eb : ea;
+      const int ra = va ? ja : jb, rb = vb ? jb : ja;
+      const uint8_t* brow = p.w + ((static_cast<int64_t>(xa) * p.nrows_w + n0 + (lane & 7)) *
+                                   p.kdim) * ESZ + (lane >> 3) * 16;
+      const int64_t row8 = (static_cast<int64_t>(xb) - xa) * p.nrows_w * p.kdim * ESZ;
+      const bool avalid = (ln == 0 && va) || (ln == 1 && vb);
+      const uint8_t* arow = p.a + (static_cast<int64_t>(ln == 1 ? rb : ra) * p.kdim) * ESZ;
+      const float* wsa = DT == kDtFp8 ? p.w_scale + (static_cast<int64_t>(xa) * (p.nrows_w / 128) +
+                                                      n0 / 128) * kblocks : nullptr;
+      const float* wsb = DT == kDtFp8 ? p.w_scale + (static_cast<int64_t>(xb) * (p.nrows_w / 128) +
+                                                      n0 / 128) * kblocks : nullptr;
+      const uint16_t* qa = QA ? p.a_src + static_cast<int64_t>(ra) * p.kdim : nullptr;
+      const uint16_t* qbr = QA ? p.a_src + static_cast<int64_t>(rb) * p.kdim : nullptr;
+      Acc acc = {0, 0, 0, 0};
+      u32x4 bf[2][NV], af[2][NV];
+      typename QaRaw<DT>::type ar[2][2];
+      float sc[2][2];  // fp8: the two slots' activation x weight scales of a step (QA: weight)
+      auto load = [&](int buf, int st) {
+        load_lines<DT>(bf[buf], brow + st * step_bytes, row8);
+        if constexpr (QA) {
+          ar[buf][0] = QaRaw<DT>::load(qa, static_cast<int64_t>(st) * T::kStepK, lane);
+          ar[buf][1] = QaRaw<DT>::load(qbr, static_cast<int64_t>(st) * T::kStepK, lane);
+          if constexpr (DT == kDtFp8) {
+            sc[buf][0] = wsa[st];
+            sc[buf][1] = wsb[st];
+          }
+        } else {
+          load_act(af[buf], arow + st * step_bytes, lg, avalid);
+          if constexpr (DT == kDtFp8) {
+            sc[buf][0] = p.a_scale[ra * kblocks + st] * wsa[st];
+            sc[buf][1] = p.a_scale[rb * kblocks + st] * wsb[st];
+          }
+        }
+      };
+      float qsa = 0.f, qsb = 0.f;  // int8 QA: the two slot rows' per-token scales
+      if (s0 < s1) load(0, s0);
+      if constexpr (QA && DT == kDtInt8) {
+        qsa = row_scale_int8(qa, p.kdim, lane);
+        qsb = row_scale_int8(qbr, p.kdim, lane);
+      }
+      for (int s = s0; s < s1; s += 2) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int cur = s + h;
+          if (cur >= s1) break;
+          if (cur + 1 < s1) load(h ^ 1, cur + 1);
+          lines_to_frag(bf[h]);
+          if constexpr (DT == kDtBf16) {
+            mma_step<DT>(acc, af[h], bf[h]);
+          } else if constexpr (DT == kDtInt8) {
+            if constexpr (QA) quant_pair_int8(ar[h][0], ar[h][1], qsa, qsb, qlds[wave], lane, af[h]);
+            mma_step_i8<DT>(acc, af[h], bf[h]);
+          } else {
+            float s_a = sc[h][0], s_b = sc[h][1];
+            if constexpr (QA) {
+              float xb;
+              s_a *= quant_pair_fp8<DT>(ar[h][0], ar[h][1], qlds[wave], lane, af[h], xb);
+              s_b *= xb;
+            }
+            const f32x4 t = mma_fp8(af[h], bf[h]);
+            acc[0] += t[0] * s_a;
+            acc[1] += t[1] * s_b;
+          }
+        }
+      }
+      float fa = 1.f, fb = 1.f;
+      if constexpr (DT == kDtInt8) {
+        fa = (QA ? qsa : p.a_scale[ra]) * p.w_scale[static_cast<int64_t>(xa) * p.nrows_w + n0 + c8];
+        fb = (QA ? qsb : p.a_scale[rb]) * p.w_scale[static_cast<int64_t>(xb) * p.nrows_w + n0 + c8];
+      }
+      part.x = static_cast<float>(acc[0]) * fa;  // C[0][c8] in lane (c8, 0)
+      part.y = static_cast<float>(acc[1]) * fb;  // C[1][8 + c8] in lane (8 + c8, 0)
+    }
+  }
+  red[wave][lane] = part;
+  __syncthreads();
+  if (wave != 0 || lane >= 8) return;
+  // lane c: output column n0 + c; slots in order, each its waves' partials
+  // in order, the bias, one bf16 rounding, then the weighted sum
+  const int col = n0 + lane;
+  float tot = 0.f;
+  for (int j = 0; j < slots; ++j) {
+    const int e = p.direct_ids[j];
+    if (e < 0 || e >= p.num_experts) continue;
+    const float gamma = p.weight_on_input ? 1.f : p.topk_w[j];
+    const float b = p.bias ? p.bias[static_cast<int64_t>(e) * p.nrows_w + col] : 0.f;
+    const int qj = j >> 1;
+    float y = 0.f;
+    for (int w = 0; w < wps; ++w) {
+      const float2 v = red[qj * wps + w][(j & 1) ? 8 + lane : lane];
+      y += (j & 1) ? v.y : v.x;
+    }
+    tot = __fadd_rn(tot, __fmul_rn(gamma, bf16_bits_to_f32(f32_to_bf16_bits(y + b))));
+  }
+  static_cast<uint16_t*>(p.out)[col] = f32_to_bf16_bits(tot);
+}
+
+template <int DT, bool QA>
+static int launch_gemm2_pair_t(const GemmParams& p, int kw, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.n_out / 8));
+#define FGS_CASE(KW_)                                                                 \
+  if (kw == KW_) {                                                                    \
+    hipLaunchKernelGGL((moe_gemm2_pair_kernel<DT, KW_, QA>), grid, dim3(KW_ * 64), 0, \
+                       stream, p);                                                    \
+    return check_launch("moe_gemm2_pair_kernel");                                     \
+  }
+  FGS_CASE(4) FGS_CASE(8) FGS_CASE(16)
+#undef FGS_CASE
+  return fail(FGS_EUNSUPPORTED, "paired GEMM2: no kernel for this wave count");
+}
+
+int launch_gemm2_pair(int dt, const GemmParams& p, int kw, hipStream_t stream) {
+  if (!p.direct_ids || p.numel < 1)
+    return fail(FGS_EINVAL, "paired GEMM2: needs the slot ids");
+  if ((p.numel + 1) / 2 > kw || p.n_out % 8 != 0)
+    return fail(FGS_EINVAL, "paired GEMM2: more slot pairs than waves, or n_out % 8 != 0");
+  if (p.a_src && (dt == kDtBf16 || p.numel > kQaMaxSlots))
+    return fail(FGS_EINVAL, "paired GEMM2: on-the-fly quantisation needs fp8 / int8");
+  switch (dt) {
+    case kDtBf16: return launch_gemm2_pair_t<kDtBf16, false>(p, kw, stream);
+    case kDtFp8:
+      return p.a_src ? launch_gemm2_pair_t<kDtFp8, true>(p, kw, stream)
+                     : launch_gemm2_pair_t<kDtFp8, false>(p, kw, stream);
+    case kDtInt8:
+      return p.a_src ? launch_gemm2_pair_t<kDtInt8, true>(p, kw, stream)
+                     : launch_gemm2_pair_t<kDtInt8, false>(p, kw, stream);
+  }
+  return fail(FGS_EUNSUPPORTED, "paired GEMM2: unknown dtype");
+}
+
 int launch_gemm2_direct(int dt, const GemmParams& p, int kw, hipStream_t stream) {
   if (!p.direct_ids || p.numel < 1)
     return fail(FGS_EINVAL, "direct GEMM2: needs the slot ids");

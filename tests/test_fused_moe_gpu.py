@@ -204,11 +204,14 @@ def test_quantised_schedules_agree(gpu, mode):
 # (FLAG_FOLD_SUM forces it) or leaves it to moe_sum (FLAG_SEPARATE_SUM).
 # Covered: both GEMM2 forms for every mode, top-k
 # of 2, odd (3: idle waves), above the 16 waves (20: slots dealt round
-# robin), 64 and 192 output column tiles, dropped slots and the router
-# weight on the input.
+# robin), 64, 128 and 192 output column tiles of 16 (below 192 the fold runs
+# two slots per MFMA on 8-column workgroups: odd top-k 7 leaves a pair's
+# second slot absent, top-k 32 is its 16-pair limit), dropped slots and the
+# router weight on the input.
 @pytest.mark.parametrize("mode", ["bf16", "fp8", "int8"])
 @pytest.mark.parametrize("K,N,E,topk", [(3072, 256, 8, 2), (3072, 256, 32, 3),
-                                        (3072, 256, 64, 20), (1024, 512, 16, 4)],
+                                        (3072, 256, 64, 20), (1024, 512, 16, 4),
+                                        (2048, 256, 64, 7), (1024, 256, 64, 32)],
                          ids=lambda v: str(v))
 @pytest.mark.parametrize("variant", ["plain", "dropped", "on_input"])
 @pytest.mark.parametrize("fold", [True, False], ids=["folded", "separate"])

@@ -1018,6 +1018,33 @@ int32_t fgs_moe_fused_bf16_bias(const void* x, const void* w13, const float* b13
   return run_fused(a);
 }
 
+int32_t fgs_moe_fused_quant_bias(int32_t qmode, const void* x, const void* w13,
+                                 const float* b13, const void* w2, const float* b2,
+                                 const float* w13_scale, const float* w2_scale,
+                                 const float* topk_weights, const int32_t* topk_ids,
+                                 int64_t m, int64_t hidden, int64_t inter,
+                                 int32_t num_experts, int32_t topk, int32_t flags,
+                                 float alpha, float limit, void* workspace,
+                                 int64_t ws_bytes, void* out, void* stream) {
+  if (qmode != FGS_QMODE_FP8_BLOCK && qmode != FGS_QMODE_INT8_CHANNEL)
+    return fail(FGS_EINVAL, "quantised bias variant: qmode must be fp8 block or int8 channel");
+  if (flags & FGS_FLAG_ACT_GELU)
+    return fail(FGS_EUNSUPPORTED, "the bias variant's activation is swiglu only");
+  if (m > 0 && (!b13 || !b2))
+    return fail(FGS_EINVAL, "bias variant needs both b13 and b2");
+  if (!(alpha == alpha) || !(limit == limit))
+    return fail(FGS_EINVAL, "alpha and limit must not be NaN");
+  FusedArgs a{qmode,     x,            w13,      w2, w13_scale, w2_scale, topk_weights,
+              topk_ids,  m,            hidden,   inter, num_experts, topk, flags,
+              workspace, ws_bytes,     out,      as_stream(stream)};
+  a.b13 = b13;
+  a.b2 = b2;
+  a.swiglu = true;
+  a.alpha = alpha;
+  a.limit = limit;
+  return run_fused(a);
+}
+
 int32_t fgs_moe_fused_fp8_block(const void* x, const void* w13,
                                 const void* w2, const float* w13_scale,
                                 const float* w2_scale, int32_t block_n,

@@ -96,6 +96,12 @@ SIGNATURES = {
          _c_void_p, _i64, _i64, _i64, _i32, _i32, _i32, ctypes.c_float,
          ctypes.c_float, _c_void_p, _i64, _c_void_p, _c_void_p],
     ),
+    "fgs_moe_fused_quant_bias": (
+        _i32,
+        [_i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _i32, _i32,
+         ctypes.c_float, ctypes.c_float, _c_void_p, _i64, _c_void_p, _c_void_p],
+    ),
     "fgs_moe_fused_fp8_block": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i32,

@@ -357,6 +357,45 @@ def _check_unsupported(**flags):
         assert value is None, _UNSUPPORTED_FEATURE_MSG.format(name=name)
 
 
+def _weight_qmode(w1, w2, use_fp8_w8a8, use_int8_w8a8, per_channel_quant,
+                  w1_scale, w2_scale, block_shape) -> int:
+    """The weights' quantisation mode from the reference's flag set, with its
+    checks (w1 [E, 2N, K], w2 [E, K, N]): bf16; ``use_fp8_w8a8`` with
+    ``block_shape=[128, 128]`` (e4m3fn, fp32 block scales ``[E, 2N/128,
+    K/128]`` / ``[E, K/128, N/128]``); ``use_int8_w8a8`` with
+    ``per_channel_quant`` (int8, fp32 ``[E, 2N]`` / ``[E, K]``)."""
+    assert not (use_fp8_w8a8 and use_int8_w8a8), (
+        "use_fp8_w8a8 and use_int8_w8a8 are exclusive")
+    E, two_n, K = w1.shape
+    N = two_n // 2
+    if use_fp8_w8a8:
+        assert block_shape is not None and list(block_shape) == [128, 128], (
+            "use_fp8_w8a8 needs block_shape=[128, 128]")
+        assert w1.dtype == torch.float8_e4m3fn and w2.dtype == torch.float8_e4m3fn, (
+            "fp8 weights must be float8_e4m3fn")
+        assert w1_scale is not None and w2_scale is not None, (
+            "use_fp8_w8a8 needs w1_scale and w2_scale")
+        assert tuple(w1_scale.shape) == (E, two_n // 128, K // 128), "w1_scale shape"
+        assert tuple(w2_scale.shape) == (E, K // 128, N // 128), "w2_scale shape"
+        return _capi.QMODE_FP8_BLOCK
+    if use_int8_w8a8:
+        assert per_channel_quant, "use_int8_w8a8 needs per_channel_quant=True"
+        _check_unsupported(block_shape=block_shape)
+        assert w1.dtype == torch.int8 and w2.dtype == torch.int8, (
+            "int8 weights must be int8")
+        assert w1_scale is not None and w2_scale is not None, (
+            "use_int8_w8a8 needs w1_scale and w2_scale")
+        assert w1_scale.numel() == E * two_n and w2_scale.numel() == E * K, (
+            "per-channel scales must be [E, 2N] and [E, K]")
+        return _capi.QMODE_INT8_CHANNEL
+    assert per_channel_quant is False, _UNSUPPORTED_FEATURE_MSG.format(
+        name="per_channel_quant")
+    _check_unsupported(w1_scale=w1_scale, w2_scale=w2_scale, block_shape=block_shape)
+    assert w1.dtype == torch.bfloat16, "w1 must be bfloat16"
+    assert w2.dtype == torch.bfloat16, "w2 must be bfloat16"
+    return _capi.QMODE_BF16
+
+
 def fused_moe(
     hidden_states: torch.Tensor,
     w1: torch.Tensor,
@@ -405,8 +444,6 @@ def fused_moe(
     assert inplace is False, "Inplace is not supported"
     if activation not in ("silu", "gelu"):
         raise ValueError(f"Unsupported FusedMoe activation: {activation}")
-    assert not (use_fp8_w8a8 and use_int8_w8a8), (
-        "use_fp8_w8a8 and use_int8_w8a8 are exclusive")
 
     assert hidden_states.ndim == 2, "hidden_states must be 2D"
     assert hidden_states.dtype == torch.bfloat16, "hidden_states must be bfloat16"
@@ -424,34 +461,8 @@ def fused_moe(
         "topk_ids / topk_weights must be [M, topk]")
     topk = topk_ids.shape[1]
 
-    if use_fp8_w8a8:
-        assert block_shape is not None and list(block_shape) == [128, 128], (
-            "use_fp8_w8a8 needs block_shape=[128, 128]")
-        assert w1.dtype == torch.float8_e4m3fn and w2.dtype == torch.float8_e4m3fn, (
-            "fp8 weights must be float8_e4m3fn")
-        assert w1_scale is not None and w2_scale is not None, (
-            "use_fp8_w8a8 needs w1_scale and w2_scale")
-        assert tuple(w1_scale.shape) == (E, two_n // 128, K // 128), "w1_scale shape"
-        assert tuple(w2_scale.shape) == (E, K // 128, N // 128), "w2_scale shape"
-        qmode = _capi.QMODE_FP8_BLOCK
-    elif use_int8_w8a8:
-        assert per_channel_quant, "use_int8_w8a8 needs per_channel_quant=True"
-        _check_unsupported(block_shape=block_shape)
-        assert w1.dtype == torch.int8 and w2.dtype == torch.int8, (
-            "int8 weights must be int8")
-        assert w1_scale is not None and w2_scale is not None, (
-            "use_int8_w8a8 needs w1_scale and w2_scale")
-        assert w1_scale.numel() == E * two_n and w2_scale.numel() == E * K, (
-            "per-channel scales must be [E, 2N] and [E, K]")
-        qmode = _capi.QMODE_INT8_CHANNEL
-    else:
-        assert per_channel_quant is False, _UNSUPPORTED_FEATURE_MSG.format(
-            name="per_channel_quant")
-        _check_unsupported(w1_scale=w1_scale, w2_scale=w2_scale,
-                           block_shape=block_shape)
-        assert w1.dtype == torch.bfloat16, "w1 must be bfloat16"
-        assert w2.dtype == torch.bfloat16, "w2 must be bfloat16"
-        qmode = _capi.QMODE_BF16
+    qmode = _weight_qmode(w1, w2, use_fp8_w8a8, use_int8_w8a8, per_channel_quant,
+                          w1_scale, w2_scale, block_shape)
 
     lib = _capi.load()
     flags = int(_flags)
@@ -601,6 +612,12 @@ def fused_moe_with_bias(
     gemm1_clamp_limit: Optional[float] = None,
     interleaved: bool = True,
     routed_scaling_factor: Optional[float] = None,
+    use_fp8_w8a8: bool = False,
+    use_int8_w8a8: bool = False,
+    per_channel_quant: bool = False,
+    w1_scale: Optional[torch.Tensor] = None,
+    w2_scale: Optional[torch.Tensor] = None,
+    block_shape: Optional[list] = None,
     _flags: int = 0,
 ) -> torch.Tensor:
     """Fused MoE with biases and the swiglu activation on SGLang-layout
@@ -621,6 +638,14 @@ def fused_moe_with_bias(
     ``gemm1_clamp_limit``. With ``apply_router_weight_on_input`` the router
     weight multiplies ``a`` before its bf16 rounding (matmul_ogs applies its
     gammas to the fused activation's output) and ``y`` is not weighted.
+
+    Quantised weights (the reference's ``w1_pcg`` / ``w2_pcg``) take the
+    flags and scales of ``fused_moe``: ``use_fp8_w8a8`` with 128x128 block
+    scales (gate rows then linear rows only, ``interleaved=False``: the
+    reference's interleaved rows would split every 128-row scale block
+    between gate and linear rows), or ``use_int8_w8a8`` with per-channel
+    scales (``w1_scale [E, 2N]`` in the same row order as ``w1``, so it is
+    de-interleaved with it); the biases add to the dequantised outputs.
     """
     logger.debug("FLAGGEMS_SGLANG FUSED_MOE_WITH_BIAS (gfx950)")
     assert hidden_states.ndim == 2, "hidden_states must be 2D"
@@ -629,14 +654,17 @@ def fused_moe_with_bias(
                     ("w2", w2), ("b2", b2), ("topk_weights", topk_weights),
                     ("topk_ids", topk_ids)):
         _require_gpu(name, t)
-    assert w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16, (
-        "w1 and w2 must be bfloat16")
     E, two_n, K = w1.shape
     N = two_n // 2
     assert hidden_states.shape[1] == K, "hidden size mismatch"
     assert tuple(w2.shape) == (E, K, N), "intermediate size mismatch"
     assert tuple(b1.shape) == (E, two_n) and tuple(b2.shape) == (E, K), (
         "b1 must be [E, 2N] and b2 [E, K]")
+    qmode = _weight_qmode(w1, w2, use_fp8_w8a8, use_int8_w8a8, per_channel_quant,
+                          w1_scale, w2_scale, block_shape)
+    if qmode == _capi.QMODE_FP8_BLOCK and interleaved:
+        raise NotImplementedError(
+            "fp8 block scales need w1's gate rows then linear rows (interleaved=False)")
     M = hidden_states.shape[0]
     assert topk_ids.shape == topk_weights.shape and topk_ids.shape[0] == M, (
         "topk_ids / topk_weights must be [M, topk]")
@@ -644,6 +672,8 @@ def fused_moe_with_bias(
     if interleaved:
         w1 = _deinterleaved(w1)
         b1 = _deinterleave_rows(b1)
+        if qmode == _capi.QMODE_INT8_CHANNEL:
+            w1_scale = _deinterleave_rows(w1_scale.reshape(E, two_n))
     alpha = 1.0 if gemm1_alpha is None else float(gemm1_alpha)
     limit = 0.0 if gemm1_clamp_limit is None else float(gemm1_clamp_limit)
 
@@ -658,16 +688,25 @@ def fused_moe_with_bias(
     b2f = b2.to(torch.float32).contiguous()
     ids = topk_ids.to(torch.int32).contiguous()
     wts = topk_weights.to(torch.float32).contiguous()
-    ws_bytes = lib.fgs_moe_workspace_bytes(M, K, N, E, topk, _capi.QMODE_BF16, flags)
+    ws_bytes = lib.fgs_moe_workspace_bytes(M, K, N, E, topk, qmode, flags)
     if ws_bytes < 0:
-        _capi.check(lib.fgs_moe_validate(M, K, N, E, topk, _capi.QMODE_BF16,
-                                         flags, 0), "fused_moe_with_bias")
+        _capi.check(lib.fgs_moe_validate(M, K, N, E, topk, qmode, flags, 0),
+                    "fused_moe_with_bias")
     out = torch.empty((M, K), dtype=torch.bfloat16, device=x.device)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=x.device)
-    rc = lib.fgs_moe_fused_bf16_bias(
-        x.data_ptr(), w1.data_ptr(), b1f.data_ptr(), w2.data_ptr(),
-        b2f.data_ptr(), wts.data_ptr(), ids.data_ptr(), M, K, N, E, topk, flags,
-        alpha, limit, ws.data_ptr(), ws_bytes, out.data_ptr(), _stream_ptr(x))
+    if qmode == _capi.QMODE_BF16:
+        rc = lib.fgs_moe_fused_bf16_bias(
+            x.data_ptr(), w1.data_ptr(), b1f.data_ptr(), w2.data_ptr(),
+            b2f.data_ptr(), wts.data_ptr(), ids.data_ptr(), M, K, N, E, topk, flags,
+            alpha, limit, ws.data_ptr(), ws_bytes, out.data_ptr(), _stream_ptr(x))
+    else:
+        s1 = w1_scale.to(torch.float32).contiguous()
+        s2 = w2_scale.to(torch.float32).contiguous()
+        rc = lib.fgs_moe_fused_quant_bias(
+            qmode, x.data_ptr(), w1.data_ptr(), b1f.data_ptr(), w2.data_ptr(),
+            b2f.data_ptr(), s1.data_ptr(), s2.data_ptr(), wts.data_ptr(),
+            ids.data_ptr(), M, K, N, E, topk, flags, alpha, limit, ws.data_ptr(),
+            ws_bytes, out.data_ptr(), _stream_ptr(x))
     _capi.check(rc, "fused_moe_with_bias")
     if routed_scaling_factor is not None and routed_scaling_factor != 1.0:
         out.mul_(routed_scaling_factor)
@@ -703,17 +742,39 @@ def triton_kernel_fused_experts_with_bias(
     """Drop-in for the reference's ``triton_kernel_fused_experts_with_bias``
     (ops/fused_moe.py:235-325): same signature and checks, reference layout
     ``w1 [E, K, 2N]`` with interleaved gate/linear columns, ``b1 [E, 2N]``,
-    ``w2 [E, N, K]``, ``b2 [E, K]``, reference routing format. bf16 weights
-    only: a precision config (``w1_pcg`` / ``w2_pcg``) is accepted and
-    ignored for bf16 weights. ``scatter_indx=None`` returns un-combined rows.
+    ``w2 [E, N, K]``, ``b2 [E, K]``, reference routing format. The
+    precision configs (``w1_pcg`` / ``w2_pcg``) matter for quantised weights:
+    int8 ``w1`` / ``w2`` take per-output-column fp32 scales from their
+    ``weight_scale`` (``[E, 2N]`` in w1's interleaved column order, ``[E,
+    K]``); for bf16 weights they are accepted and ignored. fp8 block scales
+    cannot follow the interleaved gate/linear columns (each 128-column block
+    holds both), so fp8 weights go through ``fused_moe_with_bias``.
+    ``scatter_indx=None`` returns un-combined rows.
     """
     logger.debug("FLAGGEMS_SGLANG FUSED_MOE_WITH_BIAS (gfx950)")
     assert inplace is False, "Inplace is not supported"
     assert hidden_states.dtype == torch.bfloat16, "hidden_states must be bfloat16"
     if activation != "silu":
         raise ValueError(f"Unsupported FusedMoe activation: {activation}")
-    assert w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16, (
-        "w1 and w2 must be bfloat16")
+    if w1.dtype == torch.float8_e4m3fn or w2.dtype == torch.float8_e4m3fn:
+        raise NotImplementedError(
+            "fp8 block scales do not follow the interleaved gate/linear columns; "
+            "use fused_moe_with_bias with gate rows then linear rows")
+    quant = {}
+    if w1.dtype == torch.int8 or w2.dtype == torch.int8:
+        assert w1.dtype == torch.int8 and w2.dtype == torch.int8, (
+            "w1 and w2 must both be int8")
+        s1 = getattr(w1_pcg, "weight_scale", None)
+        s2 = getattr(w2_pcg, "weight_scale", None)
+        assert s1 is not None and s2 is not None, (
+            "int8 weights need w1_pcg.weight_scale and w2_pcg.weight_scale")
+        E, two_n = w1.shape[0], w1.shape[2]
+        quant = dict(use_int8_w8a8=True, per_channel_quant=True,
+                     w1_scale=_deinterleave_rows(s1.reshape(E, two_n)),
+                     w2_scale=s2)
+    else:
+        assert w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16, (
+            "w1 and w2 must be bfloat16 or int8")
     num_tokens, hidden = hidden_states.shape
     topk_weights, topk_ids = _routing_to_topk(routing_data, gather_indx,
                                               num_tokens)
@@ -722,7 +783,7 @@ def triton_kernel_fused_experts_with_bias(
     w2n = _native_layout(w2)
     kw = dict(apply_router_weight_on_input=apply_router_weight_on_input,
               gemm1_alpha=gemm1_alpha, gemm1_clamp_limit=gemm1_clamp_limit,
-              interleaved=False)
+              interleaved=False, **quant)
 
     def call(x, tw, ti, **k):
         return fused_moe_with_bias(x, w13n, b1n, w2n, b2, tw, ti, **k)

@@ -280,6 +280,25 @@ int32_t fgs_moe_fused_bf16_bias(const void* x, const void* w13, const float* b13
                                 float alpha, float limit, void* workspace,
                                 int64_t ws_bytes, void* out, void* stream);
 
+/* The same with quantised weights: the precision configs the reference
+ * threads into its two matmul_ogs calls (w1_pcg / w2_pcg,
+ * ops/fused_moe.py:296-301, 303-324) carrying this build's w8a8 formats.
+ *   qmode FGS_QMODE_FP8_BLOCK: w13 / w2 e4m3fn with the 128x128 block
+ *       scales of fgs_moe_fused_fp8_block (activations quantised per 1x128
+ *       group inside the call);
+ *   qmode FGS_QMODE_INT8_CHANNEL: w13 / w2 int8 with the per-output-row
+ *       scales of fgs_moe_fused_int8_channel (activations per token).
+ * Biases, swiglu, gammas and the sum as fgs_moe_fused_bf16_bias; the
+ * biases add to the dequantised GEMM outputs. */
+int32_t fgs_moe_fused_quant_bias(int32_t qmode, const void* x, const void* w13,
+                                 const float* b13, const void* w2, const float* b2,
+                                 const float* w13_scale, const float* w2_scale,
+                                 const float* topk_weights, const int32_t* topk_ids,
+                                 int64_t m, int64_t hidden, int64_t inter,
+                                 int32_t num_experts, int32_t topk, int32_t flags,
+                                 float alpha, float limit, void* workspace,
+                                 int64_t ws_bytes, void* out, void* stream);
+
 /* Fused MoE, fp8 w8a8 with block scales (block_n = block_k = 128).
  *   w13 e4m3fn [E, 2*inter, hidden], w13_scale f32 [E, 2*inter/128, hidden/128]
  *   w2  e4m3fn [E, hidden, inter],   w2_scale  f32 [E, hidden/128, inter/128]

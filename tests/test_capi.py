@@ -147,6 +147,24 @@ def test_entry_points_reject_bad_arguments_before_launch():
     rc = lib.fgs_moe_fused_bf16_bias(nul, nul, 16, nul, 16, nul, nul, 4, 256, 128,
                                      4, 2, 0, float("nan"), 0.0, nul, need, nul, nul)
     assert rc == -1 and "NaN" in _capi.last_error()
+    # quantised bias variant: fp8 / int8 only, then the bias entry's checks
+    rc = lib.fgs_moe_fused_quant_bias(_capi.QMODE_BF16, nul, nul, 16, nul, 16, nul, nul,
+                                      nul, nul, 4, 256, 128, 4, 2, 0, 1.0, 0.0, nul, need,
+                                      nul, nul)
+    assert rc == -1 and "qmode" in _capi.last_error()
+    rc = lib.fgs_moe_fused_quant_bias(_capi.QMODE_INT8_CHANNEL, nul, nul, 16, nul, 16, nul,
+                                      nul, nul, nul, 4, 256, 128, 4, 2, _capi.FLAG_ACT_GELU,
+                                      1.0, 0.0, nul, need, nul, nul)
+    assert rc == -2 and "swiglu" in _capi.last_error()
+    rc = lib.fgs_moe_fused_quant_bias(_capi.QMODE_FP8_BLOCK, nul, nul, nul, nul, 16, nul,
+                                      nul, nul, nul, 4, 256, 128, 4, 2, 0, 1.0, 0.0, nul,
+                                      need, nul, nul)
+    assert rc == -1 and "b13 and b2" in _capi.last_error()
+    need8 = lib.fgs_moe_workspace_bytes(4, 256, 256, 4, 2, _capi.QMODE_INT8_CHANNEL, 0)
+    rc = lib.fgs_moe_fused_quant_bias(_capi.QMODE_INT8_CHANNEL, nul, nul, 16, nul, 16, nul,
+                                      nul, nul, nul, 4, 256, 256, 4, 2, 0, 1.0, 0.0, nul,
+                                      need8, nul, nul)
+    assert rc == -1 and "null pointer" in _capi.last_error()
     assert lib.fgs_moe_validate(4, 256, 128, 4, 2, 0, _capi.FLAG_ACT_GELU, need) == 0
 
 

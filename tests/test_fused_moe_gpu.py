@@ -495,6 +495,78 @@ def test_bias_swiglu(gpu, shape, sched, on_input):
     _check(res.cpu()[toks], ref, "bf16", f"bias swiglu {shape}")
 
 
+# Quantised weights in the bias variant (what the reference's w1_pcg / w2_pcg
+# precision configs carry into matmul_ogs, :296-301): fp8 with 128x128 block
+# scales on gate-then-linear rows, int8 with per-channel scales on interleaved
+# rows (scales de-interleaved with the rows); both schedules (M=1 the direct
+# rows with the folded sum and on-the-fly quantisation), the router weight on
+# either side. The interpretation of a precision config is parity unpinned
+# (triton_kernels is absent); the arithmetic is the oracle's dequantising MoE
+# with the bias variant's swiglu.
+@pytest.mark.parametrize("mode", ["fp8", "int8"])
+@pytest.mark.parametrize("on_input", [False, True], ids=["gammas_out", "gammas_in"])
+@pytest.mark.parametrize("sched", _SCHEDS, ids=["decode", "prefill"])
+@pytest.mark.parametrize("shape", [(1, 3072, 256, 8, 2), (7, 512, 256, 4, 2),
+                                   (300, 1024, 512, 8, 2)])
+def test_bias_swiglu_quantised(gpu, shape, sched, on_input, mode):
+    M, K, N, E, topk = shape
+    wts = testing.make_weights(K, N, E, mode, 0.1, device=gpu, seed=K + N + E + M)
+    x, tw, ti = testing.make_tokens(M, K, E, topk, device=gpu, seed=K + E + M)
+    g = torch.Generator(device=gpu).manual_seed(M + 3)
+    b1 = torch.randn(E, 2 * N, generator=g, device=gpu) * 0.5
+    b2 = torch.randn(E, K, generator=g, device=gpu) * 0.5
+    kw = dict(apply_router_weight_on_input=on_input, gemm1_alpha=1.702,
+              gemm1_clamp_limit=7.0, _flags=sched)
+    if mode == "fp8":
+        res = fm.fused_moe_with_bias(x, wts.w1, b1, wts.w2, b2, tw, ti, interleaved=False,
+                                     **wts.kwargs(mode), **kw)
+    else:
+        q = wts.kwargs(mode)
+        q["w1_scale"] = _interleave_rows(wts.w1_scale)
+        res = fm.fused_moe_with_bias(x, _interleave_rows(wts.w1), _interleave_rows(b1),
+                                     wts.w2, b2, tw, ti, **q, **kw)
+    toks = _sample(M, 48)
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=mode, w1_scale=wts.w1_scale,
+                            w2_scale=wts.w2_scale, tokens=toks, return_mag=True,
+                            activation="swiglu", b1=b1, b2=b2, alpha=1.702, limit=7.0,
+                            apply_router_weight_on_input=on_input)
+    _check(res.cpu()[toks], ref, mode, f"bias swiglu {mode} {shape}")
+
+
+def test_bias_quantised_reference_signature(gpu):
+    """int8 weights through triton_kernel_fused_experts_with_bias: the
+    reference's layouts, per-column scales from the precision configs'
+    ``weight_scale``; fp8 there is rejected (its 128-column scale blocks mix
+    interleaved gate and linear columns), and so is fp8 with interleaved rows
+    in fused_moe_with_bias."""
+    M, K, N, E, topk = 64, 512, 256, 8, 2
+    wts = testing.make_weights(K, N, E, "int8", 0.1, device=gpu, seed=17)
+    x, tw, ti = testing.make_tokens(M, K, E, topk, device=gpu, seed=17)
+    g = torch.Generator(device=gpu).manual_seed(5)
+    b1 = torch.randn(E, 2 * N, generator=g, device=gpu) * 0.5
+    b2 = torch.randn(E, K, generator=g, device=gpu) * 0.5
+    w1_ref = _interleave_rows(wts.w1).transpose(1, 2).contiguous()
+    w2_ref = wts.w2.transpose(1, 2).contiguous()
+    pcg1 = _NS(weight_scale=_interleave_rows(wts.w1_scale))
+    pcg2 = _NS(weight_scale=wts.w2_scale)
+    routing, gather, scatter = flaggems_sglang.standard_topk_to_routing(tw, ti, E)
+    res = flaggems_sglang.triton_kernel_fused_experts_with_bias(
+        x, w1_ref, pcg1, _interleave_rows(b1), w2_ref, pcg2, b2, routing, gather,
+        scatter, gemm1_alpha=1.702, gemm1_clamp_limit=7.0)
+    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode="int8", w1_scale=wts.w1_scale,
+                            w2_scale=wts.w2_scale, return_mag=True, activation="swiglu",
+                            b1=b1, b2=b2, alpha=1.702, limit=7.0)
+    _check(res.cpu(), ref, "int8", "bias compat int8")
+    f8 = testing.make_weights(K, N, E, "fp8", 0.1, device=gpu, seed=17)
+    with pytest.raises(NotImplementedError, match="interleaved"):
+        flaggems_sglang.triton_kernel_fused_experts_with_bias(
+            x, f8.w1.transpose(1, 2).contiguous(), _NS(weight_scale=f8.w1_scale), b1,
+            f8.w2.transpose(1, 2).contiguous(), _NS(weight_scale=f8.w2_scale), b2,
+            routing, gather, scatter)
+    with pytest.raises(NotImplementedError, match="interleaved"):
+        fm.fused_moe_with_bias(x, f8.w1, b1, f8.w2, b2, tw, ti, **f8.kwargs("fp8"))
+
+
 def test_bias_reference_signature(gpu):
     """triton_kernel_fused_experts_with_bias with the reference's layouts
     (w1 [E, K, 2N] interleaved columns, w2 [E, N, K]) and routing format;

@@ -296,6 +296,10 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // suffice: Qwen2 int8 M=1 +5 %, DeepSeek fp8 +9 %, Mixtral +2 %; Qwen3's
   // 128 sixteen-column tiles fold only paired: 24.7 us against 27.3 for
   // GEMM2 + moe_sum and 28.0 for the one-slot fold)
+  // one fp8 token's GEMM1 (k rows of 56+ steps, quantised on the fly) on
+  // 8 waves: DeepSeek fp8 M=1 67.0 -> 65.9 us; 8 waves lose elsewhere
+  // (Qwen3 / Qwen2 int8 / Mixtral M=1 +7..10 %, M=8..16 +3..18 %)
+  if (p.direct && p.dt == kDtFp8 && hidden / step >= 48) p.kw1 = pick_kw(hidden, step, 8, 1);
   const int pairs = (topk + 1) / 2;
   const bool pair_ok = pairs <= 16 && hidden % 8 == 0;
   const bool fold_wide = hidden / 16 >= 192;

@@ -317,10 +317,12 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
              inter % 16 == 0;
   p.chunk1 = p.fused1 ? decode_chunk(hidden, inter, topk) : 0;
   if (p.fused1) p.direct_sum = false;
-  // the folded GEMM2's waves: as many as keep its grid (one workgroup per
-  // 16 output columns) resident in one round at 16 waves per CU
+  // the folded GEMM2's waves: 8 while its grid (one workgroup per 16
+  // output columns) stays resident in one round at 16 waves per CU
+  // (measured against 16 and 4: Mixtral M=1 110.6 -> 106.9 us, Qwen2 int8
+  // 52.2 -> 51.7, DeepSeek fp8 level with 8, 4 is 7-14 % slower)
   const int64_t wgs = hidden / 16;
-  p.kwd = wgs * 16 <= kNumCUs * 16 ? 16 : wgs * 8 <= kNumCUs * 16 ? 8 : 4;
+  p.kwd = wgs * 8 <= kNumCUs * 16 ? 8 : 4;
   // paired: (topk + 1) / 2 pairs, each on the most waves (<= 16 in all)
   // that keep 3 k steps per wave
   const int pc = pair_choice();

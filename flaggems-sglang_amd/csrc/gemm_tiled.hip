@@ -5,7 +5,8 @@
 // padded row order (one expert per block, from moe_align_block_size) and
 // BNR weight rows. Activation and weight tiles stream into a STAGES-deep LDS
 // ring with LDS-DMA loads (global_load_lds_dwordx4: no staging registers),
-// SK bytes of k per stage. Each wave multiplies its (BM/WM) x (BNR/WN)
+// SK bytes of k per stage (a configuration may add a compact ring with
+// fewer activation rows and more slots for blocks that are mostly padding). Each wave multiplies its (BM/WM) x (BNR/WN)
 // sub-tile with v_mfma_f32_32x32x16_bf16; the fragments of the next half
 // stage are read while the current MFMAs run.
 //
@@ -56,19 +57,24 @@ __device__ __forceinline__ bool tile_of(int pid, int grid, int n_rb, int n_ct,
   return true;
 }
 
-template <int BM_, int BNR_, int WM_, int WN_, int SK_, int STAGES_>
+// BMA < BM: a second, compact LDS ring for row blocks whose rows from BMA on
+// are all padding -- BMA activation rows per stage in STAGES_C slots (more
+// stages in flight than the full ring fits); fuller blocks use the full one.
+template <int BM_, int BNR_, int WM_, int WN_, int SK_, int STAGES_, int BMA_ = BM_,
+          int STAGES_C_ = STAGES_>
 struct TileCfg {
   static constexpr int BM = BM_;        // rows (alignment block size)
   static constexpr int BNR = BNR_;      // weight rows per tile
   static constexpr int WM = WM_, WN = WN_;
   static constexpr int SK = SK_;        // k bytes per LDS stage row
   static constexpr int STAGES = STAGES_;
+  static constexpr int BMA = BMA_;      // activation rows of the compact ring
+  static constexpr int STAGES_C = STAGES_C_;
   static constexpr int NW = WM * WN;
   static constexpr int CPR = SK / 16;   // 16-byte chunks per stage row
   static constexpr int LR = 64 / CPR;   // rows one LDS-DMA wave load covers
   static constexpr int RPL = 256 / SK;  // stage rows per 256-byte bank line
-  static constexpr int LDS_BYTES = STAGES * (BM + BNR) * SK;
-  static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KiB");
+  static_assert(BMA <= BM && STAGES_C >= 2, "compact ring");
 };
 
 // Swizzled position of logical 16-byte chunk c of stage row r. The DMA
@@ -87,9 +93,18 @@ template <int DT, class C>
 constexpr int tiled_scale_bytes() {
   return DT == kDtFp8 ? C::NW * 256 : 0;
 }
+// LDS of one ring (COMPACT: BMA activation rows, STAGES_C slots), and the
+// launch's allocation: the larger of the rings a configuration uses.
+template <int DT, class C, bool COMPACT>
+constexpr int tiled_ring_bytes() {
+  return (COMPACT ? C::STAGES_C : C::STAGES) *
+         (((COMPACT ? C::BMA : C::BM) + C::BNR) * C::SK + tiled_scale_bytes<DT, C>());
+}
 template <int DT, class C>
 constexpr int tiled_lds_bytes() {
-  return C::STAGES * ((C::BM + C::BNR) * C::SK + tiled_scale_bytes<DT, C>());
+  return C::BMA < C::BM && tiled_ring_bytes<DT, C, true>() > tiled_ring_bytes<DT, C, false>()
+             ? tiled_ring_bytes<DT, C, true>()
+             : tiled_ring_bytes<DT, C, false>();
 }
 
 // 4-byte LDS-DMA load: lane l copies 4 bytes from `src` to byte 4*l of the
@@ -99,18 +114,22 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds_dst) {
       src, (__attribute__((address_space(3))) void*)(lds_dst), 4, 0, 0);
 }
 
-template <int DT, class C, bool GEMM1>
-__global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
-    const GemmParams p) {
+// One tile (row block rb_id of expert e, column tile tile_n, k split ks).
+// COMPACT: the row block's rows from C::BMA on are all padding, and the LDS
+// ring holds C::BMA activation rows per stage in C::STAGES_C slots.
+template <int DT, class C, bool GEMM1, bool COMPACT>
+__device__ __forceinline__ void tiled_tile(const GemmParams& p, const int rb_id,
+                                           const int tile_n, const int ks, const int e) {
   using T = TiledType<DT>;
   using Frag = typename T::Frag;
   using Acc = typename T::Acc;
   constexpr bool FP8 = DT == kDtFp8;
   constexpr bool INT8 = DT == kDtInt8;
   constexpr int ESZ = T::ESZ, FC = T::FC;
-  constexpr int BM = C::BM, BNR = C::BNR, SK = C::SK, STAGES = C::STAGES;
+  constexpr int BM = C::BM, BNR = C::BNR, SK = C::SK;
+  constexpr int STAGES = COMPACT ? C::STAGES_C : C::STAGES;
   constexpr int NW = C::NW, WN = C::WN;
-  constexpr int A_BYTES = BM * SK;
+  constexpr int A_BYTES = (COMPACT ? C::BMA : BM) * SK;  // activation rows in LDS
   constexpr int B_BYTES = BNR * SK;
   constexpr int SC_OFF = A_BYTES + B_BYTES;
   constexpr int STAGE = SC_OFF + tiled_scale_bytes<DT, C>();
@@ -127,7 +146,9 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   static_assert(STAGES >= 2 && (STAGES - 1) * NL < 64, "stages");
   static_assert(RB >= 1 && CB >= 1 && KK >= 1, "wave tile");
   static_assert(!GEMM1 || CB % 2 == 0, "gate/up pairing");
-  static_assert(tiled_lds_bytes<DT, C>() <= 160 * 1024, "gfx950 LDS is 160 KiB");
+  static_assert(tiled_ring_bytes<DT, C, COMPACT>() <= 160 * 1024, "gfx950 LDS is 160 KiB");
+  // a compact ring holds whole per-wave activation load groups
+  static_assert(!COMPACT || C::BMA % (NLA * C::LR) == 0, "compact ring rows");
   // fp8: one stage is one 128-wide k block of the block scales, and a tile's
   // weight rows (GEMM1: each of its gate and up halves) lie in whole 128-row
   // scale blocks or inside one
@@ -135,21 +156,6 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
 
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
-  constexpr int N_PER_TILE = GEMM1 ? BNR / 2 : BNR;
-  const int n_ct = static_cast<int>(p.n_out / N_PER_TILE);
-  int rb_id, tile_n;
-  if (!tile_of(blockIdx.x, gridDim.x, p.row_blocks * p.ksplit, n_ct, p.group_m,
-               p.group_n, &rb_id, &tile_n))
-    return;
-  // split-K (GEMM2 only): the row-block index space repeats once per split
-  const int ks = rb_id / p.row_blocks;
-  rb_id -= ks * p.row_blocks;
-  if (rb_id * BM >= p.num_post_pad[0]) return;
-  // row blocks smaller than the alignment block (eid_shift > 0): the expert
-  // of the enclosing block; a block that is all padding has nothing to do
-  const int e = p.expert_ids[rb_id >> p.eid_shift];
-  if (e < 0) return;
-  if (p.eid_shift > 0 && p.sorted_ids[rb_id * BM] >= p.numel) return;
 
   const int lane = threadIdx.x & 63;
   // wave index in an SGPR: LDS-DMA destinations (M0) then stay scalar
@@ -740,6 +746,35 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   }
 }
 
+template <int DT, class C, bool GEMM1>
+__global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
+    const GemmParams p) {
+  constexpr int BM = C::BM, BNR = C::BNR;
+
+  constexpr int N_PER_TILE = GEMM1 ? BNR / 2 : BNR;
+  const int n_ct = static_cast<int>(p.n_out / N_PER_TILE);
+  int rb_id, tile_n;
+  if (!tile_of(blockIdx.x, gridDim.x, p.row_blocks * p.ksplit, n_ct, p.group_m,
+               p.group_n, &rb_id, &tile_n))
+    return;
+  // split-K (GEMM2 only): the row-block index space repeats once per split
+  const int ks = rb_id / p.row_blocks;
+  rb_id -= ks * p.row_blocks;
+  if (rb_id * BM >= p.num_post_pad[0]) return;
+  // row blocks smaller than the alignment block (eid_shift > 0): the expert
+  // of the enclosing block; a block that is all padding has nothing to do
+  const int e = p.expert_ids[rb_id >> p.eid_shift];
+  if (e < 0) return;
+  if (p.eid_shift > 0 && p.sorted_ids[rb_id * BM] >= p.numel) return;
+  if constexpr (C::BMA < BM) {
+    if (p.sorted_ids[rb_id * BM + C::BMA] >= p.numel) {
+      tiled_tile<DT, C, GEMM1, true>(p, rb_id, tile_n, ks, e);
+      return;
+    }
+  }
+  tiled_tile<DT, C, GEMM1, false>(p, rb_id, tile_n, ks, e);
+}
+
 // Rasterization (FGS_MOE_GROUPM / FGS_MOE_GROUPN override; tuning aids read
 // once): row blocks per band, or, with bands off (0), column tiles per group.
 static int env_choice(const char* name, int dflt, int lo, int hi) {
@@ -808,8 +843,11 @@ using Cfg32 = TileCfg<32, 256, 1, 4, 128, 4>;   // 4 waves of 32x64
 using Cfg160 = TileCfg<160, 256, 1, 4, 128, 3>;
 // fp8 keeps a second accumulator set per k block (the block-scale fold), so
 // its 256-row configuration has 64x64 wave tiles over 128 weight rows, and
-// the stage scale area costs a stage at 64 and 32 rows.
-using Fp8Cfg256 = TileCfg<256, 128, 4, 2, 128, 3>;  // 8 waves of 64x64
+// the stage scale area costs a stage at 64 and 32 rows. Its blocks of at
+// most 160 rows (~128 rows per expert: DeepSeek M=4096) run a 4-slot ring
+// of 160 activation rows -- three stages in flight instead of two, GEMM1
+// 1.90 -> 1.77 ms -- and fuller blocks the 3-slot ring of all 256 rows.
+using Fp8Cfg256 = TileCfg<256, 128, 4, 2, 128, 3, 160, 4>;  // 8 waves of 64x64
 using Fp8Cfg64 = TileCfg<64, 256, 1, 4, 128, 3>;
 using Fp8Cfg32 = TileCfg<32, 256, 1, 4, 128, 3>;
 

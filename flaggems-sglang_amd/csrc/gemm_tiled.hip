@@ -581,6 +581,58 @@ __device__ __forceinline__ void tiled_tile(const GemmParams& p, const int rb_id,
     while (jp > 1 && 32 * jp * 32 * ob > REGION) jp /= 2;
     return jp;
   };
+  // Every load of the epilogue is issued before its first store: the vector
+  // memory counter counts stores too, so a load issued after one 32-row
+  // block's stores would wait for them to complete. Per block: the token
+  // slot of this lane's row, its int8 activation scale and (GEMM1 with
+  // weight_on_input) its router weight; per column: the int8 weight scales
+  // and the bias, loaded once for all blocks.
+  int esid[RB];
+  float esa[RB], egam[RB];
+#pragma unroll
+  for (int i = 0; i < RB; ++i) esid[i] = p.sorted_ids[row0 + wm * WROWS + i * 32 + (lane & 31)];
+#pragma unroll
+  for (int i = 0; i < RB; ++i) {
+    const int rr = wm * WROWS + i * 32 + (lane & 31);
+    const bool ok = esid[i] < p.numel;
+    esa[i] = INT8 ? p.a_scale[act_of(rr, esid[i])] : 1.f;
+    egam[i] = GEMM1 && p.weight_on_input && ok ? p.topk_w[esid[i]] : 1.f;
+  }
+  // Column values of column block j, group g4 (one f32x4 each, gate and
+  // up for GEMM1): int8 weight scales (else ones) and bias (else zeros),
+  // held in registers when they fit in 32 VGPRs, else loaded where used.
+  constexpr int CBS = GEMM1 ? CB / 2 : CB;
+  constexpr bool HOIST = CBS * (GEMM1 ? 2 : 1) <= 2;
+  struct Cols {
+    f32x4 g[HOIST ? CBS : 1][4], u[HOIST && GEMM1 ? CBS : 1][4];
+  };
+  const f32x4 ones = {1.f, 1.f, 1.f, 1.f}, zeros = {0.f, 0.f, 0.f, 0.f};
+  auto load_cols = [&](Cols& c, auto load4, int64_t col_base) {
+    if constexpr (HOIST) {
+#pragma unroll
+      for (int j = 0; j < CBS; ++j)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int64_t col = col_base + j * 32 + csub + 8 * g4;
+          c.g[j][g4] = load4(col);
+          if constexpr (GEMM1) c.u[j][g4] = load4(p.n_out + col);
+        }
+    }
+  };
+  // value of column block j, group g4 (gate; up when `up`)
+  auto col_of = [&](const Cols& c, auto load4, int64_t col_base, int j, int g4,
+                    bool up) -> f32x4 {
+    if constexpr (HOIST) {
+      if constexpr (GEMM1) return up ? c.u[j][g4] : c.g[j][g4];
+      else return c.g[j][g4];
+    } else {
+      return load4((up ? p.n_out : 0) + col_base + j * 32 + csub + 8 * g4);
+    }
+  };
+  auto sc4 = [&](int64_t col) -> f32x4 { return wscale4(col); };
+  auto no_sc4 = [&](int64_t) -> f32x4 { return ones; };
+  auto b4 = [&](int64_t col) -> f32x4 { return bias4(col); };
+  auto no_b4 = [&](int64_t) -> f32x4 { return zeros; };
   // GEMM1 with silu and no bias (the common case): the router-weight
   // scaling as a compile-time branch, no bias adds, pairwise conversions
   if constexpr (GEMM1) {
@@ -589,36 +641,40 @@ __device__ __forceinline__ void tiled_tile(const GemmParams& p, const int rb_id,
       constexpr std::integral_constant<int, JP * 4> ch{};
       static_assert(32 * JP * 32 * 2 <= REGION, "staging fits");
       const int col_base = tile_n * (BNR / 2) + wn * (WCOLS / 2);
+      Cols sc;
+      if constexpr (INT8) load_cols(sc, sc4, col_base);
+      auto scale_at = [&](int j, int g4, bool up) -> f32x4 {
+        if constexpr (INT8) return col_of(sc, sc4, col_base, j, g4, up);
+        else return no_sc4(0);
+      };
       auto emit = [&](auto scale_c) {
         constexpr bool SCALE = decltype(scale_c)::value;
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
           if (i >= nlive) break;  // all-pad blocks (wave-uniform)
-          const int rr = wm * WROWS + i * 32 + (lane & 31);
-          const int sid = p.sorted_ids[row0 + rr];
-          const float sa = INT8 ? p.a_scale[act_of(rr, sid)] : 1.f;
-          const float gamma = SCALE && sid < p.numel ? p.topk_w[sid] : 1.f;
+          const int sid = esid[i];
+          const float sa = esa[i];
+          const float gamma = egam[i];
           const int r = lane & 31;
 #pragma unroll
           for (int jp0 = 0; jp0 < CB / 2; jp0 += JP) {
 #pragma unroll
             for (int jl = 0; jl < JP; ++jl) {
               const int jb = jp0 + jl;
-              const int col0 = col_base + jb * 32 + csub;
 #pragma unroll
               for (int g4 = 0; g4 < 4; ++g4) {
-                const f32x4 swg = wscale4(col0 + 8 * g4);
-                const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
+                const f32x4 sg = scale_at(jb, g4, false);
+                const f32x4 su = scale_at(jb, g4, true);
                 const Acc& ag = acc[i][jb];
                 const Acc& au = acc[i][jb + CB / 2];
                 const int v = 4 * g4;
                 uint2 v2;
                 v2.x = silu_mul_bf16x2<SCALE>(
-                    value(ag, v, sa, swg[0]), value(ag, v + 1, sa, swg[1]),
-                    value(au, v, sa, swu[0]), value(au, v + 1, sa, swu[1]), gamma);
+                    value(ag, v, sa, sg[0]), value(ag, v + 1, sa, sg[1]),
+                    value(au, v, sa, su[0]), value(au, v + 1, sa, su[1]), gamma);
                 v2.y = silu_mul_bf16x2<SCALE>(
-                    value(ag, v + 2, sa, swg[2]), value(ag, v + 3, sa, swg[3]),
-                    value(au, v + 2, sa, swu[2]), value(au, v + 3, sa, swu[3]), gamma);
+                    value(ag, v + 2, sa, sg[2]), value(ag, v + 3, sa, sg[3]),
+                    value(au, v + 2, sa, su[2]), value(au, v + 3, sa, su[3]), gamma);
                 *reinterpret_cast<uint2*>(slot_at(ch, r, jl * 4 + g4) + half * 8) = v2;
               }
             }
@@ -634,115 +690,144 @@ __device__ __forceinline__ void tiled_tile(const GemmParams& p, const int rb_id,
       else emit(std::false_type{});
       return;
     }
-#pragma unroll
-    for (int i = 0; i < RB; ++i) {
-      const int rr = wm * WROWS + i * 32 + (lane & 31);
-      const int r = row0 + rr;
-      const int sid = p.sorted_ids[r];
-      const bool valid = sid < p.numel;
-      if (!valid) continue;  // pad rows: never stored
-      const float sa = INT8 ? p.a_scale[act_row(rr)] : 1.f;
+    // other activations and the bias variant: stores straight from the
+    // accumulator layout
+    const int col_base = tile_n * (BNR / 2) + wn * (WCOLS / 2);
+    auto emit = [&](auto bias_c) {
+      constexpr bool BIAS = decltype(bias_c)::value;
+      Cols sc, bs;
+      if constexpr (INT8) load_cols(sc, sc4, col_base);
+      if constexpr (BIAS) load_cols(bs, b4, col_base);
+      auto scale_at = [&](int j, int g4, bool up) -> f32x4 {
+        if constexpr (INT8) return col_of(sc, sc4, col_base, j, g4, up);
+        else return no_sc4(0);
+      };
+      auto bias_at = [&](int j, int g4, bool up) -> f32x4 {
+        if constexpr (BIAS) return col_of(bs, b4, col_base, j, g4, up);
+        else return no_b4(0);
+      };
       const bool scale = p.weight_on_input != 0;
-      const float gamma = scale ? p.topk_w[sid] : 0.f;
-      uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
 #pragma unroll
-      for (int jb = 0; jb < CB / 2; ++jb) {
-        const int col0 = tile_n * (BNR / 2) + wn * (WCOLS / 2) + jb * 32 + csub;
+      for (int i = 0; i < RB; ++i) {
+        const int r = row0 + wm * WROWS + i * 32 + (lane & 31);
+        if (esid[i] >= p.numel) continue;  // pad rows: never stored
+        const float sa = esa[i];
+        const float gamma = egam[i];
+        uint16_t* orow = out + static_cast<int64_t>(r) * p.n_out;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const f32x4 swg = wscale4(col0 + 8 * g4);
-          const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
-          const f32x4 bg = bias4(col0 + 8 * g4);
-          const f32x4 bu = bias4(p.n_out + col0 + 8 * g4);
-          uint32_t w0 = 0, w1 = 0;
+        for (int jb = 0; jb < CB / 2; ++jb) {
+          const int col0 = col_base + jb * 32 + csub;
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const uint32_t b = gemm1_epilogue(
-                value(acc[i][jb], 4 * g4 + t, sa, swg[t]) + bg[t],
-                value(acc[i][jb + CB / 2], 4 * g4 + t, sa, swu[t]) + bu[t], scale, gamma,
-                p.act, p.alpha, p.limit);
-            if (t < 2) w0 |= b << (16 * t);
-            else w1 |= b << (16 * (t - 2));
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const f32x4 sg = scale_at(jb, g4, false);
+            const f32x4 su = scale_at(jb, g4, true);
+            const f32x4 bg = bias_at(jb, g4, false);
+            const f32x4 bu = bias_at(jb, g4, true);
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const uint32_t b = gemm1_epilogue(
+                  value(acc[i][jb], 4 * g4 + t, sa, sg[t]) + bg[t],
+                  value(acc[i][jb + CB / 2], 4 * g4 + t, sa, su[t]) + bu[t], scale,
+                  gamma, p.act, p.alpha, p.limit);
+              if (t < 2) w0 |= b << (16 * t);
+              else w1 |= b << (16 * (t - 2));
+            }
+            uint2 v2;
+            v2.x = w0;
+            v2.y = w1;
+            *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
           }
-          uint2 v2;
-          v2.x = w0;
-          v2.y = w1;
-          *reinterpret_cast<uint2*>(orow + col0 + 8 * g4) = v2;
         }
       }
-    }
+    };
+    if (bias) emit(std::true_type{});
+    else emit(std::false_type{});
   } else {
     const int col_base = tile_n * BNR + wn * WCOLS;
+    auto emit = [&](auto bias_c) {
+      constexpr bool BIAS = decltype(bias_c)::value;
+      Cols sc, bs;
+      if constexpr (INT8) load_cols(sc, sc4, col_base);
+      if constexpr (BIAS) load_cols(bs, b4, col_base);
+      auto scale_at = [&](int j, int g4) -> f32x4 {
+        if constexpr (INT8) return col_of(sc, sc4, col_base, j, g4, false);
+        else return no_sc4(0);
+      };
+      auto bias_at = [&](int j, int g4) -> f32x4 {
+        if constexpr (BIAS) return col_of(bs, b4, col_base, j, g4, false);
+        else return no_b4(0);
+      };
 #pragma unroll
-    for (int i = 0; i < RB; ++i) {
-      if (i >= nlive) break;  // all-pad blocks (wave-uniform)
-      const int rr = wm * WROWS + i * 32 + (lane & 31);
-      const int sid = p.sorted_ids[row0 + rr];
-      const float sa = INT8 ? p.a_scale[act_of(rr, sid)] : 1.f;
-      const int r = lane & 31;
-      if (p.ksplit > 1) {
-        // fp32 partial sums of split ks, reduced in fixed order by moe_sum
-        constexpr int JP = pass_blocks(4, CB);
-        constexpr std::integral_constant<int, JP * 8> ch{};
-        static_assert(32 * JP * 32 * 4 <= REGION, "staging fits");
+      for (int i = 0; i < RB; ++i) {
+        if (i >= nlive) break;  // all-pad blocks (wave-uniform)
+        const int sid = esid[i];
+        const float sa = esa[i];
+        const int r = lane & 31;
+        if (p.ksplit > 1) {
+          // fp32 partial sums of split ks, reduced in fixed order by moe_sum
+          constexpr int JP = pass_blocks(4, CB);
+          constexpr std::integral_constant<int, JP * 8> ch{};
+          static_assert(32 * JP * 32 * 4 <= REGION, "staging fits");
 #pragma unroll
-        for (int jp0 = 0; jp0 < CB; jp0 += JP) {
+          for (int jp0 = 0; jp0 < CB; jp0 += JP) {
 #pragma unroll
-          for (int jl = 0; jl < JP; ++jl) {
-            const int j = jp0 + jl;
-            const int col0 = col_base + j * 32 + csub;
+            for (int jl = 0; jl < JP; ++jl) {
+              const int j = jp0 + jl;
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-              const f32x4 sw = wscale4(col0 + 8 * g4);
-              const f32x4 bb = bias4(col0 + 8 * g4);
-              const int v = 4 * g4;
-              *reinterpret_cast<f32x4*>(slot_at(ch, r, jl * 8 + g4 * 2 + half)) =
-                  f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0],
-                        value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
-                        value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
-                        value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
+              for (int g4 = 0; g4 < 4; ++g4) {
+                const f32x4 w = scale_at(j, g4);
+                const f32x4 b = bias_at(j, g4);
+                const int v = 4 * g4;
+                *reinterpret_cast<f32x4*>(slot_at(ch, r, jl * 8 + g4 * 2 + half)) =
+                    f32x4{value(acc[i][j], v, sa, w[0]) + b[0],
+                          value(acc[i][j], v + 1, sa, w[1]) + b[1],
+                          value(acc[i][j], v + 2, sa, w[2]) + b[2],
+                          value(acc[i][j], v + 3, sa, w[3]) + b[3]};
+              }
             }
+            drain(ch, [&](int sr) -> uint8_t* {
+              const int row_sid = __shfl(sid, sr, 64);
+              if (row_sid >= p.numel) return nullptr;
+              return reinterpret_cast<uint8_t*>(
+                  static_cast<float*>(p.out) +
+                  (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out + col_base + jp0 * 32);
+            });
           }
-          drain(ch, [&](int sr) -> uint8_t* {
-            const int row_sid = __shfl(sid, sr, 64);
-            if (row_sid >= p.numel) return nullptr;
-            return reinterpret_cast<uint8_t*>(
-                static_cast<float*>(p.out) +
-                (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out + col_base + jp0 * 32);
-          });
-        }
-      } else {
-        constexpr int JP = pass_blocks(2, CB);
-        constexpr std::integral_constant<int, JP * 4> ch{};
-        static_assert(32 * JP * 32 * 2 <= REGION, "staging fits");
+        } else {
+          constexpr int JP = pass_blocks(2, CB);
+          constexpr std::integral_constant<int, JP * 4> ch{};
+          static_assert(32 * JP * 32 * 2 <= REGION, "staging fits");
 #pragma unroll
-        for (int jp0 = 0; jp0 < CB; jp0 += JP) {
+          for (int jp0 = 0; jp0 < CB; jp0 += JP) {
 #pragma unroll
-          for (int jl = 0; jl < JP; ++jl) {
-            const int j = jp0 + jl;
-            const int col0 = col_base + j * 32 + csub;
+            for (int jl = 0; jl < JP; ++jl) {
+              const int j = jp0 + jl;
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-              const f32x4 sw = wscale4(col0 + 8 * g4);
-              const f32x4 bb = bias4(col0 + 8 * g4);
-              const int v = 4 * g4;
-              uint2 v2;
-              v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
-                                 value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
-              v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
-                                 value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
-              *reinterpret_cast<uint2*>(slot_at(ch, r, jl * 4 + g4) + half * 8) = v2;
+              for (int g4 = 0; g4 < 4; ++g4) {
+                const f32x4 w = scale_at(j, g4);
+                const f32x4 b = bias_at(j, g4);
+                const int v = 4 * g4;
+                uint2 v2;
+                v2.x = pack_bf16x2(value(acc[i][j], v, sa, w[0]) + b[0],
+                                   value(acc[i][j], v + 1, sa, w[1]) + b[1]);
+                v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, w[2]) + b[2],
+                                   value(acc[i][j], v + 3, sa, w[3]) + b[3]);
+                *reinterpret_cast<uint2*>(slot_at(ch, r, jl * 4 + g4) + half * 8) = v2;
+              }
             }
+            drain(ch, [&](int sr) -> uint8_t* {
+              const int row_sid = __shfl(sid, sr, 64);
+              if (row_sid >= p.numel) return nullptr;
+              return reinterpret_cast<uint8_t*>(out + static_cast<int64_t>(row_sid) * p.n_out +
+                                                col_base + jp0 * 32);
+            });
           }
-          drain(ch, [&](int sr) -> uint8_t* {
-            const int row_sid = __shfl(sid, sr, 64);
-            if (row_sid >= p.numel) return nullptr;
-            return reinterpret_cast<uint8_t*>(out + static_cast<int64_t>(row_sid) * p.n_out +
-                                              col_base + jp0 * 32);
-          });
         }
       }
-    }
+    };
+    if (bias) emit(std::true_type{});
+    else emit(std::false_type{});
   }
 }
 

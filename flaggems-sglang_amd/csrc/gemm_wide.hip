@@ -51,7 +51,11 @@ struct WideCfg {
   static constexpr int NL = NLA + NLB;
   static constexpr int SLOT = BM * SK;        // bytes per operand slot
   static constexpr int B_OFF = NS * SLOT;
-  static constexpr int LDS_BYTES = 2 * NS * SLOT;
+  // past the ring: a 2 KiB table per wave of what the epilogue reads
+  // (column scales / bias, and per row the token slot and scales)
+  static constexpr int TAB_OFF = 2 * NS * SLOT;
+  static constexpr int TAB_BYTES = 2048;
+  static constexpr int LDS_BYTES = TAB_OFF + NW * TAB_BYTES;
   static_assert(BM == BNR, "one slot size for both operands");
   static_assert(KK % 2 == 0, "fragment double buffer wraps at a stage boundary");
   static_assert(NS >= 2 && (NS - 2) * NL < 64, "ring depth / vmcnt range");
@@ -479,10 +483,6 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
       uint8_t* stg = lds + (wave < 2 ? fslot * SLOT + wave * (SLOT / 2)
                                      : B_OFF + fslot * SLOT + (wave - 2) * (SLOT / 2));
       static_assert(SLOT / 2 >= 32 * WCOLS * 4, "a 32-row fp32 block fits a wave's staging");
-      auto wscale4 = [&](int64_t wrow) -> f32x4 {
-        if constexpr (INT8) return *reinterpret_cast<const f32x4*>(wsc + wrow);
-        else return f32x4{1.f, 1.f, 1.f, 1.f};
-      };
       auto value = [&](const Acc& a, int v, float sa, float sw) -> float {
         if constexpr (INT8) return static_cast<float>(a[v]) * sa * sw;
         else return a[v];
@@ -494,6 +494,39 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       };
+      // Everything the epilogue reads from global memory -- per row of this
+      // wave's live blocks the token slot, int8 activation scale and router
+      // weight; per column the int8 weight scale and bias -- is loaded
+      // first and parked in the wave's LDS table: the vector memory counter
+      // counts stores too, so a global load issued after one block's stores
+      // would wait for them to complete. Table (floats): [0, 128) column
+      // scales (GEMM1: 64 gate, 64 up), [128, 256) bias (GEMM2) or router
+      // weights (GEMM1), [256, 384) token slots, [384, 512) row scales;
+      // row (block i, r) at i * 32 + r.
+      float* tab = reinterpret_cast<float*>(lds + C::TAB_OFF + wave * C::TAB_BYTES);
+      int* tsid = reinterpret_cast<int*>(tab + 256);
+      const bool woi = GEMM1 && p.weight_on_input;
+      static_assert(RB * 32 <= 128, "table rows");
+#pragma unroll
+      for (int q = 0; q < (NLIVE + 1) / 2; ++q) {
+        // lanes 0-31 take block 2q, lanes 32-63 block 2q+1, row lane & 31
+        const int i = 2 * q + (lane >> 5);
+        if (i < NLIVE) {
+          const int rr = i * 64 + wm * 32 + (lane & 31);
+          const int sid = p.sorted_ids[row0 + rr];
+          const bool ok = sid < p.numel;
+          const int t = i * 32 + (lane & 31);
+          tsid[t] = sid;
+          if constexpr (INT8)
+            tab[384 + t] = p.a_scale[GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? rr : 0)];
+          if (woi) tab[128 + t] = ok ? p.topk_w[sid] : 1.f;
+        }
+      }
+      auto tab_sid = [&](int i, int r) -> int { return tsid[i * 32 + r]; };
+      auto row_sa = [&](int i) -> float {
+        if constexpr (INT8) return tab[384 + i * 32 + (lane & 31)];
+        else return 1.f;
+      };
       if constexpr (GEMM1) {
         // silu, no bias (the launch guarantees both): 64 output columns per
         // wave, 128-byte staged rows (8 chunks). The router-weight scaling is
@@ -502,22 +535,29 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
         constexpr int CH = WCOLS / 2 / 8;  // chunks per staged row
         uint16_t* out = static_cast<uint16_t*>(p.out);
         const int col_base = cur.ct * (BNR / 2) + wn * (WCOLS / 2);
+        static_assert(WCOLS / 2 == 64, "a lane per gate column");
+        if constexpr (INT8) {
+          tab[lane] = wsc[col_base + lane];
+          tab[64 + lane] = wsc[p.n_out + col_base + lane];
+        }
+        stage_sync();
+        auto csc4 = [&](int c) -> f32x4 {
+          if constexpr (INT8) return *reinterpret_cast<const f32x4*>(tab + c);
+          else return f32x4{1.f, 1.f, 1.f, 1.f};
+        };
         auto emit = [&](auto scale_c) {
           constexpr bool SCALE = decltype(scale_c)::value;
 #pragma unroll
           for (int i = 0; i < NLIVE; ++i) {
-            const int sid = p.sorted_ids[row0 + i * 64 + wm * 32 + (lane & 31)];
-            const bool ok = sid < p.numel;
-            const float sa = INT8 ? p.a_scale[ok ? sid / p.topk : 0] : 1.f;
-            const float gamma = SCALE && ok ? p.topk_w[sid] : 1.f;
+            const float sa = row_sa(i);
+            const float gamma = SCALE ? tab[128 + i * 32 + (lane & 31)] : 1.f;
             const int r = lane & 31;
 #pragma unroll
             for (int jb = 0; jb < CB / 2; ++jb) {
-              const int col0 = col_base + jb * 32 + csub;
 #pragma unroll
               for (int g4 = 0; g4 < 4; ++g4) {
-                const f32x4 swg = wscale4(col0 + 8 * g4);
-                const f32x4 swu = wscale4(p.n_out + col0 + 8 * g4);
+                const f32x4 swg = csc4(jb * 32 + csub + 8 * g4);
+                const f32x4 swu = csc4(64 + jb * 32 + csub + 8 * g4);
                 const Acc& ag = acc[i][jb];
                 const Acc& au = acc[i][jb + CB / 2];
                 const int v = 4 * g4;
@@ -538,9 +578,9 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
             for (int k = 0; k < 32 / (64 / CH); ++k) {
               const int sr = k * (64 / CH) + lane / CH;
               const int c = lane % CH;
-              const int row_sid = __shfl(sid, sr, 64);
+              const int rsid = tab_sid(i, sr);
               const uint4 val = *reinterpret_cast<const uint4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
-              if (row_sid < p.numel) {
+              if (rsid < p.numel) {
                 const int64_t orow = row0 + i * 64 + wm * 32 + sr;
                 *reinterpret_cast<uint4*>(out + orow * p.n_out + col_base + c * 8) = val;
               }
@@ -552,89 +592,106 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
         else emit(std::false_type{});
       } else {
         const float* bias = p.bias && ks == 0 ? p.bias + wbase : nullptr;
-        auto bias4 = [&](int64_t col) -> f32x4 {
-          return bias ? *reinterpret_cast<const f32x4*>(bias + col)
-                      : f32x4{0.f, 0.f, 0.f, 0.f};
-        };
-        const int col_base = cur.ct * BNR + wn * WCOLS;
-#pragma unroll
-        for (int i = 0; i < NLIVE; ++i) {
-          const int rr = i * 64 + wm * 32 + (lane & 31);
-          const int sid = p.sorted_ids[row0 + rr];
-          const float sa = INT8 ? p.a_scale[row0 + (sid < p.numel ? rr : 0)] : 1.f;
-          const int r = lane & 31;
-          if (p.ksplit > 1 || cur.slot >= 0) {
-            // fp32 partials (k splits, tail pieces): 512-byte staged rows
-            // (32 chunks), 2 rows per pass
-            constexpr int CH = WCOLS * 4 / 16;
-#pragma unroll
-            for (int j = 0; j < CB; ++j) {
-              const int col0 = col_base + j * 32 + csub;
-#pragma unroll
-              for (int g4 = 0; g4 < 4; ++g4) {
-                const f32x4 sw = wscale4(col0 + 8 * g4);
-                const f32x4 bb = bias4(col0 + 8 * g4);
-                const int v = 4 * g4;
-                const int c = j * 8 + g4 * 2 + half;
-                *reinterpret_cast<f32x4*>(stg + r * (CH * 16) + ((c ^ (r % CH)) * 16)) =
-                    f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0],
-                          value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
-                          value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
-                          value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
-              }
-            }
-            stage_sync();
-            float* outf = static_cast<float*>(p.out);
-#pragma unroll
-            for (int k = 0; k < 32 / (64 / CH); ++k) {
-              const int sr = k * (64 / CH) + lane / CH;
-              const int c = lane % CH;
-              const int row_sid = __shfl(sid, sr, 64);
-              const f32x4 val = *reinterpret_cast<const f32x4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
-              if (row_sid >= p.numel) continue;
-              float* dst;
-              if (cur.slot >= 0)  // tail piece: [slot][tile row][tile column]
-                dst = p.tail_part + (static_cast<int64_t>(cur.slot) * BM + i * 64 + wm * 32 + sr) * BNR +
-                      wn * WCOLS + c * 4;
-              else
-                dst = outf + (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out + col_base + c * 4;
-              *reinterpret_cast<f32x4*>(dst) = val;
-            }
-            stage_sync();
-          } else {
-            // bf16 rows: 256-byte staged rows (16 chunks), 4 rows per pass
-            constexpr int CH = WCOLS * 2 / 16;
-            uint16_t* out = static_cast<uint16_t*>(p.out);
-#pragma unroll
-            for (int j = 0; j < CB; ++j) {
-              const int col0 = col_base + j * 32 + csub;
-#pragma unroll
-              for (int g4 = 0; g4 < 4; ++g4) {
-                const f32x4 sw = wscale4(col0 + 8 * g4);
-                const f32x4 bb = bias4(col0 + 8 * g4);
-                const int v = 4 * g4;
-                uint2 v2;
-                v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
-                                   value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
-                v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
-                                   value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
-                const int c = j * 4 + g4;
-                *reinterpret_cast<uint2*>(stg + r * (CH * 16) + ((c ^ (r % CH)) * 16) + half * 8) = v2;
-              }
-            }
-            stage_sync();
-#pragma unroll
-            for (int k = 0; k < 32 / (64 / CH); ++k) {
-              const int sr = k * (64 / CH) + lane / CH;
-              const int c = lane % CH;
-              const int row_sid = __shfl(sid, sr, 64);
-              const uint4 val = *reinterpret_cast<const uint4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
-              if (row_sid < p.numel)
-                *reinterpret_cast<uint4*>(out + static_cast<int64_t>(row_sid) * p.n_out + col_base + c * 8) = val;
-            }
-            stage_sync();
+        // the bias as a compile-time branch: without one the epilogue
+        // issues no loads between its stores
+        auto run = [&](auto bias_c) {
+          constexpr bool BIAS = decltype(bias_c)::value;
+          const int col_base = cur.ct * BNR + wn * WCOLS;
+          static_assert(WCOLS == 128, "two columns per lane");
+          if constexpr (INT8) {
+            tab[lane] = wsc[col_base + lane];
+            tab[64 + lane] = wsc[col_base + 64 + lane];
           }
-        }
+          if constexpr (BIAS) {
+            tab[128 + lane] = bias[col_base + lane];
+            tab[192 + lane] = bias[col_base + 64 + lane];
+          }
+          stage_sync();
+          auto csc4 = [&](int c) -> f32x4 {
+            if constexpr (INT8) return *reinterpret_cast<const f32x4*>(tab + c);
+            else return f32x4{1.f, 1.f, 1.f, 1.f};
+          };
+          auto cb4 = [&](int c) -> f32x4 {
+            if constexpr (BIAS) return *reinterpret_cast<const f32x4*>(tab + 128 + c);
+            else return f32x4{0.f, 0.f, 0.f, 0.f};
+          };
+#pragma unroll
+          for (int i = 0; i < NLIVE; ++i) {
+            const float sa = row_sa(i);
+            const int r = lane & 31;
+            if (p.ksplit > 1 || cur.slot >= 0) {
+              // fp32 partials (k splits, tail pieces): 512-byte staged rows
+              // (32 chunks), 2 rows per pass
+              constexpr int CH = WCOLS * 4 / 16;
+#pragma unroll
+              for (int j = 0; j < CB; ++j) {
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                  const f32x4 sw = csc4(j * 32 + csub + 8 * g4);
+                  const f32x4 bb = cb4(j * 32 + csub + 8 * g4);
+                  const int v = 4 * g4;
+                  const int c = j * 8 + g4 * 2 + half;
+                  *reinterpret_cast<f32x4*>(stg + r * (CH * 16) + ((c ^ (r % CH)) * 16)) =
+                      f32x4{value(acc[i][j], v, sa, sw[0]) + bb[0],
+                            value(acc[i][j], v + 1, sa, sw[1]) + bb[1],
+                            value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                            value(acc[i][j], v + 3, sa, sw[3]) + bb[3]};
+                }
+              }
+              stage_sync();
+              float* outf = static_cast<float*>(p.out);
+#pragma unroll
+              for (int k = 0; k < 32 / (64 / CH); ++k) {
+                const int sr = k * (64 / CH) + lane / CH;
+                const int c = lane % CH;
+                const int row_sid = tab_sid(i, sr);
+                const f32x4 val = *reinterpret_cast<const f32x4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
+                if (row_sid >= p.numel) continue;
+                float* dst;
+                if (cur.slot >= 0)  // tail piece: [slot][tile row][tile column]
+                  dst = p.tail_part + (static_cast<int64_t>(cur.slot) * BM + i * 64 + wm * 32 + sr) * BNR +
+                        wn * WCOLS + c * 4;
+                else
+                  dst = outf + (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out + col_base + c * 4;
+                *reinterpret_cast<f32x4*>(dst) = val;
+              }
+              stage_sync();
+            } else {
+              // bf16 rows: 256-byte staged rows (16 chunks), 4 rows per pass
+              constexpr int CH = WCOLS * 2 / 16;
+              uint16_t* out = static_cast<uint16_t*>(p.out);
+#pragma unroll
+              for (int j = 0; j < CB; ++j) {
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                  const f32x4 sw = csc4(j * 32 + csub + 8 * g4);
+                  const f32x4 bb = cb4(j * 32 + csub + 8 * g4);
+                  const int v = 4 * g4;
+                  uint2 v2;
+                  v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
+                                     value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
+                  v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
+                                     value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
+                  const int c = j * 4 + g4;
+                  *reinterpret_cast<uint2*>(stg + r * (CH * 16) + ((c ^ (r % CH)) * 16) + half * 8) = v2;
+                }
+              }
+              stage_sync();
+#pragma unroll
+              for (int k = 0; k < 32 / (64 / CH); ++k) {
+                const int sr = k * (64 / CH) + lane / CH;
+                const int c = lane % CH;
+                const int row_sid = tab_sid(i, sr);
+                const uint4 val = *reinterpret_cast<const uint4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
+                if (row_sid < p.numel)
+                  *reinterpret_cast<uint4*>(out + static_cast<int64_t>(row_sid) * p.n_out + col_base + c * 8) = val;
+              }
+              stage_sync();
+            }
+          }
+        };
+        if (bias) run(std::true_type{});
+        else run(std::false_type{});
       }
     }
   };

@@ -445,6 +445,30 @@ def test_block_remainders(gpu, mode, N):
     assert torch.equal(res, again)
 
 
+@pytest.mark.parametrize("mode,K,N", [("bf16", 512, 256), ("int8", 512, 256), ("fp8", 512, 256),
+                                      ("fp8", 1024, 512)])
+def test_tiled_configs_bit_identical(gpu, mode, K, N):
+    """Every tiled configuration -- 256/128/64/32/160-row blocks, the 4-wave
+    kernel, the fp8 tile's compact and full rings -- computes each output
+    element with the same operations in the same order (per 128-byte k
+    stage the same MFMA k steps, then the same scale fold), so on the same
+    inputs all of them give the same bits; blocks holding 1..255 rows after
+    full ones (the ring edge at 160 included) exercise every partial-block
+    path. A layout or indexing slip in any one configuration breaks this
+    even where it stays inside the oracle tolerance."""
+    rem = [1, 33, 128, 159, 160, 161, 200, 255, 65, 8]
+    counts = [256 * (1 + e % 2) + r for e, r in enumerate(rem)]
+    w, ids = _routing_with_counts(counts, gpu, seed=N)
+    M = ids.shape[0]
+    wts = testing.make_weights(K, N, len(counts), mode, 0.05, device=gpu, seed=K + N + 7)
+    g = torch.Generator(device=gpu).manual_seed(N + 11)
+    x = torch.randn(M, K, generator=g, device=gpu).to(torch.bfloat16)
+    outs = [fm.fused_moe(x, wts.w1, wts.w2, w, ids, _flags=_capi.flag_tile(cfg), **wts.kwargs(mode))
+            for cfg in range(_capi.TILED_CONFIGS)]
+    for cfg in range(1, _capi.TILED_CONFIGS):
+        assert torch.equal(outs[0], outs[cfg]), f"{mode} K={K} N={N}: tile 0 vs tile {cfg}"
+
+
 # ------------------------------------------------- activations and biases ---
 _SCHEDS = [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL]
 

@@ -73,7 +73,7 @@ struct Plan {
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
   int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail, o_part,
-      o_xst,
+      o_xst, o_rids, o_rw,
       total;
 };
 
@@ -371,6 +371,9 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   if (p.tiled && p.dt == kDtFp8 && p.tile_cfg == 0)
     p.o_xst = take((hidden / 128) * p.max_padded * 4);
   p.o_part = p.fused1 ? take(static_cast<int64_t>(topk) * (inter / p.chunk1) * hidden * 4) : -1;
+  // a call on the routing tuple: each flat slot's expert id and gate scale
+  p.o_rids = take(numel * 4);
+  p.o_rw = take(numel * 4);
   p.total = o;
   *pl = p;
   return FGS_OK;
@@ -484,6 +487,11 @@ struct FusedArgs {
   // stage events off for this call (the allocation-free entry point: event
   // creation is a runtime allocation)
   bool no_profile = false;
+  // routing tuple input (gate_scal, gather_indx.src_indx, expt_hist) in
+  // place of topk_weights / topk_ids
+  const float* gate_scal = nullptr;
+  const int32_t* gather_src = nullptr;
+  const int32_t* expt_hist = nullptr;
 };
 
 static int run_fused(const FusedArgs& a) {
@@ -491,8 +499,9 @@ static int run_fused(const FusedArgs& a) {
                     a.ws_bytes, true);
   if (rc) return rc;
   if (a.m == 0) return FGS_OK;  // nothing to read or write
-  if (!a.x || !a.w13 || !a.w2 || !a.topk_weights || !a.topk_ids || !a.out ||
-      !a.ws)
+  const bool routed = a.gather_src != nullptr;
+  if (!a.x || !a.w13 || !a.w2 || !a.out || !a.ws ||
+      (routed ? (!a.gate_scal || !a.expt_hist) : (!a.topk_weights || !a.topk_ids)))
     return fail(FGS_EINVAL, "null pointer argument");
   if (a.qmode != FGS_QMODE_BF16 && (!a.w13_scale || !a.w2_scale))
     return fail(FGS_EINVAL, "quantised mode needs w13_scale and w2_scale");
@@ -511,12 +520,26 @@ static int run_fused(const FusedArgs& a) {
   uint16_t* a2 = reinterpret_cast<uint16_t*>(ws + p.o_a2);
   uint16_t* y = reinterpret_cast<uint16_t*>(ws + p.o_y);
   const int64_t numel = a.m * a.topk;
+  // the per-slot routing every later stage reads
+  const float* topk_w = a.topk_weights;
+  const int32_t* topk_ids = a.topk_ids;
 
   if (a.no_profile) g_prof.cur = nullptr;
   else g_prof.begin();
   g_prof.mark(0, a.stream);
-  if (!p.direct) {
-    rc = launch_align(a.topk_ids, numel, a.e, p.block_m, sorted, eids, npp,
+  if (routed) {
+    // the routing tuple's gathered order is the alignment's order: one
+    // launch gives the padded order and each slot's expert and gate scale
+    int32_t* rids = reinterpret_cast<int32_t*>(ws + p.o_rids);
+    float* rw = reinterpret_cast<float*>(ws + p.o_rw);
+    rc = launch_routing_order(a.gate_scal, a.gather_src, a.expt_hist, numel, a.e, p.block_m,
+                              p.max_padded, p.direct ? nullptr : sorted, eids, npp, rids, rw,
+                              a.stream);
+    if (rc) return rc;
+    topk_w = rw;
+    topk_ids = rids;
+  } else if (!p.direct) {
+    rc = launch_align(topk_ids, numel, a.e, p.block_m, sorted, eids, npp,
                       p.max_padded, a.stream,
                       p.o_alg >= 0 ? reinterpret_cast<int32_t*>(ws + p.o_alg) : nullptr);
     if (rc) return rc;
@@ -559,8 +582,8 @@ static int run_fused(const FusedArgs& a) {
     d.w2 = a.w2;
     d.b13 = a.b13;
     d.b2 = a.b2;
-    d.topk_w = a.topk_weights;
-    d.ids = a.topk_ids;
+    d.topk_w = topk_w;
+    d.ids = topk_ids;
     d.part = reinterpret_cast<float*>(ws + p.o_part);
     d.out = a.out;
     d.hidden = a.hidden;
@@ -590,7 +613,7 @@ static int run_fused(const FusedArgs& a) {
   g1.sorted_ids = sorted;
   g1.expert_ids = eids;
   g1.num_post_pad = npp;
-  g1.topk_w = a.topk_weights;
+  g1.topk_w = topk_w;
   g1.out = a2;
   g1.kdim = a.hidden;
   g1.n_out = a.inter;
@@ -607,7 +630,7 @@ static int run_fused(const FusedArgs& a) {
   g1.a_scale_kstride = p.o_xst >= 0 ? p.max_padded : 0;
   if (p.direct) {
     // slot j is row tile j; a2 holds the compact slot rows
-    g1.direct_ids = a.topk_ids;
+    g1.direct_ids = topk_ids;
   }
   if (p.qfold1) g1.a_src = static_cast<const uint16_t*>(a.x);
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, static_cast<int>(p.n_launch),
@@ -683,11 +706,11 @@ static int run_fused(const FusedArgs& a) {
 
   if (p.ksplit2 > 1)
     rc = launch_moe_sum_partials(reinterpret_cast<const float*>(y), p.ksplit2,
-                                 a.out, a.m, a.topk, a.hidden, a.topk_ids, a.e,
-                                 on_input ? nullptr : a.topk_weights, a.stream);
+                                 a.out, a.m, a.topk, a.hidden, topk_ids, a.e,
+                                 on_input ? nullptr : topk_w, a.stream);
   else
-    rc = launch_moe_sum_routed(y, a.out, a.m, a.topk, a.hidden, a.topk_ids,
-                               a.e, on_input ? nullptr : a.topk_weights,
+    rc = launch_moe_sum_routed(y, a.out, a.m, a.topk, a.hidden, topk_ids,
+                               a.e, on_input ? nullptr : topk_w,
                                a.stream);
   g_prof.mark(6, a.stream);
   return rc;
@@ -1083,6 +1106,55 @@ int32_t fgs_moe_fused_int8_channel(const void* x, const void* w13,
               inter,                  num_experts,  topk,     flags, workspace,
               ws_bytes,               out,          as_stream(stream)};
   return run_fused(a);
+}
+
+int32_t fgs_moe_fused_routed(int32_t qmode, const void* x, const void* w13, const void* w2,
+                             const float* w13_scale, const float* w2_scale, const float* b13,
+                             const float* b2, float alpha, float limit,
+                             const float* gate_scal, const int32_t* gather_src,
+                             const int32_t* expt_hist, int64_t m, int64_t hidden,
+                             int64_t inter, int32_t num_experts, int32_t topk, int32_t flags,
+                             void* workspace, int64_t ws_bytes, void* out, void* stream) {
+  const bool bias = b13 != nullptr || b2 != nullptr;
+  if (bias && (!b13 || !b2)) return fail(FGS_EINVAL, "bias variant needs both b13 and b2");
+  if (bias && (flags & FGS_FLAG_ACT_GELU))
+    return fail(FGS_EUNSUPPORTED, "the bias variant's activation is swiglu only");
+  if (bias && (!(alpha == alpha) || !(limit == limit)))
+    return fail(FGS_EINVAL, "alpha and limit must not be NaN");
+  if (m > 0 && (!gate_scal || !gather_src || !expt_hist))
+    return fail(FGS_EINVAL, "null pointer argument");
+  FusedArgs a{qmode,     x,        w13,      w2,    w13_scale,   w2_scale, nullptr,
+              nullptr,   m,        hidden,   inter, num_experts, topk,     flags,
+              workspace, ws_bytes, out,      as_stream(stream)};
+  a.gate_scal = gate_scal;
+  a.gather_src = gather_src;
+  a.expt_hist = expt_hist;
+  if (bias) {
+    a.b13 = b13;
+    a.b2 = b2;
+    a.swiglu = true;
+    a.alpha = alpha;
+    a.limit = limit;
+  }
+  return run_fused(a);
+}
+
+int32_t fgs_moe_routing_to_topk(const float* gate_scal, const int32_t* gather_src,
+                                const int32_t* expt_hist, int64_t m, int32_t topk,
+                                int32_t num_experts, float* topk_weights, int32_t* topk_ids,
+                                void* stream) {
+  if (m < 0 || topk < 1) return fail(FGS_EINVAL, "m >= 0 and topk >= 1 required");
+  if (num_experts < 1 || num_experts > kMaxExperts)
+    return fail(FGS_EINVAL, "num_experts must be in [1, 1024]");
+  const int64_t numel = m * topk;
+  if (numel >= (int64_t(1) << 31))
+    return fail(FGS_EUNSUPPORTED, "m * topk too large for int32 indices");
+  if (numel == 0) return FGS_OK;
+  if (!gate_scal || !gather_src || !expt_hist || !topk_weights || !topk_ids)
+    return fail(FGS_EINVAL, "null pointer argument");
+  return launch_routing_order(gate_scal, gather_src, expt_hist, numel, num_experts, 1, numel,
+                              nullptr, nullptr, nullptr, topk_ids, topk_weights,
+                              as_stream(stream));
 }
 
 }  // extern "C"

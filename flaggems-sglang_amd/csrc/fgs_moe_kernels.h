@@ -77,7 +77,7 @@ int launch_align(const int32_t* ids, int64_t numel, int num_experts,
 
 // Routing-format conversion (routing.hip): the triton_kernels routing tuple
 // of _standard_topk_to_triton_kernels, block metadata for block_m in
-// {16, 32, 64, 128}. num_experts <= 1022 (two extra id classes).
+// {16, 32, 64, 128}. num_experts <= 1022.
 constexpr int kRoutingMaxExperts = 1022;
 int64_t routing_max_tiles(int64_t numel, int num_experts);
 int64_t routing_workspace_bytes(int64_t numel, int num_experts);
@@ -86,6 +86,15 @@ int launch_topk_to_routing(const float* weights, const int32_t* ids, int64_t m, 
                            int32_t* gate_indx, int32_t* hist, int32_t* token_offs_raw,
                            int32_t* token_offs_pad, int32_t* block_pid_map,
                            int64_t max_tiles, void* workspace, hipStream_t stream);
+
+// The routing tuple -> the alignment's padded order (sorted_ids non-null:
+// sorted_ids [max_padded], expert_ids [max_padded / block], num_post_pad)
+// and / or per flat slot its expert id and gate scale (ids_out non-null:
+// ids_out, w_out [numel]); num_experts <= 1024. See routing.hip.
+int launch_routing_order(const float* gate_scal, const int32_t* src, const int32_t* hist,
+                         int64_t numel, int num_experts, int block, int64_t max_padded,
+                         int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_post_pad,
+                         int32_t* ids_out, float* w_out, hipStream_t stream);
 
 int launch_silu_and_mul(const void* in, void* out, int64_t rows, int64_t n,
                         hipStream_t stream);

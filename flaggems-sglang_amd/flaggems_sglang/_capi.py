@@ -65,6 +65,11 @@ SIGNATURES = {
          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64,
          _c_void_p],
     ),
+    "fgs_moe_routing_to_topk": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _c_void_p, _c_void_p,
+         _c_void_p],
+    ),
     "fgs_moe_silu_and_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "fgs_moe_sum": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _i64, _c_void_p]),
     "fgs_moe_topk_gating": (
@@ -101,6 +106,12 @@ SIGNATURES = {
         [_i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
          _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _i32, _i32,
          ctypes.c_float, ctypes.c_float, _c_void_p, _i64, _c_void_p, _c_void_p],
+    ),
+    "fgs_moe_fused_routed": (
+        _i32,
+        [_i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, ctypes.c_float, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p,
+         _i64, _i64, _i64, _i32, _i32, _i32, _c_void_p, _i64, _c_void_p, _c_void_p],
     ),
     "fgs_moe_fused_fp8_block": (
         _i32,

@@ -189,21 +189,46 @@ def standard_topk_to_routing(topk_weights, topk_ids, n_expts_tot):
     )
 
 
-def _routing_to_topk(routing_data, gather_indx, num_tokens):
-    """Inverse of :func:`standard_topk_to_routing`: rebuild per-token
-    ``(topk_weights, topk_ids)`` (ids ascending within a token, the order the
-    reference's conversion produces at ops/fused_moe.py:130)."""
+def _routing_args(routing_data, gather_indx, num_tokens):
+    """The routing tuple's device arrays as the C ABI takes them:
+    ``(gate_scal f32, src_indx int32, expt_hist int32, topk, E)``, each
+    contiguous on the GPU."""
     top_k = int(routing_data.n_expts_act)
-    hist = routing_data.expt_hist.to(torch.int64)
-    src = gather_indx.src_indx.to(torch.int64)
+    gate = routing_data.gate_scal
+    src = gather_indx.src_indx
+    hist = routing_data.expt_hist
+    for name, t in (("routing_data.gate_scal", gate), ("gather_indx.src_indx", src),
+                    ("routing_data.expt_hist", hist)):
+        _require_gpu(name, t)
     n = num_tokens * top_k
-    expert_of_pos = torch.repeat_interleave(
-        torch.arange(hist.numel(), device=hist.device), hist, output_size=n
-    )
-    ids = torch.empty(n, dtype=torch.int32, device=src.device)
+    assert gate.numel() == n and src.numel() == n, (
+        "routing tuple does not hold num_tokens * n_expts_act gates")
+    E = hist.numel()
+    n_tot = getattr(routing_data, "n_expts_tot", E)
+    assert int(n_tot) == E, "routing_data.expt_hist must hold n_expts_tot counts"
+    return (gate.to(torch.float32).contiguous(), src.to(torch.int32).contiguous(),
+            hist.to(torch.int32).contiguous(), top_k, E)
+
+
+def _routing_to_topk(routing_data, gather_indx, num_tokens):
+    """Inverse of :func:`standard_topk_to_routing` on the GPU
+    (``fgs_moe_routing_to_topk``, one kernel): per-token ``(topk_weights,
+    topk_ids)`` in the row-sorted slot order of the tuple (ids ascending
+    within a token, the order of the reference's conversion,
+    ops/fused_moe.py:130). Expert e owns the gathered positions of
+    ``token_offs_raw`` = exclusive sums of ``expt_hist`` (the ranges
+    matmul_ogs reads); positions past the histogram's total come back as id
+    -1 (dropped)."""
+    gate, src, hist, top_k, E = _routing_args(routing_data, gather_indx, num_tokens)
+    n = num_tokens * top_k
     wts = torch.empty(n, dtype=torch.float32, device=src.device)
-    ids[src] = expert_of_pos.to(torch.int32)
-    wts[src] = routing_data.gate_scal.to(torch.float32)
+    ids = torch.empty(n, dtype=torch.int32, device=src.device)
+    _capi.check(
+        _capi.load().fgs_moe_routing_to_topk(
+            gate.data_ptr(), src.data_ptr(), hist.data_ptr(), num_tokens, top_k, E,
+            wts.data_ptr(), ids.data_ptr(), _stream_ptr(src)),
+        "routing_to_topk",
+    )
     return wts.view(num_tokens, top_k), ids.view(num_tokens, top_k)
 
 
@@ -507,6 +532,68 @@ def fused_moe(
     return out
 
 
+def _fused_routed(hidden_states, w1, w2, routing_data, gather_indx, *,
+                  qmode=None, w1_scale=None, w2_scale=None, b1=None, b2=None,
+                  alpha=1.0, limit=0.0, activation="silu",
+                  apply_router_weight_on_input=False, _flags=0):
+    """One fused call on the routing tuple (``fgs_moe_fused_routed``):
+    SGLang-layout weights ``w1 [E, 2N, K]`` (gate rows then up / linear
+    rows), ``w2 [E, K, N]``; the tuple's gathered order is the GEMMs' row
+    order (no top-k reconstruction, no second alignment). ``b1`` / ``b2``
+    (both or neither) select the bias variant with swiglu(alpha, limit)."""
+    for name, t in (("hidden_states", hidden_states), ("w1", w1), ("w2", w2)):
+        _require_gpu(name, t)
+    M, K = hidden_states.shape
+    E, two_n, Kw = w1.shape
+    N = two_n // 2
+    assert Kw == K, "hidden size mismatch"
+    assert tuple(w2.shape) == (E, K, N), "intermediate size mismatch"
+    gate, src, hist, topk, E_r = _routing_args(routing_data, gather_indx, M)
+    assert E_r == E, "routing_data.expt_hist must hold one count per expert"
+    if qmode is None:
+        qmode = _capi.QMODE_BF16
+    lib = _capi.load()
+    flags = int(_flags)
+    if apply_router_weight_on_input:
+        flags |= _capi.FLAG_ROUTER_WEIGHT_ON_INPUT
+    if activation == "gelu":
+        flags |= _capi.FLAG_ACT_GELU
+    x = hidden_states.contiguous()
+    w1 = w1.contiguous()
+    w2 = w2.contiguous()
+    ws_bytes = lib.fgs_moe_workspace_bytes(M, K, N, E, topk, qmode, flags)
+    if ws_bytes < 0:
+        _capi.check(lib.fgs_moe_validate(M, K, N, E, topk, qmode, flags, 0),
+                    "fused_moe (routing tuple)")
+    out = torch.empty((M, K), dtype=torch.bfloat16, device=x.device)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=x.device)
+    s1 = s2 = None
+    if qmode != _capi.QMODE_BF16:
+        s1 = w1_scale.to(torch.float32).contiguous()
+        s2 = w2_scale.to(torch.float32).contiguous()
+    b1f = b2f = None
+    if b1 is not None or b2 is not None:
+        assert b1 is not None and b2 is not None, (
+            "Bias execution requires both w13_bias and w2_bias")
+        assert tuple(b1.shape) == (E, two_n) and tuple(b2.shape) == (E, K), (
+            "b1 must be [E, 2N] and b2 [E, K]")
+        b1f = b1.to(torch.float32).contiguous()
+        b2f = b2.to(torch.float32).contiguous()
+
+    def ptr(t):
+        return None if t is None else t.data_ptr()
+
+    _capi.check(
+        lib.fgs_moe_fused_routed(
+            qmode, x.data_ptr(), w1.data_ptr(), w2.data_ptr(), ptr(s1), ptr(s2),
+            ptr(b1f), ptr(b2f), float(alpha), float(limit), gate.data_ptr(),
+            src.data_ptr(), hist.data_ptr(), M, K, N, E, topk, flags, ws.data_ptr(),
+            ws_bytes, out.data_ptr(), _stream_ptr(x)),
+        "fused_moe (routing tuple)",
+    )
+    return out
+
+
 # ``[E, A, B] -> [E, B, A]`` contiguous, once per weight (the reference
 # plugin transposes both weights on every call, ops/fused_moe.py:342-343).
 # A weight passed as a transposed view of a native-layout tensor converts
@@ -567,16 +654,16 @@ def triton_kernel_fused_experts(
         raise ValueError(f"Unsupported FusedMoe activation: {activation}")
 
     num_tokens, hidden = hidden_states.shape
-    topk_weights, topk_ids = _routing_to_topk(routing_data, gather_indx,
-                                              num_tokens)
     w13n = _native_layout(w1)
     w2n = _native_layout(w2)
     if scatter_indx is not None:
-        out = fused_moe(hidden_states, w13n, w2n, topk_weights, topk_ids,
-                        activation=activation,
-                        apply_router_weight_on_input=apply_router_weight_on_input)
+        out = _fused_routed(hidden_states, w13n, w2n, routing_data, gather_indx,
+                            activation=activation,
+                            apply_router_weight_on_input=apply_router_weight_on_input)
         return out.view(num_tokens, hidden)
     # No combine: one row per (token, slot) in the gate (row-sorted) order.
+    topk_weights, topk_ids = _routing_to_topk(routing_data, gather_indx,
+                                              num_tokens)
     return _uncombined(
         lambda x, tw, ti: fused_moe(
             x, w13n, w2n, tw, ti, activation=activation,
@@ -776,11 +863,19 @@ def triton_kernel_fused_experts_with_bias(
         assert w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16, (
             "w1 and w2 must be bfloat16 or int8")
     num_tokens, hidden = hidden_states.shape
-    topk_weights, topk_ids = _routing_to_topk(routing_data, gather_indx,
-                                              num_tokens)
     w13n = _transposed_deinterleaved(w1)
     b1n = _deinterleave_rows(b1)
     w2n = _native_layout(w2)
+    if scatter_indx is not None:
+        out = _fused_routed(
+            hidden_states, w13n, w2n, routing_data, gather_indx,
+            qmode=_capi.QMODE_INT8_CHANNEL if quant else _capi.QMODE_BF16,
+            w1_scale=quant.get("w1_scale"), w2_scale=quant.get("w2_scale"),
+            b1=b1n, b2=b2,
+            alpha=1.0 if gemm1_alpha is None else float(gemm1_alpha),
+            limit=0.0 if gemm1_clamp_limit is None else float(gemm1_clamp_limit),
+            apply_router_weight_on_input=apply_router_weight_on_input)
+        return out.view(num_tokens, hidden)
     kw = dict(apply_router_weight_on_input=apply_router_weight_on_input,
               gemm1_alpha=gemm1_alpha, gemm1_clamp_limit=gemm1_clamp_limit,
               interleaved=False, **quant)
@@ -788,8 +883,8 @@ def triton_kernel_fused_experts_with_bias(
     def call(x, tw, ti, **k):
         return fused_moe_with_bias(x, w13n, b1n, w2n, b2, tw, ti, **k)
 
-    if scatter_indx is not None:
-        return call(hidden_states, topk_weights, topk_ids, **kw).view(num_tokens, hidden)
+    topk_weights, topk_ids = _routing_to_topk(routing_data, gather_indx,
+                                              num_tokens)
     return _uncombined(call, hidden_states, topk_weights, topk_ids, **kw)
 
 
@@ -830,11 +925,11 @@ def fused_moe_flagos(obj, layer, dispatch_output):
     cfg = obj.runner.config
     hidden_states = dispatch_output.hidden_states
     topk_output = dispatch_output.topk_output
+    routing = None
     if isinstance(topk_output, (tuple, list)) and len(topk_output) == 3 and \
             hasattr(topk_output[0], "gate_scal"):
-        routing_data, gather_indx, _ = topk_output
-        topk_weights, topk_ids = _routing_to_topk(routing_data, gather_indx,
-                                                  hidden_states.shape[0])
+        routing = topk_output[:2]  # (routing_data, gather_indx)
+        topk_weights = topk_ids = None
     else:
         topk_weights, topk_ids = topk_output.topk_weights, topk_output.topk_ids
     no_combine = bool(getattr(cfg, "no_combine", False))
@@ -849,25 +944,42 @@ def fused_moe_flagos(obj, layer, dispatch_output):
             raise ValueError(f"Unsupported FusedMoe activation: {activation}")
         w13 = _deinterleaved(layer.w13_weight)
         b13n = _deinterleave_rows(b13)
+        alpha = getattr(cfg, "gemm1_alpha", None)
+        limit = getattr(cfg, "gemm1_clamp_limit", None)
 
         def call(x, tw, ti):
             return fused_moe_with_bias(
                 x, w13, b13n, layer.w2_weight, b2, tw, ti,
-                apply_router_weight_on_input=on_input,
-                gemm1_alpha=getattr(cfg, "gemm1_alpha", None),
-                gemm1_clamp_limit=getattr(cfg, "gemm1_clamp_limit", None),
-                interleaved=False)
+                apply_router_weight_on_input=on_input, gemm1_alpha=alpha,
+                gemm1_clamp_limit=limit, interleaved=False)
+
+        def call_routed(x):
+            return _fused_routed(
+                x, w13, layer.w2_weight, *routing, b1=b13n, b2=b2,
+                alpha=1.0 if alpha is None else float(alpha),
+                limit=0.0 if limit is None else float(limit),
+                apply_router_weight_on_input=on_input)
     else:
         def call(x, tw, ti):
             return fused_moe(x, layer.w13_weight, layer.w2_weight, tw, ti,
                              activation=activation,
                              apply_router_weight_on_input=on_input)
+
+        def call_routed(x):
+            return _fused_routed(x, layer.w13_weight, layer.w2_weight, *routing,
+                                 activation=activation,
+                                 apply_router_weight_on_input=on_input)
     if no_combine:
+        if routing is not None:
+            topk_weights, topk_ids = _routing_to_topk(*routing, hidden_states.shape[0])
         rows = _uncombined(call, hidden_states, topk_weights, topk_ids)
         output = rows.view(hidden_states.shape[0], topk_ids.shape[1],
                            hidden_states.shape[-1])
     else:
-        output = call(hidden_states, topk_weights, topk_ids)
+        if routing is not None:
+            output = call_routed(hidden_states)
+        else:
+            output = call(hidden_states, topk_weights, topk_ids)
         scale = getattr(cfg, "routed_scaling_factor", None)
         if scale is not None and scale != 1.0:
             output.mul_(scale)

@@ -130,8 +130,10 @@ int64_t fgs_moe_align_scratch_bytes(int64_t numel, int32_t num_experts);
  * numel = m * topk; num_experts <= 1022; max_tiles >=
  * fgs_moe_routing_max_tiles(numel, E) (compute_expt_data_torch's bound);
  * workspace: fgs_moe_routing_workspace_bytes(numel, E) bytes, 256-aligned.
- * Ids < 0 (slots not routed) sort ahead of expert 0 and ids >= E behind
- * expert E-1, each group in slot order. Deterministic (no atomics). */
+ * Slots whose id is outside [0, E) (not routed here) sort behind expert
+ * E-1, in slot order, where no expert's token_offs_raw range reaches them
+ * (the reference's argsort would put negative ids ahead of expert 0; its
+ * callers never pass any). Deterministic (no atomics). */
 int64_t fgs_moe_routing_max_tiles(int64_t numel, int32_t num_experts);
 int64_t fgs_moe_routing_workspace_bytes(int64_t numel, int32_t num_experts);
 int32_t fgs_moe_topk_to_routing(const float* topk_weights, const int32_t* topk_ids,
@@ -140,6 +142,23 @@ int32_t fgs_moe_topk_to_routing(const float* topk_weights, const int32_t* topk_i
                                 int32_t* hist, int32_t* token_offs_raw,
                                 int32_t* token_offs_pad, int32_t* block_pid_map,
                                 int64_t max_tiles, void* workspace, int64_t ws_bytes,
+                                void* stream);
+
+/* The inverse conversion: the routing tuple -> per-slot (topk_weights,
+ * topk_ids) in the row-sorted slot order of the tuple's flat indices (each
+ * token's slots by ascending expert id, ops/fused_moe.py:130). Expert e owns
+ * the gathered positions [token_offs_raw[e], token_offs_raw[e + 1]) of
+ * gather_src, with token_offs_raw the exclusive sums of expt_hist -- the
+ * ranges matmul_ogs reads (ops/fused_moe.py:205-231); slots at positions
+ * past the histogram's total get id -1 (dropped). For v = gather_src[p]:
+ * topk_ids[v] = that expert, topk_weights[v] = gate_scal[p].
+ *   gate_scal f32 [m*topk], gather_src int32 [m*topk] (gather_indx.src_indx,
+ *   a permutation of [0, m*topk)), expt_hist int32 [num_experts];
+ *   num_experts <= 1024. Counts are clamped to the slots that exist;
+ *   gather_src entries outside [0, m*topk) are skipped. */
+int32_t fgs_moe_routing_to_topk(const float* gate_scal, const int32_t* gather_src,
+                                const int32_t* expt_hist, int64_t m, int32_t topk,
+                                int32_t num_experts, float* topk_weights, int32_t* topk_ids,
                                 void* stream);
 
 /* silu_and_mul: out[r, c] = bf16(silu(f32(in[r, c])) * f32(in[r, n + c])).
@@ -298,6 +317,27 @@ int32_t fgs_moe_fused_quant_bias(int32_t qmode, const void* x, const void* w13,
                                  int32_t num_experts, int32_t topk, int32_t flags,
                                  float alpha, float limit, void* workspace,
                                  int64_t ws_bytes, void* out, void* stream);
+
+/* Fused MoE on the reference's routing tuple instead of (topk_weights,
+ * topk_ids): the inputs triton_kernel_fused_experts
+ * (ops/fused_moe.py:149-232) and triton_kernel_fused_experts_with_bias
+ * (:235-325) hand to matmul_ogs -- routing_data.gate_scal, gather_indx.src_indx
+ * and routing_data.expt_hist. The tuple's gathered order is used as the
+ * GEMMs' expert-sorted order directly (one kernel builds the block-padded
+ * rows and each slot's expert id and gate scale; no top-k reconstruction, no
+ * second alignment), with the slot conventions of fgs_moe_routing_to_topk.
+ * qmode and scales as fgs_moe_fused_bf16 / _fp8_block / _int8_channel; b13
+ * and b2 both null (silu, or gelu with FGS_FLAG_ACT_GELU) or both set (the
+ * bias variant: swiglu(alpha, limit) as fgs_moe_fused_bf16_bias). Same
+ * workspace (fgs_moe_workspace_bytes) and output as those entry points on
+ * the equivalent (topk_weights, topk_ids). */
+int32_t fgs_moe_fused_routed(int32_t qmode, const void* x, const void* w13, const void* w2,
+                             const float* w13_scale, const float* w2_scale, const float* b13,
+                             const float* b2, float alpha, float limit,
+                             const float* gate_scal, const int32_t* gather_src,
+                             const int32_t* expt_hist, int64_t m, int64_t hidden,
+                             int64_t inter, int32_t num_experts, int32_t topk, int32_t flags,
+                             void* workspace, int64_t ws_bytes, void* out, void* stream);
 
 /* Fused MoE, fp8 w8a8 with block scales (block_n = block_k = 128).
  *   w13 e4m3fn [E, 2*inter, hidden], w13_scale f32 [E, 2*inter/128, hidden/128]

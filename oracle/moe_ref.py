@@ -136,7 +136,13 @@ def topk_to_routing(topk_weights, topk_ids, n_expts_tot: int):
 
     * :130-131 sort each token's ids ascending, carrying the weights (ties,
       which top-k routing never produces, keep slot order);
-    * :133 flatten; :134 stable argsort of the flat ids -> ``topk_indx``;
+    * :133 flatten; :134 stable argsort of the flat ids -> ``topk_indx``,
+      with ids outside ``[0, n_expts_tot)`` (slots not routed here) keyed
+      behind expert ``n_expts_tot - 1``, in flat order: matmul_ogs reads
+      expert e's rows at ``[token_offs_raw[e], token_offs_raw[e+1])`` with
+      ``token_offs_raw`` starting at 0 (:140), so no unrouted slot may sit
+      ahead of expert 0 (where argsort would put negative ids; the
+      reference's callers never pass any);
     * :135 its inverse -> ``gate_indx``; :136 ``gate_scal`` = weights at
       ``topk_indx``;
     * :137-139 ``hist``: ids in ``[0, n_expts_tot)`` counted per expert
@@ -154,7 +160,8 @@ def topk_to_routing(topk_weights, topk_ids, n_expts_tot: int):
         flat_ids += [int(ids[t, j]) for j in order]
         flat_w += [w[t, j] for j in order]
     n = M * k
-    topk_indx = sorted(range(n), key=lambda i: (flat_ids[i], i))
+    topk_indx = sorted(range(n), key=lambda i: (
+        flat_ids[i] if 0 <= flat_ids[i] < n_expts_tot else n_expts_tot, i))
     gate_indx = [0] * n
     for p, i in enumerate(topk_indx):
         gate_indx[i] = p
@@ -167,6 +174,56 @@ def topk_to_routing(topk_weights, topk_ids, n_expts_tot: int):
             np.array(topk_indx, dtype=np.int32).reshape(n),
             np.array(gate_indx, dtype=np.int32).reshape(n),
             np.array(hist, dtype=np.int32))
+
+
+def routing_order(gate_scal, src_indx, hist, n_gates: int, block: int):
+    """What the grouped GEMMs take from a routing tuple (plain Python loops):
+    expert e owns the gathered positions ``[raw[e], raw[e] + h[e])`` of
+    ``src_indx``, ``raw`` = exclusive sums of the histogram ``h`` -- the
+    ``token_offs_raw`` ranges matmul_ogs reads (ops/fused_moe.py:140,
+    205-231). ``h`` is the histogram clamped so the ranges stay inside
+    ``[0, n_gates)`` (negative counts read as 0, running sums cut at
+    ``n_gates``).
+
+    Returns numpy ``(sorted_ids, expert_ids, num_post_pad, ids, weights)``:
+    the block-padded order of :func:`align` (expert e's segment lists
+    ``src_indx[raw[e] : raw[e] + h[e]]``, pads and out-of-range entries =
+    ``n_gates``; ``expert_ids`` per block, -1 past the padded total) and per
+    flat slot ``v = src_indx[p]`` its expert (-1 for ``p`` past the
+    histogram's total) and weight ``gate_scal[p]``."""
+    src = [int(v) for v in np.asarray(src_indx).reshape(-1)]
+    gs = np.asarray(gate_scal, dtype=np.float32).reshape(-1)
+    E = len(hist)
+    h, run = [], 0
+    for c in (int(v) for v in hist):
+        c = min(max(c, 0), n_gates - run)
+        h.append(c)
+        run += c
+    raw = [0]
+    for c in h:
+        raw.append(raw[-1] + c)
+    padded = [(c + block - 1) // block * block for c in h]
+    max_padded = n_gates + E * (block - 1)
+    sorted_ids = [n_gates] * max_padded
+    expert_ids = [-1] * (max_padded // block)
+    pos = 0
+    for e in range(E):
+        for i in range(h[e]):
+            v = src[raw[e] + i]
+            sorted_ids[pos + i] = v if 0 <= v < n_gates else n_gates
+        for b in range(padded[e] // block):
+            expert_ids[pos // block + b] = e
+        pos += padded[e]
+    ids = np.full(n_gates, -7, dtype=np.int32)  # every slot of a permutation is written
+    w = np.zeros(n_gates, dtype=np.float32)
+    for p, v in enumerate(src):
+        if not 0 <= v < n_gates:
+            continue
+        e = next((x for x in range(E) if raw[x] <= p < raw[x + 1]), -1)
+        ids[v] = e
+        w[v] = gs[p]
+    return (np.array(sorted_ids, dtype=np.int32), np.array(expert_ids, dtype=np.int32),
+            pos, ids, w)
 
 
 def routing_max_tiles(n_gates: int, n_expts_tot: int) -> int:

@@ -166,6 +166,28 @@ def test_entry_points_reject_bad_arguments_before_launch():
                                       need8, nul, nul)
     assert rc == -1 and "null pointer" in _capi.last_error()
     assert lib.fgs_moe_validate(4, 256, 128, 4, 2, 0, _capi.FLAG_ACT_GELU, need) == 0
+    # routing-tuple entry: bias pair, swiglu only, the tuple's arrays
+    rc = lib.fgs_moe_fused_routed(0, nul, nul, nul, nul, nul, 16, nul, 1.0, 0.0, 16, 16,
+                                  16, 4, 256, 128, 4, 2, 0, nul, need, nul, nul)
+    assert rc == -1 and "b13 and b2" in _capi.last_error()
+    rc = lib.fgs_moe_fused_routed(0, nul, nul, nul, nul, nul, 16, 16, 1.0, 0.0, 16, 16,
+                                  16, 4, 256, 128, 4, 2, _capi.FLAG_ACT_GELU, nul, need,
+                                  nul, nul)
+    assert rc == -2 and "swiglu" in _capi.last_error()
+    rc = lib.fgs_moe_fused_routed(0, nul, nul, nul, nul, nul, nul, nul, 1.0, 0.0, nul, 16,
+                                  16, 4, 256, 128, 4, 2, 0, nul, need, nul, nul)
+    assert rc == -1 and "null pointer" in _capi.last_error()
+    rc = lib.fgs_moe_fused_routed(0, 16, 16, 16, nul, nul, nul, nul, 1.0, 0.0, 16, 16,
+                                  16, 4, 256, 128, 4, 2, 0, 256, need - 1, 16, nul)
+    assert rc == -1 and "workspace" in _capi.last_error()
+    rc = lib.fgs_moe_fused_routed(0, nul, nul, nul, nul, nul, nul, nul, 1.0, 0.0, nul, nul,
+                                  nul, 0, 256, 128, 4, 2, 0, nul, need, nul, nul)
+    assert rc == 0  # no tokens: nothing read or written
+    # routing tuple -> per-slot routing
+    assert lib.fgs_moe_routing_to_topk(nul, nul, nul, 4, 0, 8, nul, nul, nul) == -1
+    assert lib.fgs_moe_routing_to_topk(nul, nul, nul, 4, 2, 2000, nul, nul, nul) == -1
+    assert lib.fgs_moe_routing_to_topk(nul, nul, nul, 4, 2, 8, nul, nul, nul) == -1
+    assert lib.fgs_moe_routing_to_topk(nul, nul, nul, 0, 2, 8, nul, nul, nul) == 0
 
 
 def test_profile_modes():

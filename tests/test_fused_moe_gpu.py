@@ -1,11 +1,14 @@
 """GPU parity of the fused MoE against the CPU oracle.
 
 Shapes: the reference's own test shapes (tests/accuracy_utils.py:114-131,
-seed M+K+N+E+topk as in tests/test_fused_moe.py:66, weights randn*0.1) and
-the five measured layer configurations at full size. Large cases compare a
-sample of tokens: each output row depends only on its own token, so the
-oracle computes exactly those rows (weights stay on the GPU; only touched
-experts are copied to the host).
+seed M+K+N+E+topk as in tests/test_fused_moe.py:66, weights randn*0.1),
+compared on every token as the reference compares them, and the five
+measured layer configurations at full size. Those compare a sample of
+tokens chosen so that every row block the GEMMs run (each expert's last,
+partly filled block included) holds at least one sampled row: each output
+row depends only on its own token, so the oracle computes exactly those
+rows (weights stay on the GPU; only touched experts are copied to the
+host).
 
 Tolerance: |res - ref| <= atol + rtol*s elementwise, where s is the
 magnitude sum_j |w_j * y_j| of the top-k terms an output sums (outputs that
@@ -96,12 +99,14 @@ def _per_slot_ref(x, w1, w2, w, ids, ascending=False, **kw):
 @pytest.mark.parametrize("shape", testing.REF_SHAPES_SMALL + testing.REF_SHAPES_LARGE,
                          ids=lambda s: "M{}_K{}_N{}_E{}_topk{}".format(*s))
 def test_fused_moe_reference_shapes(gpu, shape):
+    """Every output element of every token, as the reference's own test
+    compares them (tests/test_fused_moe.py:98-110)."""
     M, K, N, E, topk = shape
     x, w1, w2, w, ids = _ref_inputs(M, K, N, E, topk, gpu)
     res = flaggems_sglang.fused_moe(x, w1, w2, w, ids)
-    toks = _sample(M)
-    ref = moe_ref.fused_moe(x, w1, w2, w, ids, tokens=toks, return_mag=True)
-    _check(res.cpu()[toks], ref, "bf16", f"ref-shape {shape}")
+    ref = moe_ref.fused_moe(x, w1, w2, w, ids, return_mag=True)
+    assert res.shape == (M, K)
+    _check(res.cpu(), ref, "bf16", f"ref-shape {shape}")
 
 
 @pytest.mark.parametrize("shape", testing.REF_SHAPES_SMALL,
@@ -116,21 +121,58 @@ def test_fused_moe_input_gate(gpu, shape):
     _check(res.cpu(), ref, "bf16", f"input-gate {shape}")
 
 
-@pytest.mark.parametrize("shape", testing.REF_SHAPES_SMALL + [(64, 1280, 3072, 64, 8)],
+def _row_sorted(w, ids):
+    """Each token's slots by ascending expert id (the routing tuple's flat
+    order, ops/fused_moe.py:130), as (weights, ids) on the same device."""
+    sid, order = torch.sort(ids.long(), dim=1)
+    return torch.gather(w, 1, order), sid.to(torch.int32)
+
+
+@pytest.mark.parametrize("on_input", [False, True], ids=["out-gate", "in-gate"])
+@pytest.mark.parametrize("shape", testing.REF_SHAPES_SMALL + testing.REF_SHAPES_LARGE,
                          ids=lambda s: "M{}_K{}_N{}_E{}_topk{}".format(*s))
-def test_triton_kernel_fused_experts_compat(gpu, shape):
+def test_triton_kernel_fused_experts_compat(gpu, shape, on_input):
     """Reference signature and layouts: w1 [E, K, 2N], w2 [E, N, K] and the
-    (RoutingData, GatherIndx, ScatterIndx) routing format."""
+    (RoutingData, GatherIndx, ScatterIndx) routing format, consumed directly
+    (fgs_moe_fused_routed). Every token against the oracle, and bit for bit
+    against fused_moe on the same routing in the tuple's slot order (same
+    kernels, same row order, same slot order in the sum)."""
     M, K, N, E, topk = shape
+    if on_input and shape not in testing.REF_SHAPES_SMALL:
+        pytest.skip("the reference tests the input gate on its small shapes only")
     x, w1, w2, w, ids = _ref_inputs(M, K, N, E, topk, gpu)
     w1_ref = w1.transpose(1, 2).contiguous()
     w2_ref = w2.transpose(1, 2).contiguous()
     rd, gi, si = flaggems_sglang.standard_topk_to_routing(w, ids, E)
-    res = flaggems_sglang.triton_kernel_fused_experts(x, w1_ref, w2_ref, rd, gi, si)
+    res = flaggems_sglang.triton_kernel_fused_experts(
+        x, w1_ref, w2_ref, rd, gi, si, apply_router_weight_on_input=on_input)
+    ref = moe_ref.fused_moe(x, w1, w2, w, ids, apply_router_weight_on_input=on_input,
+                            return_mag=True)
+    _check(res.cpu(), ref, "bf16", f"compat {shape} on_input={on_input}")
+    sw, sids = _row_sorted(w, ids)
+    res_native = flaggems_sglang.fused_moe(x, w1, w2, sw, sids,
+                                           apply_router_weight_on_input=on_input)
+    assert torch.equal(res, res_native)
+
+
+def test_triton_kernel_fused_experts_dropped_slot(gpu):
+    """A tuple from standard_topk_to_routing with unrouted slots (-1: they go
+    behind the last expert, outside every token_offs_raw range) gives what
+    fused_moe gives for the same slots, bit for bit, and the inverse hands
+    the -1 back."""
+    M, K, N, E, topk = 48, 256, 512, 8, 2
+    x, w1, w2, w, ids = _ref_inputs(M, K, N, E, topk, gpu)
+    ids = ids.clone()
+    ids[::4, 0] = -1
+    rd, gi, si = flaggems_sglang.standard_topk_to_routing(w, ids, E)
+    tw, ti = fm._routing_to_topk(rd, gi, M)
+    sw, sids = _row_sorted(w, ids)
+    assert torch.equal(ti, sids) and torch.equal(tw, sw)
+    res = flaggems_sglang.triton_kernel_fused_experts(
+        x, w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous(), rd, gi, si)
+    assert torch.equal(res, flaggems_sglang.fused_moe(x, w1, w2, sw, sids))
     ref = moe_ref.fused_moe(x, w1, w2, w, ids, return_mag=True)
-    _check(res.cpu(), ref, "bf16", f"compat {shape}")
-    res_native = flaggems_sglang.fused_moe(x, w1, w2, w, ids)
-    _check(res.cpu(), res_native.cpu(), "bf16", "compat vs native")
+    _check(res.cpu(), ref, "bf16", "compat dropped slots")
 
 
 @pytest.mark.parametrize("sched", [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL, 0],
@@ -720,6 +762,40 @@ CONFIG_CASES = [("small", 64)] + [
 ]
 
 
+_QMODE = {"bf16": _capi.QMODE_BF16, "fp8": _capi.QMODE_FP8_BLOCK,
+          "int8": _capi.QMODE_INT8_CHANNEL}
+_TILE_ROWS = {0: 256, 1: 128, 2: 64, 3: 32, 4: 160}
+
+
+def _schedule_block(M, cfg):
+    """Rows per GEMM row block of the schedule a call of this shape runs."""
+    sched = _capi.schedule(M, cfg.K, cfg.N, cfg.E, cfg.topk, _QMODE[cfg.mode])
+    if sched.startswith("tiled"):
+        return _TILE_ROWS[int(sched.split("cfg=")[1].split()[0])]
+    if sched.startswith("stream"):
+        return 16 * int(sched.split("mt=")[1].split()[0])
+    return None  # one token: no alignment
+
+
+def block_cover_tokens(topk_ids, E, block):
+    """Tokens whose slots hit every half of every row block of the padded
+    expert order (the alignment of ``block`` rows; the halves are the
+    128-row tiles fp8's GEMM2 runs on 256-row blocks): for each half that
+    holds a live row, the token of its last live row -- for an expert's
+    last, partly filled block that is the row next to the padding."""
+    ids = topk_ids.cpu().numpy()
+    numel, topk = ids.size, ids.shape[1]
+    s, _, npp = moe_ref.align(ids, E, block)
+    half = max(block // 2, 1)
+    toks = set()
+    for b in range(0, npp, half):
+        seg = s[b:b + half]
+        live = seg[seg < numel]
+        if live.size:
+            toks.add(int(live[-1]) // topk)
+    return toks
+
+
 @pytest.mark.parametrize("name,M", CONFIG_CASES, ids=[f"{n}-M{m}" for n, m in CONFIG_CASES])
 def test_fused_moe_configs(gpu, name, M):
     cfg = testing.CONFIGS[name]
@@ -729,6 +805,12 @@ def test_fused_moe_configs(gpu, name, M):
                                     seed=M + cfg.K + cfg.N + cfg.E + cfg.topk)
     res = flaggems_sglang.fused_moe(x, wts.w1, wts.w2, tw, ti, **wts.kwargs(cfg.mode))
     toks = _sample(M, 8 if cfg.mode == "fp8" else 16)
+    block = _schedule_block(M, cfg)
+    if M == max(cfg.Ms) and block is not None:
+        cover = block_cover_tokens(ti, cfg.E, block)
+        toks = sorted(set(toks) | cover)
+        print(f"{name} M={M}: {len(toks)} tokens cover every half of the "
+              f"{block}-row blocks")
     ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, mode=cfg.mode,
                             w1_scale=wts.w1_scale, w2_scale=wts.w2_scale,
                             tokens=toks, return_mag=True)

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from flaggems_sglang import ops  # noqa: F401
+from flaggems_sglang import _capi, ops  # noqa: F401
 from flaggems_sglang.ops import fused_moe as fm
 from oracle import moe_ref
 
@@ -234,8 +234,47 @@ def test_standard_topk_to_routing_bit_exact(gpu, M, k, E, drop):
     for bm in moe_ref.ROUTING_BLOCK_MS:
         assert np.array_equal(ed.token_offs_pad[bm].cpu().numpy(), pad[bm])
         assert np.array_equal(ed.block_pid_map[bm].cpu().numpy(), pid[bm])
-    if M and not drop:
+    if M:
+        # the inverse (fgs_moe_routing_to_topk) rebuilds the row-sorted
+        # routing, unrouted slots as -1 (they sit past the histogram's total)
         tw, ti = fm._routing_to_topk(rd, gi, M)
-        order = torch.argsort(ids.long(), dim=1)
-        assert torch.equal(ti.cpu().long(), torch.gather(ids.long(), 1, order))
+        _, _, _, rid, rwt = moe_ref.routing_order(gate_scal, topk_indx, hist, M * k, 1)
+        assert np.array_equal(ti.cpu().numpy().reshape(-1), rid)
+        assert np.array_equal(tw.cpu().numpy().reshape(-1), rwt)
+        key = torch.where((ids >= 0) & (ids < E), ids.long(), torch.full_like(ids.long(), -1))
+        sid, order = torch.sort(key, dim=1)
+        assert torch.equal(ti.cpu().long(), sid)
         assert torch.equal(tw.cpu(), torch.gather(w, 1, order))
+
+
+@pytest.mark.parametrize("M,k,E,bad", [(9, 4, 16, None), (300, 8, 128, None),
+                                       (64, 2, 8, "over"), (64, 2, 8, "neg"),
+                                       (64, 2, 8, "src")])
+def test_routing_to_topk_bit_exact_with_bad_tuples(gpu, M, k, E, bad):
+    """fgs_moe_routing_to_topk against the oracle's routing_order on tuples a
+    caller may get wrong: a histogram summing past the gate count, negative
+    counts, gather entries out of range (clamped / skipped, never read or
+    written out of bounds)."""
+    w, ids = _routing(M, E, k, M + k + E, "cpu")
+    gate_scal, topk_indx, _, hist = moe_ref.topk_to_routing(w, ids, E)
+    hist, topk_indx = hist.copy(), topk_indx.copy()
+    if bad == "over":
+        hist[0] += 40
+    elif bad == "neg":
+        hist[1] = -5
+    elif bad == "src":
+        topk_indx[3] = M * k + 7
+        topk_indx[5] = -2
+    _, _, _, rid, rwt = moe_ref.routing_order(gate_scal, topk_indx, hist, M * k, 1)
+    written = rid != -7
+    lib = _capi.load()
+    dev = lambda a: torch.from_numpy(a).to(gpu)
+    gs, src, hs = dev(gate_scal), dev(topk_indx), dev(hist)
+    tw = torch.full((M * k,), 9.0, device=gpu)
+    ti = torch.full((M * k,), -7, dtype=torch.int32, device=gpu)
+    _capi.check(lib.fgs_moe_routing_to_topk(gs.data_ptr(), src.data_ptr(), hs.data_ptr(), M,
+                                            k, E, tw.data_ptr(), ti.data_ptr(), None),
+                "routing_to_topk")
+    torch.cuda.synchronize()
+    assert np.array_equal(ti.cpu().numpy(), rid)
+    assert np.array_equal(tw.cpu().numpy()[written], rwt[written])

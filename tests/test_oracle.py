@@ -45,11 +45,17 @@ def test_align_known_answer_dropped_and_empty():
 
 def _reference_routing_steps(topk_weights, topk_ids, n_expts_tot):
     """The reference's conversion steps (ops/fused_moe.py:130-139) run with
-    torch library ops: per-row sort, stable argsort, gather, histc."""
+    torch library ops: per-row sort, stable argsort, gather, histc. The
+    argsort key relabels ids outside [0, E) as E (the one change the
+    restatement makes, for slots the reference's callers never produce:
+    they must sit behind expert E-1, outside every token_offs_raw range);
+    ids in range are the reference's own keys."""
     expt_indx_2d, sort_indices = torch.sort(topk_ids, dim=1)
     expt_scal = torch.gather(topk_weights, 1, sort_indices).reshape(-1)
     expt_indx = expt_indx_2d.reshape(-1).to(torch.int32)
-    topk_indx = torch.argsort(expt_indx, stable=True)
+    key = torch.where((expt_indx >= 0) & (expt_indx < n_expts_tot), expt_indx,
+                      torch.full_like(expt_indx, n_expts_tot))
+    topk_indx = torch.argsort(key, stable=True)
     gate_scal = expt_scal[topk_indx]
     hist = torch.histc(expt_indx.float(), bins=n_expts_tot,
                        max=n_expts_tot - 1).int()
@@ -90,7 +96,7 @@ def test_align_matches_reference_stable_order(M, k, E, B):
 def test_topk_to_routing_matches_reference_steps(M, k, E, drop):
     """The loop restatement equals the reference's conversion re-run with
     torch library ops (sort, stable argsort, gather, histc), including slots
-    marked -1 (not routed), which the reference's stable argsort puts first."""
+    marked -1 (not routed), which go behind the last expert."""
     g = torch.Generator().manual_seed(M * 31 + k + E)
     w, ids = moe_ref.route(torch.randn(M, E, generator=g), k)
     ids = ids.long()
@@ -102,6 +108,58 @@ def test_topk_to_routing_matches_reference_steps(M, k, E, drop):
     assert np.array_equal(gate_scal, r_scal.numpy())
     assert np.array_equal(hist, r_hist.numpy())
     assert np.array_equal(gate_indx, torch.argsort(r_indx, stable=True).numpy())
+
+
+def test_topk_to_routing_dropped_known_answer_round_trip():
+    """Hand-worked: ids [[2, -1], [0, 1], [1, 3]], E = 4. Row-sorted flat ids
+    [-1, 2, 0, 1, 1, 3]; the unrouted slot (flat 0) goes last:
+    topk_indx [2, 3, 4, 1, 5, 0], hist [1, 2, 1, 1]. routing_order gives
+    every slot back its id (-1 for flat 0: past the histogram's total) and
+    weight, and the padded order of align() on the row-sorted ids."""
+    w = torch.tensor([[0.25, 0.75], [0.5, 0.5], [0.125, 0.875]])
+    ids = torch.tensor([[2, -1], [0, 1], [1, 3]])
+    gate_scal, topk_indx, gate_indx, hist = moe_ref.topk_to_routing(w, ids, 4)
+    assert topk_indx.tolist() == [2, 3, 4, 1, 5, 0]
+    assert hist.tolist() == [1, 2, 1, 1]
+    assert gate_indx.tolist() == [5, 3, 0, 1, 2, 4]
+    assert gate_scal.tolist() == [0.5, 0.5, 0.125, 0.25, 0.875, 0.75]
+    s, e, npp, rid, rw = moe_ref.routing_order(gate_scal, topk_indx, hist, 6, 2)
+    assert rid.tolist() == [-1, 2, 0, 1, 1, 3]  # row-sorted: token 0 is [-1, 2]
+    assert rw.tolist() == [0.75, 0.25, 0.5, 0.5, 0.125, 0.875]
+    s_ref, e_ref, npp_ref = moe_ref.align(np.array([[-1, 2], [0, 1], [1, 3]]), 4, 2)
+    assert npp == npp_ref == 8 and s.tolist() == s_ref.tolist()
+    assert e.tolist() == e_ref.tolist()
+
+
+@pytest.mark.parametrize("M,k,E,B", [(1, 2, 8, 16), (33, 4, 16, 32), (100, 8, 128, 64),
+                                     (257, 2, 8, 256), (64, 8, 256, 1)])
+def test_routing_order_inverts_topk_to_routing(M, k, E, B):
+    """Round trip: routing_order(topk_to_routing(w, ids)) gives the row-sorted
+    (weights, ids) back bit for bit, and its padded order equals align() of
+    the row-sorted ids (align is pinned separately), dropped slots included."""
+    g = torch.Generator().manual_seed(M + k + E + B)
+    w, ids = moe_ref.route(torch.randn(M, E, generator=g), k)
+    ids = ids.long()
+    ids[::5, -1] = -1
+    gate_scal, topk_indx, _, hist = moe_ref.topk_to_routing(w, ids, E)
+    s, e, npp, rid, rw = moe_ref.routing_order(gate_scal, topk_indx, hist, M * k, B)
+    sid, order = torch.sort(ids, dim=1)
+    sw = torch.gather(w, 1, order)
+    assert rid.tolist() == sid.reshape(-1).tolist()
+    assert torch.equal(torch.from_numpy(rw), sw.reshape(-1))
+    s_ref, e_ref, npp_ref = moe_ref.align(sid.numpy(), E, B)
+    assert npp == npp_ref and s.tolist() == s_ref.tolist() and e.tolist() == e_ref.tolist()
+
+
+def test_routing_order_clamps_a_bad_histogram():
+    """Counts summing past n_gates are cut at n_gates; negative counts read
+    as 0; out-of-range src entries become pads."""
+    src = np.array([3, 0, 9, 1], dtype=np.int32)
+    s, e, npp, rid, rw = moe_ref.routing_order(np.ones(4, np.float32), src, [-2, 3, 5], 4, 2)
+    # h = [0, 3, 1]: expert 1 reads positions 0..2, expert 2 position 3
+    assert npp == 6 and s[:6].tolist() == [3, 0, 4, 4, 1, 4]
+    assert e.tolist() == [1, 1, 2]  # max_padded = 4 + 3 * 1 = 7: three blocks
+    assert rid.tolist() == [1, 2, -7, 1]  # slot 2 is never named by src
 
 
 def test_expt_data_known_answer():
@@ -459,6 +517,142 @@ def test_moe_slot_order_and_dropped_slots():
     w1only[:, 1] = 0
     assert torch.equal(moe_ref.fused_moe(x, w1, w2, w, ids2),
                        moe_ref.fused_moe(x, w1, w2, w1only, ids))
+
+
+# ------------------------------------- quantised modes, float64 brute force ---
+def _e4m3_table():
+    vals = sorted({_e4m3fn_decode(c) for c in range(256) if not math.isnan(_e4m3fn_decode(c))})
+    return np.array(vals)
+
+
+def _e4m3_round(v):
+    """Nearest e4m3fn value of float64 v (|v| <= 448), ties to the even code,
+    from the OCP code table (pinned above), not torch's cast."""
+    table = _e4m3_table()
+    even = {_e4m3fn_decode(c) for c in range(256) if c % 2 == 0}
+    out = np.empty_like(v)
+    for i, x in np.ndenumerate(v):
+        d = np.abs(table - x)
+        best = table[d == d.min()]
+        out[i] = best[0] if len(best) == 1 else [b for b in best if b in even][0]
+    return out
+
+
+def _bf16(v):
+    return torch.from_numpy(np.asarray(v, dtype=np.float32)).to(torch.bfloat16).double().numpy()
+
+
+def _bruteforce_quant_moe(x, w1q, w2q, s1, s2, w, ids, mode):
+    """The w8a8 layer in float64 with explicit loops over tokens, slots and
+    scale blocks: weights dequantised element by element (fp8: scale block
+    [r // 128, c // 128] of the [rows, cols] weight; int8: scale of output row
+    r), activations quantised by the definitions (scale = max(amax, 1e-10) /
+    448 per 1x128 group, or / 127 per row, in fp32; fp8 codes by the OCP
+    table, int8 round half to even), GEMM1 output rounded to bf16, silu*up
+    rounded to bf16, re-quantised, GEMM2 rounded to bf16, weighted fp64 sum
+    rounded to bf16."""
+    xd = x.float().double().numpy()
+    T, K = xd.shape
+    N = w2q.shape[2]
+    out = np.zeros((T, K))
+
+    def deq(q, sc, e):
+        qd = q[e].float().double().numpy()
+        R, C = qd.shape
+        sd = sc[e].double().numpy()
+        dq = np.empty((R, C))
+        for r in range(R):
+            if mode == "fp8":
+                for cb in range(C // 128):
+                    dq[r, cb * 128:(cb + 1) * 128] = qd[r, cb * 128:(cb + 1) * 128] * sd[r // 128, cb]
+            else:
+                dq[r] = qd[r] * sd[r]
+        return dq
+
+    def qdq(row):
+        row = row.copy()
+        if mode == "fp8":
+            for g in range(len(row) // 128):
+                seg = row[g * 128:(g + 1) * 128]
+                sc = np.float32(max(np.float32(np.abs(seg).max()), np.float32(1e-10))) / np.float32(448.0)
+                q = _e4m3_round(np.clip((seg.astype(np.float32) / sc).astype(np.float64), -448, 448))
+                row[g * 128:(g + 1) * 128] = q * np.float64(sc)
+            return row
+        sc = np.float32(max(np.float32(np.abs(row).max()), np.float32(1e-10))) / np.float32(127.0)
+        q = np.clip(np.round((row.astype(np.float32) / sc).astype(np.float64)), -127, 127)
+        return q * np.float64(sc)
+
+    cache = {}
+    for t in range(T):
+        xq = qdq(xd[t])
+        for j in range(ids.shape[1]):
+            e = int(ids[t, j])
+            if e not in cache:
+                cache[e] = (deq(w1q, s1, e), deq(w2q, s2, e))
+            W13, W2 = cache[e]
+            h = _bf16(W13 @ xq)
+            g, u = h[:N], h[N:]
+            a = _bf16(g / (1.0 + np.exp(-g)) * u)
+            y = _bf16(W2 @ qdq(a))
+            out[t] += float(w[t, j]) * y
+    return _bf16(out)
+
+
+def _quant_case(mode, K, N, E, seed):
+    x, w1, w2, w, ids = _inputs(10, K, N, E, 2, seed=seed, scale=0.05)
+    quant = moe_ref.quant_weight_fp8_block if mode == "fp8" else moe_ref.quant_weight_int8_channel
+    q1 = [quant(w1[e]) for e in range(E)]
+    q2 = [quant(w2[e]) for e in range(E)]
+    w1q, w2q = torch.stack([a for a, _ in q1]), torch.stack([a for a, _ in q2])
+    s1, s2 = torch.stack([b for _, b in q1]), torch.stack([b for _, b in q2])
+    # scales that differ strongly between blocks / rows, so an operand's
+    # scale read at the wrong index moves the result
+    g = torch.Generator().manual_seed(seed)
+    s1 = s1 * (0.5 + 3 * torch.rand(s1.shape, generator=g))
+    s2 = s2 * (0.5 + 3 * torch.rand(s2.shape, generator=g))
+    return x, w1q, w2q, s1, s2, w, ids
+
+
+def _close_to_bruteforce(got, want):
+    diff = np.abs(got.float().double().numpy() - want)
+    return float(diff.sum() / np.abs(want).sum()), float(diff.max())
+
+
+@pytest.mark.parametrize("mode", ["fp8", "int8"])
+def test_quantised_oracle_matches_float64_bruteforce(mode):
+    """oracle.fused_moe(mode=fp8|int8) against the float64 brute force on
+    non-square shapes (fp8: a 4 x 3 block grid for W13, 3 x 2 for W2; int8:
+    2N != K rows), where a scale read along the wrong axis cannot even be
+    applied. The two differ only where the fp32 and fp64 sums round a bf16
+    intermediate to neighbouring values (then the re-quantised element may
+    move by one grid step)."""
+    x, w1q, w2q, s1, s2, w, ids = _quant_case(mode, 384, 256, 3, 21)
+    got = moe_ref.fused_moe(x, w1q, w2q, w, ids, mode=mode, w1_scale=s1, w2_scale=s2)
+    want = _bruteforce_quant_moe(x, w1q, w2q, s1, s2, w, ids, mode)
+    mean_rel, _ = _close_to_bruteforce(got, want)
+    assert mean_rel <= 1e-4, mean_rel
+
+
+@pytest.mark.parametrize("mode", ["fp8", "int8"])
+def test_quantised_bruteforce_rejects_a_scale_axis_swap(mode, monkeypatch):
+    """On a square shape (2N = K, a 2 x 2 fp8 block grid) a scale applied
+    along the wrong axis keeps its shape; planted in the oracle's weight
+    dequantisation, the brute-force comparison above rejects it."""
+    x, w1q, w2q, s1, s2, w, ids = _quant_case(mode, 256, 128, 3, 22)
+    want = _bruteforce_quant_moe(x, w1q, w2q, s1, s2, w, ids, mode)
+    honest = moe_ref.fused_moe(x, w1q, w2q, w, ids, mode=mode, w1_scale=s1, w2_scale=s2)
+    assert _close_to_bruteforce(honest, want)[0] <= 1e-4
+
+    def swapped(mode_, a1, a2, sc1, sc2, e):
+        a, b = a1[e].cpu(), a2[e].cpu()
+        if mode_ == "fp8":
+            return (moe_ref.dequant_weight_fp8_block(a, sc1[e].cpu().t().contiguous()),
+                    moe_ref.dequant_weight_fp8_block(b, sc2[e].cpu()))
+        return a.float() * sc1[e].cpu().float()[None, :], b.float() * sc2[e].cpu().float()[:, None]
+
+    monkeypatch.setattr(moe_ref, "_expert_weights", swapped)
+    bad = moe_ref.fused_moe(x, w1q, w2q, w, ids, mode=mode, w1_scale=s1, w2_scale=s2)
+    assert _close_to_bruteforce(bad, want)[0] > 5e-2
 
 
 def test_moe_quantised_modes_track_bf16():

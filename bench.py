@@ -8,33 +8,39 @@ with every input already resident in HBM. Prints ONE JSON line:
 * ``value``: TFLOP/s of the whole layer at M=4096 (FLOPs = 6*M*topk*K*N),
   ``ms_per_step`` = ms/layer;
 * ``roofline``: the dominant kernel (largest stage time, measured with HIP
-  events recorded around each stage on the launch stream, over the timed
-  region) against MI355X's peak;
-* ``sweep``: ms/layer, TFLOP/s, GB/s and roofline fractions at every M of
-  the configuration (M = 1 .. 4096), each with its own warmup and timing;
-* ``configs``: the same rows for every other measured configuration
-  (DeepSeek-V3 fp8, Qwen3 bf16 uniform and skewed, Qwen2 int8, the small
-  CPU-sized layer) at each of its M;
+  events the library records around each stage on the launch stream, over
+  the timed calls) against MI355X's peak, with the HBM bytes per launch
+  rocprofv3 counted (``traffic``, ``profiles/traffic_<cfg>.json``) and the
+  MFMA-busy fraction (``profiles/mfma_<cfg>.json``);
 * ``cpu_baseline``: the repo's CPU torch reference (oracle/) on a bounded
-  sample of the same workload, on this host's cores.
+  sample of the headline layer, on this host's cores;
+* ``rows``: one compact row per (configuration, M) -- field names in
+  ``row_fields`` -- for every configuration of
+  flaggems_sglang.testing.CONFIGS: ms/layer, TFLOP/s, GB/s, both roofline
+  fractions, the dominant GEMM with its own fraction, counter traffic and
+  MFMA busy where profiled, the CPU oracle's time on a token sample of the
+  same inputs, the parity of that sample against the GPU output (max abs,
+  mean rel, within tolerance) and whether the alignment of that routing is
+  bit-exact. ``ref_bench`` is the reference's own benchmark
+  (benchmark/test_fused_moe.py:53-73): ``triton_kernel_fused_experts`` on the
+  routing tuple at (M, 1280, 3072, 64, 8), with ``fused_moe`` on the same
+  inputs timed beside it (``ref_fields``).
 
-Each row's ``roofline`` names the dominant kernel (the slower GEMM) with its
-achieved rate against the MI355X peak; where a committed rocprofv3 summary
-covers the shape it also carries ``traffic`` (HBM bytes per launch,
-``profiles/traffic_<cfg>.json``) and ``mfma_busy`` (fraction of SIMD cycles
-the MFMA pipe is busy, ``profiles/mfma_<cfg>.json``).
-
-Options: ``--config`` picks another configuration of
-flaggems_sglang.testing.CONFIGS (its largest M is then the headline),
-``--no-sweep`` / ``--no-configs`` / ``--no-cpu`` skip those legs
-(profiling runs).
+Options: ``--config`` picks another headline configuration (its largest M
+unless ``--m``), ``--no-sweep`` / ``--no-configs`` / ``--no-cpu`` skip those
+legs (profiling runs).
 """
 
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
+
+# the CPU oracle's worker threads sleep as soon as a parallel region ends,
+# so they never compete with the host thread that launches the timed calls
+os.environ.setdefault("OMP_WAIT_POLICY", "PASSIVE")
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 for _p in (ROOT, os.path.join(ROOT, "flaggems-sglang_amd")):
@@ -47,7 +53,18 @@ PEAK_HBM_GBS = 8000.0
 PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0, "int8": 5000.0}
 FLUSH_BYTES = 512 << 20  # > MALL (256 MB): flush between steps when small
 SPIN_CYCLES = 400_000    # ~0.2 ms of GPU spin ahead of each flushed call
-OTHER_CONFIGS = ("deepseek_fp8", "qwen3", "qwen3_skewed", "qwen2_int8", "small")
+OTHER_CONFIGS = ("ref_bench", "deepseek_fp8", "qwen3", "qwen3_skewed", "qwen2_int8",
+                 "small")
+ROW_FIELDS = ("M", "ms", "tflops", "gbs", "frac_hbm", "frac_mfma", "dom", "dom_frac",
+              "traffic", "mfma_busy", "cpu_ms", "cpu_tokens", "max_abs", "mean_rel",
+              "parity", "align_bitexact")
+# ref_bench rows: the reference-signature call, then fused_moe on the same inputs
+REF_FIELDS = ROW_FIELDS + ("ms_fused_moe", "sig_over_fused_moe")
+CPU_SAMPLE = 4  # tokens the per-row CPU oracle runs on
+# untimed calls ahead of each row: the first tens of calls after a new
+# weight set run a few % slow (measured: 30 flushed one-token calls 0.0516
+# ms, the next 30 0.0477)
+SWEEP_WARMUP = 20
 
 
 def log(*a):
@@ -95,13 +112,41 @@ def calibrate_copy():
                       "bytes_written": n, "launches": 3}), flush=True)
 
 
-class Layer:
-    """One configuration's weights plus a token batch, ready to call."""
+def make_config_weights(cfg, dev):
+    """The configuration's weights. ref_bench keeps the reference's layout
+    (w1 [E, K, 2N], w2 [E, N, K], randn * 0.1, as its benchmark builds them);
+    the others the SGLang layout of flaggems_sglang.testing.make_weights."""
+    import torch
 
-    def __init__(self, cfg, weights, M, device, flags=0):
+    from flaggems_sglang import testing
+
+    if cfg.name != "ref_bench":
+        return testing.make_weights(cfg.K, cfg.N, cfg.E, cfg.mode, cfg.w_scale, device=dev)
+    g = torch.Generator(device=dev).manual_seed(cfg.K + cfg.N + cfg.E)
+    w1 = torch.empty((cfg.E, cfg.K, 2 * cfg.N), dtype=torch.bfloat16, device=dev)
+    w2 = torch.empty((cfg.E, cfg.N, cfg.K), dtype=torch.bfloat16, device=dev)
+    for e in range(cfg.E):
+        w1[e] = (torch.randn((cfg.K, 2 * cfg.N), generator=g, device=dev) *
+                 cfg.w_scale).to(torch.bfloat16)
+        w2[e] = (torch.randn((cfg.N, cfg.K), generator=g, device=dev) *
+                 cfg.w_scale).to(torch.bfloat16)
+    return testing.MoEWeights(w1, w2)
+
+
+class Layer:
+    """One configuration's weights plus a token batch, ready to call.
+
+    ``ref_sig``: the call is the reference's entry point,
+    ``triton_kernel_fused_experts(x, w1, w2, routing_data, gather_indx,
+    scatter_indx)`` on reference-layout weights with the routing tuple built
+    (untimed) by standard_topk_to_routing, as the reference's benchmark
+    builds it (benchmark/test_fused_moe.py:26-50)."""
+
+    def __init__(self, cfg, weights, M, device, flags=0, ref_sig=False):
+        import flaggems_sglang
         from flaggems_sglang import testing
 
-        self.cfg, self.w, self.M, self.flags = cfg, weights, M, flags
+        self.cfg, self.w, self.M, self.flags, self.ref_sig = cfg, weights, M, flags, ref_sig
         self.x, self.tw, self.ti = testing.make_tokens(
             M, cfg.K, cfg.E, cfg.topk, cfg.scoring, cfg.hot_experts,
             cfg.hot_bias, device=device, seed=M + cfg.K + cfg.N + cfg.E + cfg.topk)
@@ -110,12 +155,27 @@ class Layer:
         self.bytes = testing.layer_bytes(M, cfg.K, cfg.N, cfg.topk, cfg.mode,
                                          self.ti, cfg.E)
         self.touched = int(self.ti.unique().numel())
+        if ref_sig:
+            self.routing = flaggems_sglang.standard_topk_to_routing(self.tw, self.ti, cfg.E)
+
+    def native_weights(self):
+        """w1 [E, 2N, K], w2 [E, K, N]: for ref_bench the contiguous copies
+        the reference-signature entry converts once and caches."""
+        if self.cfg.name == "ref_bench":
+            from flaggems_sglang.ops import fused_moe as fm
+
+            return fm._native_layout(self.w.w1), fm._native_layout(self.w.w2)
+        return self.w.w1, self.w.w2
 
     def __call__(self):
         import flaggems_sglang
 
-        return flaggems_sglang.fused_moe(self.x, self.w.w1, self.w.w2, self.tw,
-                                         self.ti, _flags=self.flags, **self.kw)
+        if self.ref_sig:
+            return flaggems_sglang.triton_kernel_fused_experts(
+                self.x, self.w.w1, self.w.w2, *self.routing)
+        w1, w2 = self.native_weights()
+        return flaggems_sglang.fused_moe(self.x, w1, w2, self.tw, self.ti,
+                                         _flags=self.flags, **self.kw)
 
 
 def time_layer(layer, steps, warmup, flush, profile_timed=False):
@@ -194,23 +254,12 @@ def _profile_entry(kind, cfg_name, M, stage):
         return json.load(f).get("by_stage", {}).get(f"{cfg_name}:{M}:{stage}") or None
 
 
-def measured_traffic(cfg_name, M, stage):
-    """HBM bytes per launch of a stage's kernel, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/traffic_<cfg>.json,
-    copy-calibrated), or None when that configuration was not profiled."""
-    return _profile_entry("traffic", cfg_name, M, stage)
-
-
-def measured_mfma(cfg_name, M, stage):
-    """MFMA-pipe busy fraction of a stage's kernel from the committed
-    rocprofv3 summary (profiles/mfma_<cfg>.json): SQ_VALU_MFMA_BUSY_CYCLES
-    over the SIMD-cycles of the dispatch (GRBM_GUI_ACTIVE per XCD times the
-    1024 SIMDs), or None when not profiled."""
-    return _profile_entry("mfma", cfg_name, M, stage)
-
-
 def dominant(layer, stages):
-    """Roofline object for the slowest stage (a GEMM in every config)."""
+    """Roofline object for the slowest stage (a GEMM in every config):
+    achieved rate of its algorithmic FLOPs or bytes per launch over its
+    event-measured average, the peak, and -- where a committed rocprofv3
+    summary covers the shape -- the counted HBM bytes per launch and the
+    MFMA-busy fraction."""
     cfg = layer.cfg
     name = max(("gemm1", "gemm2"), key=lambda s: stages.get(s, 0.0))
     t = stages[name] * 1e-3
@@ -224,53 +273,183 @@ def dominant(layer, stages):
         flops = 2.0 * M * k * K * N
         wbytes = layer.touched * K * N * bw
         io = M * k * N * bw + M * k * K * 2
+    alg = wbytes + io
     tflops = flops / t / 1e12
-    gbs = (wbytes + io) / t / 1e9
+    gbs = alg / t / 1e9
     frac_mfma = tflops / PEAK_TFLOPS[cfg.mode]
     frac_hbm = gbs / PEAK_HBM_GBS
-    meas = measured_traffic(cfg.name, M, name)
+    meas = _profile_entry("traffic", cfg.name, M, name)
     traffic = None if meas is None else round(meas["fetch_bytes"] + meas["write_bytes"])
-    mf = measured_mfma(cfg.name, M, name)
-    extra = {"algorithmic_bytes": round(wbytes + io),
-             "traffic_source": None if meas is None else
-             "profiles/traffic_%s.json: rocprofv3 FETCH_SIZE + WRITE_SIZE per "
-             "dispatch, scaled by a 1 GiB copy (profiled avg %.4f ms)"
-             % (cfg.name, meas["avg_ns"] / 1e6),
-             "mfma_busy": None if mf is None else round(mf["mfma_busy"], 4),
-             "valu_per_mfma": None if mf is None else round(mf["valu_per_mfma"], 2),
-             "mfma_source": None if mf is None else
-             "profiles/mfma_%s.json: rocprofv3 SQ_VALU_MFMA_BUSY_CYCLES / "
-             "(GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs) per dispatch" % cfg.name}
-    if frac_mfma >= frac_hbm:
-        return {"kernel": f"moe_gemm ({name})", "bound": "mfma",
-                "achieved": round(tflops, 2), "peak": PEAK_TFLOPS[cfg.mode],
-                "unit": "TFLOP/s", "frac": round(frac_mfma, 4), "traffic": traffic,
-                "per_unit": f"{'4' if name == 'gemm1' else '2'}*M*topk*K*N flops",
-                "avg_ms": round(stages[name], 4), **extra}
-    return {"kernel": f"moe_gemm ({name})", "bound": "hbm",
-            "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(frac_hbm, 4), "traffic": traffic,
-            "per_unit": "touched_experts * weight bytes + activations",
-            "avg_ms": round(stages[name], 4), **extra}
+    mf = _profile_entry("mfma", cfg.name, M, name)
+    mfma = frac_mfma >= frac_hbm
+    return {"kernel": f"moe_gemm ({name})", "stage": name,
+            "bound": "mfma" if mfma else "hbm",
+            "achieved": round(tflops if mfma else gbs, 2),
+            "peak": PEAK_TFLOPS[cfg.mode] if mfma else PEAK_HBM_GBS,
+            "unit": "TFLOP/s" if mfma else "GB/s",
+            "frac": round(frac_mfma if mfma else frac_hbm, 4),
+            "traffic": traffic, "algorithmic_bytes": round(alg),
+            "traffic_ratio": None if traffic is None else round(traffic / alg, 3),
+            "mfma_busy": None if mf is None else round(mf["mfma_busy"], 4),
+            "avg_ms": round(stages[name], 4)}
 
 
-def row(layer, ms, stages):
+def _sample_tokens(M, n=CPU_SAMPLE):
+    return sorted({0, M // 3, (2 * M) // 3, M - 1})[:n] if M > n else list(range(M))
+
+
+def cpu_check(layer, out, cpu_w):
+    """The CPU oracle on a token sample of the row's own inputs: its time,
+    and its parity against the GPU output of the same call. Returns
+    (cpu_ms, tokens, max_abs, mean_rel, ok)."""
+    from flaggems_sglang import testing
+    from oracle import moe_ref
+
     cfg = layer.cfg
+    toks = _sample_tokens(layer.M)
+    x, tw, ti = layer.x.cpu(), layer.tw.cpu(), layer.ti.cpu()
+    t0 = time.perf_counter()
+    ref, mag = moe_ref.fused_moe(x, cpu_w.w1, cpu_w.w2, tw, ti, mode=cfg.mode,
+                                 w1_scale=cpu_w.w1_scale, w2_scale=cpu_w.w2_scale,
+                                 tokens=toks, return_mag=True)
+    dt = (time.perf_counter() - t0) * 1e3
+    tol = testing.TOL[cfg.mode]
+    ok, max_abs, mean_rel = moe_ref.compare(out.cpu()[toks], ref, tol["atol"], tol["rtol"],
+                                            mag)
+    ok = ok and mean_rel <= tol["mean_rel"]
+    return dt, len(toks), max_abs, mean_rel, ok
+
+
+def align_check(layer):
+    """moe_align_block_size (HIP) on the row's routing against the oracle's
+    C restatement, at the block size the call's schedule uses: bit-exact?"""
+    import flaggems_sglang
+    from flaggems_sglang import _capi
+    from oracle import moe_ref
+
+    cfg = layer.cfg
+    qm = {"bf16": _capi.QMODE_BF16, "fp8": _capi.QMODE_FP8_BLOCK,
+          "int8": _capi.QMODE_INT8_CHANNEL}[cfg.mode]
+    sched = _capi.schedule(layer.M, cfg.K, cfg.N, cfg.E, cfg.topk, qm)
+    block = 16
+    if sched.startswith("tiled"):
+        block = {0: 256, 1: 128, 2: 64, 3: 32, 4: 160}[int(sched.split("cfg=")[1].split()[0])]
+    elif sched.startswith("stream"):
+        block = 16 * int(sched.split("mt=")[1].split()[0])
+    s, e, npp = flaggems_sglang.moe_align_block_size(layer.ti, cfg.E, block)
+    rs, re_, rnpp = moe_ref.align(layer.ti.cpu().numpy(), cfg.E, block)
+    n = int(npp.item())
+    return (n == rnpp and bool((s.cpu().numpy() == rs).all())
+            and bool((e.cpu().numpy() == re_).all()))
+
+
+def rates(layer, ms):
+    """ms/layer and the layer's TFLOP/s, GB/s and roofline fractions."""
     t = ms * 1e-3
     tflops = layer.flops / t / 1e12
     gbs = layer.bytes / t / 1e9
-    return {
-        "M": layer.M, "ms": round(ms, 4), "tflops": round(tflops, 2),
-        "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
-        "frac_mfma": round(tflops / PEAK_TFLOPS[cfg.mode], 4),
-        "experts_touched": layer.touched,
-        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
-    }
+    return {"M": layer.M, "ms": round(ms, 4), "tflops": round(tflops, 2),
+            "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+            "frac_mfma": round(tflops / PEAK_TFLOPS[layer.cfg.mode], 4)}
 
 
-def cpu_baseline(layer, budget_s=25.0):
+def measure_row(layer, args):
+    """GPU part of one row of ROW_FIELDS (timing with the profiler off, the
+    stage split from a second pass, the output of one more call for the
+    parity check, the alignment check). Returns (row, stages, output)."""
+    flush = layer.bytes < FLUSH_BYTES
+    ms, stages = time_layer(layer, args.sweep_steps, SWEEP_WARMUP, flush)
+    dom = dominant(layer, stages)
+    row = {**rates(layer, ms),
+           "dom": dom["stage"], "dom_frac": dom["frac"], "traffic": dom["traffic"],
+           "mfma_busy": dom["mfma_busy"], "cpu_ms": None, "cpu_tokens": None,
+           "max_abs": None, "mean_rel": None, "parity": None,
+           "align_bitexact": align_check(layer)}
+    return row, stages, layer().cpu()
+
+
+def cpu_row(row, layer, out, cpu_w):
+    """CPU part of a row: the oracle's time and parity on the token sample."""
+    cms, n, max_abs, mean_rel, ok = cpu_check(layer, out, cpu_w)
+    row.update(cpu_ms=round(cms, 1), cpu_tokens=n, max_abs=round(max_abs, 5),
+               mean_rel=float(f"{mean_rel:.3g}"), parity=ok)
+
+
+def host_weights(cfg, weights):
+    """The configuration's weights on the host for the CPU oracle (bf16
+    weights as fp32 once, so the oracle's per-expert conversion is free;
+    fp8 / int8 stay quantised: the oracle dequantises the experts it
+    touches)."""
+    from flaggems_sglang import testing
+
+    w1, w2 = weights.w1, weights.w2
+    if cfg.name == "ref_bench":
+        w1, w2 = w1.transpose(1, 2), w2.transpose(1, 2)
+    if cfg.mode == "bf16":
+        return testing.MoEWeights(w1.cpu().float(), w2.cpu().float())
+    return testing.MoEWeights(w1.cpu(), w2.cpu(), weights.w1_scale.cpu(),
+                              weights.w2_scale.cpu())
+
+
+def sweep_config(cfg, dev, args, weights=None, cpu_w=None):
+    """Rows of one configuration at each of its M (compact lists in
+    ROW_FIELDS / REF_FIELDS order); its weights are freed after."""
+    import torch
+
+    t0 = time.perf_counter()
+    own = weights is None
+    if own:
+        weights = make_config_weights(cfg, dev)
+        torch.cuda.synchronize()
+    log(f"{cfg.name}: weights {weights.nbytes() / 1e9:.2f} GB in "
+        f"{time.perf_counter() - t0:.1f}s")
+    # every GPU measurement of the configuration first, then the CPU oracle
+    rows, done = [], []
+    for m in cfg.Ms:
+        ref_sig = cfg.name == "ref_bench"
+        lay = Layer(cfg, weights, m, dev, args.flags, ref_sig=ref_sig)
+        if ref_sig:
+            # both paths warm before either is timed
+            for sig in (False, True):
+                lay.ref_sig = sig
+                for _ in range(SWEEP_WARMUP):
+                    lay()
+        r, st, out = measure_row(lay, args)
+        if ref_sig:
+            # the same inputs through fused_moe, alternating with the
+            # reference-signature call three times each (medians), so a
+            # drift of the device state between passes favours neither
+            flush = lay.bytes < FLUSH_BYTES
+            t_sig, t_nat = [r["ms"]], []
+            for sig in (False, True, False, True, False):
+                lay.ref_sig = sig
+                (t_sig if sig else t_nat).append(
+                    time_layer(lay, args.sweep_steps, SWEEP_WARMUP, flush)[0])
+            ms_s, ms_n = statistics.median(t_sig), statistics.median(t_nat)
+            r.update(**rates(lay, ms_s), ms_fused_moe=round(ms_n, 4),
+                     sig_over_fused_moe=round(ms_s / ms_n, 4))
+        log(f"{cfg.name} M={m}: {json.dumps(r)} stages={json.dumps(st)}")
+        done.append((r, lay, out))
+    if not args.no_cpu:
+        if cpu_w is None:
+            cpu_w = host_weights(cfg, weights)
+        for r, lay, out in done:
+            cpu_row(r, lay, out, cpu_w)
+            log(f"{cfg.name} M={lay.M} cpu: {r['cpu_ms']} ms on {r['cpu_tokens']} tokens, "
+                f"max_abs={r['max_abs']} mean_rel={r['mean_rel']} parity={r['parity']}")
+    fields = REF_FIELDS if cfg.name == "ref_bench" else ROW_FIELDS
+    rows = [[r[f] for f in fields] for r, _, _ in done]
+    if own:
+        del weights
+    done = None
+    torch.cuda.empty_cache()
+    return rows
+
+
+def cpu_baseline(layer, cpu_w, budget_s=25.0):
     """The repo's CPU torch reference (oracle/) on a bounded token sample of
-    the same layer, on every core this process may use."""
+    the headline layer, on every core this process may use: the median of
+    three runs (one when a run takes more than a third of the budget)."""
     import torch
 
     from oracle import moe_ref
@@ -278,58 +457,25 @@ def cpu_baseline(layer, budget_s=25.0):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     cfg = layer.cfg
-    x = layer.x.cpu()
-    tw, ti = layer.tw.cpu(), layer.ti.cpu()
-    w1 = layer.w.w1.cpu()
-    w2 = layer.w.w2.cpu()
-    s1 = layer.w.w1_scale.cpu() if layer.w.w1_scale is not None else None
-    s2 = layer.w.w2_scale.cpu() if layer.w.w2_scale is not None else None
+    x, tw, ti = layer.x.cpu(), layer.tw.cpu(), layer.ti.cpu()
     n = min(layer.M, 512)
     toks = list(range(n))
-    t0 = time.perf_counter()
-    moe_ref.fused_moe(x, w1, w2, tw, ti, mode=cfg.mode, w1_scale=s1,
-                      w2_scale=s2, tokens=toks)
-    dt = time.perf_counter() - t0
-    reps = 1
-    if dt * 2 < budget_s:
+    times = []
+    for _ in range(3):
         t0 = time.perf_counter()
-        moe_ref.fused_moe(x, w1, w2, tw, ti, mode=cfg.mode, w1_scale=s1,
-                          w2_scale=s2, tokens=toks)
-        dt = min(dt, time.perf_counter() - t0)
-        reps = 2
+        moe_ref.fused_moe(x, cpu_w.w1, cpu_w.w2, tw, ti, mode=cfg.mode,
+                          w1_scale=cpu_w.w1_scale, w2_scale=cpu_w.w2_scale, tokens=toks)
+        times.append(time.perf_counter() - t0)
+        if times[0] * 3 > budget_s:
+            break
+    dt = statistics.median(times)
     flops = 6.0 * n * cfg.topk * cfg.K * cfg.N
     return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s",
             "cores": torch.get_num_threads(), "kind": "port",
             "ms_per_layer_sample": round(dt * 1e3, 1),
             "sample": f"oracle.moe_ref.fused_moe (torch fp32 on CPU) on the first "
                       f"{n} of {layer.M} tokens of the same {cfg.name} layer, "
-                      f"best of {reps}"}
-
-
-def sweep_config(cfg, dev, args):
-    """Rows (ms/layer, TFLOP/s, GB/s, roofline fractions, dominant kernel)
-    of one configuration at each of its M; its weights are freed after."""
-    import torch
-
-    from flaggems_sglang import testing
-
-    t0 = time.perf_counter()
-    weights = testing.make_weights(cfg.K, cfg.N, cfg.E, cfg.mode, cfg.w_scale,
-                                   device=dev)
-    torch.cuda.synchronize()
-    log(f"{cfg.name}: weights {weights.nbytes() / 1e9:.2f} GB in "
-        f"{time.perf_counter() - t0:.1f}s")
-    rows = []
-    for m in cfg.Ms:
-        lay = Layer(cfg, weights, m, dev, args.flags)
-        sms, sst = time_layer(lay, args.sweep_steps, 3, lay.bytes < FLUSH_BYTES)
-        r = row(lay, sms, sst)
-        r["roofline"] = dominant(lay, sst)
-        rows.append(r)
-        log(f"{cfg.name} M={m}: {json.dumps(r)}")
-    del weights
-    torch.cuda.empty_cache()
-    return rows
+                      f"median of {len(times)}"}
 
 
 # ---------------------------------------------------------------------------
@@ -623,36 +769,31 @@ def main():
     props = torch.cuda.get_device_properties(dev)
     log(f"device: {props.name} CUs={props.multi_processor_count} "
         f"mem={props.total_memory / 2**30:.0f} GiB")
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
     cfg = testing.CONFIGS[args.config]
     M = args.m or max(cfg.Ms)
     t0 = time.perf_counter()
-    weights = testing.make_weights(cfg.K, cfg.N, cfg.E, cfg.mode, cfg.w_scale,
-                                   device=dev)
+    weights = make_config_weights(cfg, dev)
     torch.cuda.synchronize()
     log(f"weights {weights.nbytes() / 1e9:.2f} GB in {time.perf_counter() - t0:.1f}s")
 
-    head = Layer(cfg, weights, M, dev, args.flags)
+    head = Layer(cfg, weights, M, dev, args.flags, ref_sig=cfg.name == "ref_bench")
     small_ws = head.bytes < FLUSH_BYTES
     ms, stages = time_layer(head, args.steps, args.warmup, flush=small_ws,
                             profile_timed=True)
     log(f"headline {cfg.name} M={M}: {ms:.4f} ms/layer stages={stages}")
+    roof = dominant(head, stages)
 
-    sweep, lay = [], None
+    rows = {}
+    cpu_w = None if args.no_cpu else host_weights(cfg, weights)
     if not args.no_sweep:
-        for m in cfg.Ms:
-            lay = head if m == M else Layer(cfg, weights, m, dev, args.flags)
-            flush = lay.bytes < FLUSH_BYTES
-            sms, sst = time_layer(lay, args.sweep_steps, 3, flush)
-            r = row(lay, sms, sst)
-            r["roofline"] = dominant(lay, sst)
-            sweep.append(r)
-            log(f"sweep M={m}: {json.dumps(r)}")
-
+        rows[cfg.name] = sweep_config(cfg, dev, args, weights, cpu_w)
     cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(head)
+    if cpu_w is not None:
+        cpu = cpu_baseline(head, cpu_w)
         log(f"cpu baseline: {cpu}")
-
+    cpu_w = None
     tflops = head.flops / (ms * 1e-3) / 1e12
     out = {
         "metric": METRIC,
@@ -675,19 +816,21 @@ def main():
                    "layer_flops": head.flops, "layer_bytes": head.bytes,
                    "gb_s": round(head.bytes / (ms * 1e-3) / 1e9, 1),
                    "cold_cache": small_ws},
-        "roofline": dominant(head, stages),
+        "roofline": roof,
         "stages_ms": {k: round(v, 4) for k, v in stages.items()},
         "cpu_baseline": cpu,
-        "sweep": sweep,
-        "configs": {},
-        "device": {"name": props.name, "cus": props.multi_processor_count},
+        "device": {"name": props.name, "cus": props.multi_processor_count,
+                   "host_cores": cores},
     }
     if not args.no_configs and args.config == "mixtral" and args.m is None:
-        head = weights = lay = None  # the headline weights go before the next set
+        head = weights = None  # the headline weights go before the next set
         torch.cuda.empty_cache()
         for name in OTHER_CONFIGS:
-            out["configs"][name] = sweep_config(testing.CONFIGS[name], dev, args)
-    print(json.dumps(out), flush=True)
+            rows[name] = sweep_config(testing.CONFIGS[name], dev, args)
+    out["row_fields"] = list(ROW_FIELDS)
+    out["ref_fields"] = list(REF_FIELDS)
+    out["rows"] = rows
+    print(json.dumps(out, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":

@@ -527,14 +527,22 @@ static int run_fused(const FusedArgs& a) {
   if (a.no_profile) g_prof.cur = nullptr;
   else g_prof.begin();
   g_prof.mark(0, a.stream);
-  if (routed) {
+  int32_t* rids = reinterpret_cast<int32_t*>(ws + p.o_rids);
+  const int32_t* route_hist = nullptr;
+  if (routed && p.direct) {
+    // one token: its gathered order is its slots' ascending expert order,
+    // so GEMM rows are gathered positions, weighted by gate_scal as it
+    // stands; GEMM1 finds each position's expert from the histogram and
+    // records it (rids) for GEMM2 and the top-k sum -- no extra launch
+    topk_w = a.gate_scal;
+    topk_ids = rids;
+    route_hist = a.expt_hist;
+  } else if (routed) {
     // the routing tuple's gathered order is the alignment's order: one
     // launch gives the padded order and each slot's expert and gate scale
-    int32_t* rids = reinterpret_cast<int32_t*>(ws + p.o_rids);
     float* rw = reinterpret_cast<float*>(ws + p.o_rw);
     rc = launch_routing_order(a.gate_scal, a.gather_src, a.expt_hist, numel, a.e, p.block_m,
-                              p.max_padded, p.direct ? nullptr : sorted, eids, npp, rids, rw,
-                              a.stream);
+                              p.max_padded, sorted, eids, npp, rids, rw, a.stream);
     if (rc) return rc;
     topk_w = rw;
     topk_ids = rids;
@@ -575,7 +583,7 @@ static int run_fused(const FusedArgs& a) {
   }
 
   g_prof.mark(2, a.stream);
-  if (p.fused1) {
+  if (p.fused1 && !routed) {
     DecodeParams d{};
     d.x = a.x;
     d.w13 = a.w13;
@@ -631,6 +639,8 @@ static int run_fused(const FusedArgs& a) {
   if (p.direct) {
     // slot j is row tile j; a2 holds the compact slot rows
     g1.direct_ids = topk_ids;
+    g1.route_hist = route_hist;
+    g1.route_ids = rids;
   }
   if (p.qfold1) g1.a_src = static_cast<const uint16_t*>(a.x);
   rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, static_cast<int>(p.n_launch),
@@ -670,6 +680,7 @@ static int run_fused(const FusedArgs& a) {
 
   g_prof.mark(4, a.stream);
   GemmParams g2 = g1;
+  g2.route_hist = nullptr;
   g2.a = act2;
   g2.a_scale = act2_scale;
   g2.w = static_cast<const uint8_t*>(a.w2);

@@ -37,6 +37,34 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
          (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
 }
 
+// The expert whose range of a routing tuple's gathered order holds position
+// j: expert e owns [raw[e], raw[e] + h[e]) with raw the running sums of the
+// histogram (token_offs_raw, the ranges matmul_ogs reads; counts clamped as
+// the routing-order kernel clamps them: negative -> 0, sums capped at
+// numel); -1 past the total. A wave-wide computation (64 experts per step,
+// DPP-free shuffles); every lane of the wave returns the same value.
+__device__ __forceinline__ int routed_expert_of(const int32_t* __restrict__ hist,
+                                                int num_experts, int64_t numel, int64_t j) {
+  const int lane = threadIdx.x & 63;
+  int64_t base = 0;
+  for (int e0 = 0; e0 < num_experts; e0 += 64) {
+    const int e = e0 + lane;
+    const int64_t h = e < num_experts ? static_cast<int64_t>(max(hist[e], 0)) : 0;
+    int64_t s = h < numel ? h : numel;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int64_t o = __shfl_up(s, d, 64);
+      if (lane >= d) s += o;
+    }
+    const int64_t incl = base + s < numel ? base + s : numel;
+    const uint64_t hit = __ballot(incl > j);
+    if (hit) return e0 + __ffsll(static_cast<long long>(hit)) - 1;
+    const int64_t tot = __shfl(s, 63, 64);
+    base = base + tot < numel ? base + tot : numel;
+  }
+  return -1;
+}
+
 // silu(g) * u in fp32, the activation of the reference's
 // _silu_and_mul_kernel (ops/fused_moe.py:58-62): g / (1 + exp(-g)) * u,
 // with the division done as a hardware reciprocal (1 ulp).

@@ -55,6 +55,13 @@ struct GemmParams {
   int64_t a_scale_kstride;    // tiled fp8: > 0 -> a_scale is k-block-major
                               // over the padded rows, a_scale[kb * stride +
                               // padded row]; 0 -> [rows][kblocks]
+  const int32_t* route_hist;  // direct rows of a call on the routing tuple
+                              // (GEMM1): row j is gathered position j, its
+                              // expert found from this histogram
+                              // (routed_expert_of) in place of direct_ids[j]
+                              // and recorded in route_ids[j] for GEMM2 and
+                              // the top-k sum; null: off
+  int32_t* route_ids;
 };
 
 // Router gating (scores -> top-k -> renormalise), one wave per token;

@@ -272,7 +272,14 @@ __global__ __launch_bounds__(KW * 64) void moe_gemm_stream_kernel(
   int e;
   if constexpr (DIRECT) {
     if (rb >= p.numel) return;
-    e = p.direct_ids[rb];
+    if (GEMM1 && p.route_hist) {
+      // routing tuple: row rb is gathered position rb; the first column
+      // tile records its expert for GEMM2 and the top-k sum
+      e = routed_expert_of(p.route_hist, p.num_experts, p.numel, rb);
+      if (blockIdx.x == 0 && threadIdx.x == 0) p.route_ids[rb] = e;
+    } else {
+      e = p.direct_ids[rb];
+    }
     if (e < 0 || e >= p.num_experts) return;  // dropped slot: never read
   } else {
     if (rb * BM >= p.num_post_pad[0]) return;

@@ -208,7 +208,7 @@ __device__ int64_t block_inclusive_scan64(int64_t v, int64_t* tmp) {
   const int tid = threadIdx.x;
   tmp[tid] = v;
   __syncthreads();
-  for (int d = 1; d < kOrderThreads; d <<= 1) {
+  for (int d = 1; d < static_cast<int>(blockDim.x); d <<= 1) {
     const int64_t add = tid >= d ? tmp[tid - d] : 0;
     __syncthreads();
     tmp[tid] += add;
@@ -243,8 +243,9 @@ __device__ __forceinline__ int first_above(const int32_t* incl, int n, int64_t x
 //     v = src[p] in [0, numel): ids_out[v] = the expert whose range holds p
 //     (-1 past the histogram's total: a slot no expert reads),
 //     w_out[v] = gate_scal[p].
-// Every workgroup derives the offsets itself (E <= 1024) and then walks its
-// share of the positions; no atomics, so the result is deterministic.
+// Every workgroup (one thread per expert: blockDim >= E, a power of two up
+// to 1024) derives the offsets itself and then walks its share of the
+// positions; no atomics, so the result is deterministic.
 __global__ __launch_bounds__(kOrderThreads) void routing_order_kernel(
     const float* __restrict__ gate_scal, const int32_t* __restrict__ src,
     const int32_t* __restrict__ hist, int64_t numel, int num_experts, int block,
@@ -302,10 +303,15 @@ int launch_routing_order(const float* gate_scal, const int32_t* src, const int32
                          int64_t numel, int num_experts, int block, int64_t max_padded,
                          int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_post_pad,
                          int32_t* ids_out, float* w_out, hipStream_t stream) {
+  if (num_experts < 1 || num_experts > kOrderThreads)
+    return fail(FGS_EINVAL, "routing order: num_experts must be in [1, 1024]");
+  // one wave for up to 64 experts (its barriers cost next to nothing)
+  int threads = 64;
+  while (threads < num_experts) threads *= 2;
   const int64_t work = std::max<int64_t>(sorted_ids ? max_padded : 0, numel);
   const int blocks =
-      static_cast<int>(std::min<int64_t>(std::max<int64_t>((work + kOrderThreads - 1) / kOrderThreads, 1), 256));
-  hipLaunchKernelGGL(routing_order_kernel, dim3(blocks), dim3(kOrderThreads), 0, stream,
+      static_cast<int>(std::min<int64_t>(std::max<int64_t>((work + threads - 1) / threads, 1), 1024));
+  hipLaunchKernelGGL(routing_order_kernel, dim3(blocks), dim3(threads), 0, stream,
                      gate_scal, src, hist, numel, num_experts, block, max_padded, sorted_ids,
                      expert_ids, num_post_pad, ids_out, w_out);
   return check_launch("routing_order_kernel");

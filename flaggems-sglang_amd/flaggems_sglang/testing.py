@@ -46,6 +46,11 @@ CONFIGS = {
                               scoring="sigmoid"),
     "qwen2_int8": MoEConfig("qwen2_int8", 3584, 2560, 64, 8,
                             (1, 64, 1024, 8192), mode="int8"),
+    # the reference's own benchmark (benchmark/test_fused_moe.py:53-73 over
+    # benchmark/attri_util.py:62-70): triton_kernel_fused_experts on the
+    # routing tuple, weights randn * 0.1 in the reference layout
+    "ref_bench": MoEConfig("ref_bench", 1280, 3072, 64, 8,
+                           (1, 4, 17, 64, 1024, 2048, 4096), w_scale=0.1),
 }
 
 # Reference test shapes (M, K, N, E, topk): tests/accuracy_utils.py:114-131.

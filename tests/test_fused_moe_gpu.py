@@ -155,12 +155,14 @@ def test_triton_kernel_fused_experts_compat(gpu, shape, on_input):
     assert torch.equal(res, res_native)
 
 
-def test_triton_kernel_fused_experts_dropped_slot(gpu):
+@pytest.mark.parametrize("M", [1, 48])
+def test_triton_kernel_fused_experts_dropped_slot(gpu, M):
     """A tuple from standard_topk_to_routing with unrouted slots (-1: they go
     behind the last expert, outside every token_offs_raw range) gives what
     fused_moe gives for the same slots, bit for bit, and the inverse hands
-    the -1 back."""
-    M, K, N, E, topk = 48, 256, 512, 8, 2
+    the -1 back (M=1: the one-token schedule, where GEMM1 finds each
+    gathered position's expert from the histogram)."""
+    K, N, E, topk = 256, 512, 8, 2
     x, w1, w2, w, ids = _ref_inputs(M, K, N, E, topk, gpu)
     ids = ids.clone()
     ids[::4, 0] = -1
@@ -173,6 +175,28 @@ def test_triton_kernel_fused_experts_dropped_slot(gpu):
     assert torch.equal(res, flaggems_sglang.fused_moe(x, w1, w2, sw, sids))
     ref = moe_ref.fused_moe(x, w1, w2, w, ids, return_mag=True)
     _check(res.cpu(), ref, "bf16", "compat dropped slots")
+
+
+@pytest.mark.parametrize("mode", ["fp8", "int8", "bf16"])
+@pytest.mark.parametrize("M", [1, 3, 300])
+def test_fused_routed_quantised_bit_identical(gpu, mode, M):
+    """fgs_moe_fused_routed with fp8 / int8 / bf16 weights (one token: the
+    direct schedule; more: the routing-order kernel in place of the
+    alignment) gives fused_moe's bits on the same routing in the tuple's
+    slot order, dropped slots included."""
+    K, N, E, topk = 512, 256, 16, 4
+    cfg = testing.MoEConfig("t", K, N, E, topk, (M,), mode=mode)
+    wts = testing.make_weights(K, N, E, mode, 0.05, device=gpu)
+    x, tw, ti = testing.make_tokens(M, K, E, topk, device=gpu, seed=M + 5)
+    ti = ti.clone()
+    ti[::2, 1] = -1
+    rd, gi, _ = flaggems_sglang.standard_topk_to_routing(tw, ti, E)
+    qm = {"bf16": None, "fp8": _capi.QMODE_FP8_BLOCK, "int8": _capi.QMODE_INT8_CHANNEL}[mode]
+    res = fm._fused_routed(x, wts.w1, wts.w2, rd, gi, qmode=qm, w1_scale=wts.w1_scale,
+                           w2_scale=wts.w2_scale)
+    sw, sids = _row_sorted(tw, ti)
+    ref = flaggems_sglang.fused_moe(x, wts.w1, wts.w2, sw, sids, **wts.kwargs(cfg.mode))
+    assert torch.equal(res, ref)
 
 
 @pytest.mark.parametrize("sched", [_capi.FLAG_FORCE_DECODE, _capi.FLAG_FORCE_PREFILL, 0],

@@ -24,6 +24,14 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
+const char* tuning_env(const char* name) {
+  static const bool on = [] {
+    const char* v = getenv("FGS_MOE_TUNING");
+    return v && strcmp(v, "1") == 0;
+  }();
+  return on ? getenv(name) : nullptr;
+}
+
 int check_launch(const char* what) {
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess)
@@ -37,7 +45,7 @@ static int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
 constexpr int kMaxExperts = 1024;
 constexpr int kKnownFlags = FGS_FLAG_ROUTER_WEIGHT_ON_INPUT | FGS_FLAG_ACT_GELU |
-                            FGS_FLAG_SINGLE_FUSED | FGS_FLAG_SEPARATE_QUANT |
+                            FGS_FLAG_SEPARATE_QUANT |
                             FGS_FLAG_FORCE_DECODE | FGS_FLAG_FORCE_PREFILL |
                             FGS_FLAG_SEPARATE_SUM | FGS_FLAG_FOLD_SUM |
                             FGS_FLAG_TILE_MASK;
@@ -64,15 +72,12 @@ struct Plan {
   bool direct_sum; // ... and GEMM2 folds the top-k sum (no moe_sum)
   int kwd;         // waves of the folded GEMM2
   bool pair2;      // ... two slots per MFMA (moe_gemm2_pair_kernel)
-  bool fused1;     // one token, bf16: both GEMMs in one launch (decode.hip)
-                   // plus the ordered reduction
-  int chunk1;      // its intermediate columns per workgroup
   bool qfold1;     // one token, fp8 / int8: GEMM1 quantises x itself
   bool qfold;      // one token, fp8 / int8: GEMM2 quantises the GEMM1 output rows
                    // itself (no quantiser launch between the GEMMs)
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
-  int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail, o_part,
+  int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail,
       o_xst, o_rids, o_rw,
       total;
 };
@@ -113,7 +118,7 @@ static int pick_ksplit(int64_t numel, int e, int bm, int64_t hidden,
 // rows with moe_sum, 3 direct rows, always folded.
 static int direct_choice() {
   static const int d = [] {
-    const char* v = getenv("FGS_MOE_DIRECT");
+    const char* v = tuning_env("FGS_MOE_DIRECT");
     const int x = v ? atoi(v) : 1;
     return (x >= 0 && x <= 3) ? x : 1;
   }();
@@ -124,7 +129,7 @@ static int direct_choice() {
 // read once).
 static int forced_ksplit() {
   static const int k = [] {
-    const char* v = getenv("FGS_MOE_KSPLIT");
+    const char* v = tuning_env("FGS_MOE_KSPLIT");
     const int x = v ? atoi(v) : 0;
     return (x >= 1 && x <= 4) ? x : 0;
   }();
@@ -135,30 +140,20 @@ static int forced_ksplit() {
 // GEMM2 (a tuning aid; read once).
 static int tail_choice() {
   static const int t = [] {
-    const char* v = getenv("FGS_MOE_TAIL");
+    const char* v = tuning_env("FGS_MOE_TAIL");
     const int x = v ? atoi(v) : 1;
     return (x == 0 || x == 1) ? x : 1;
   }();
   return t;
 }
 
-// FGS_MOE_FUSED1=1 makes the single-token fused path of bf16 layers the
-// default (otherwise FGS_FLAG_SINGLE_FUSED selects it; read once).
 // FGS_MOE_PAIR (0 never, 1 always, unset: by output width) runs the folded
 // single-token GEMM2 with two slots per MFMA (a tuning aid; read once).
 static int pair_choice() {
   static const int f = [] {
-    const char* v = getenv("FGS_MOE_PAIR");
+    const char* v = tuning_env("FGS_MOE_PAIR");
     if (!v) return -1;
     return atoi(v) == 1 ? 1 : atoi(v) == 0 ? 0 : -1;
-  }();
-  return f;
-}
-
-static int fused1_choice() {
-  static const int f = [] {
-    const char* v = getenv("FGS_MOE_FUSED1");
-    return v && atoi(v) == 1 ? 1 : 0;
   }();
   return f;
 }
@@ -168,7 +163,7 @@ static int fused1_choice() {
 // output rows only (GEMM2), 4 both (a tuning aid; read once).
 static int qfold_choice() {
   static const int q = [] {
-    const char* v = getenv("FGS_MOE_QFOLD");
+    const char* v = tuning_env("FGS_MOE_QFOLD");
     if (!v) return 1;
     const int c = atoi(v);
     return c >= 0 && c <= 4 ? c : 1;
@@ -307,16 +302,6 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   p.direct_sum = p.direct && !(flags & FGS_FLAG_SEPARATE_SUM) &&
                  ((flags & FGS_FLAG_FOLD_SUM) || dc == 3 ||
                   (dc == 1 && (fold_wide || fold_pair)));
-  // One bf16 token: GEMM1, the activation and GEMM2 in one launch per
-  // (slot, chunk of intermediate columns), then an ordered reduction (the
-  // schedule flags that pick the unfused sum keep the direct kernels).
-  p.fused1 = p.direct && p.dt == kDtBf16 &&
-             ((flags & FGS_FLAG_SINGLE_FUSED) || fused1_choice()) && topk <= kDecodeMaxSlots &&
-             !(flags & (FGS_FLAG_SEPARATE_SUM | FGS_FLAG_FOLD_SUM)) && hidden % 256 == 0 &&
-             hidden <= kDecodeMaxHidden &&
-             inter % 16 == 0;
-  p.chunk1 = p.fused1 ? decode_chunk(hidden, inter, topk) : 0;
-  if (p.fused1) p.direct_sum = false;
   // the folded GEMM2's waves: 8 while its grid (one workgroup per 16
   // output columns) stays resident in one round at 16 waves per CU
   // (measured against 16 and 4: Mixtral M=1 110.6 -> 106.9 us, Qwen2 int8
@@ -370,7 +355,6 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // gather costs what it saves)
   if (p.tiled && p.dt == kDtFp8 && p.tile_cfg == 0)
     p.o_xst = take((hidden / 128) * p.max_padded * 4);
-  p.o_part = p.fused1 ? take(static_cast<int64_t>(topk) * (inter / p.chunk1) * hidden * 4) : -1;
   // a call on the routing tuple: each flat slot's expert id and gate scale
   p.o_rids = take(numel * 4);
   p.o_rw = take(numel * 4);
@@ -583,36 +567,6 @@ static int run_fused(const FusedArgs& a) {
   }
 
   g_prof.mark(2, a.stream);
-  if (p.fused1 && !routed) {
-    DecodeParams d{};
-    d.x = a.x;
-    d.w13 = a.w13;
-    d.w2 = a.w2;
-    d.b13 = a.b13;
-    d.b2 = a.b2;
-    d.topk_w = topk_w;
-    d.ids = topk_ids;
-    d.part = reinterpret_cast<float*>(ws + p.o_part);
-    d.out = a.out;
-    d.hidden = a.hidden;
-    d.inter = a.inter;
-    d.slots = a.topk;
-    d.num_experts = a.e;
-    d.chunk = p.chunk1;
-    d.n_chunks = static_cast<int32_t>(a.inter / p.chunk1);
-    d.weight_on_input = on_input ? 1 : 0;
-    d.act = a.swiglu ? kActSwiglu : (a.flags & FGS_FLAG_ACT_GELU) ? kActGelu : kActSilu;
-    d.alpha = a.alpha;
-    d.limit = a.limit;
-    rc = launch_decode_fused(d, a.stream);
-    if (rc) return rc;
-    g_prof.mark(3, a.stream);
-    g_prof.mark(4, a.stream);
-    rc = launch_decode_reduce(d, a.stream);
-    g_prof.mark(5, a.stream);
-    g_prof.mark(6, a.stream);
-    return rc;
-  }
   GemmParams g1{};
   g1.a = act;
   g1.a_scale = act_scale;
@@ -934,9 +888,7 @@ int32_t fgs_moe_schedule(int64_t m, int64_t hidden, int64_t inter, int32_t num_e
   Plan p;
   make_plan(m, hidden, inter, num_experts, topk, qmode, flags, &p);
   std::string s;
-  if (p.fused1) {
-    s = "fused1 chunk=" + std::to_string(p.chunk1);
-  } else if (p.direct) {
+  if (p.direct) {
     s = p.direct_sum ? (p.pair2 ? "direct_sum pair" : "direct_sum") : "direct";
     if (p.qfold || p.qfold1)
       s += p.qfold && p.qfold1 ? " qfold" : p.qfold1 ? " qfold_x" : " qfold_a2";
@@ -1023,6 +975,18 @@ int32_t fgs_moe_fused_bf16_noalloc(const void* x, const void* w13, const void* w
                     std::to_string(static_cast<int64_t>(FGS_NOALLOC_SCRATCH_BYTES)) +
                     "-byte device scratch (use fgs_moe_fused_bf16 with a workspace)");
   if (m == 0) return FGS_OK;
+  // the scratch is the current device's: a stream of another device would
+  // run on memory it cannot use
+  if (stream) {
+    int cur = -1, sdev = -1;
+    if (hipGetDevice(&cur) != hipSuccess ||
+        hipStreamGetDevice(as_stream(stream), &sdev) != hipSuccess)
+      return fail(FGS_ELAUNCH, "fgs_moe_fused_bf16_noalloc: cannot query the stream's device");
+    if (sdev != cur)
+      return fail(FGS_EINVAL, "fgs_moe_fused_bf16_noalloc: the stream belongs to device " +
+                                  std::to_string(sdev) + ", the current device is " +
+                                  std::to_string(cur));
+  }
   void* ws = device_scratch();
   if (!ws) return FGS_ELAUNCH;
   FusedArgs a{FGS_QMODE_BF16, x,      w13,    w2,          nullptr,

@@ -182,5 +182,10 @@ __device__ __forceinline__ uint32_t cvt_pk_fp8(float a, float b) {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
+// A schedule tuning aid from the environment: getenv(name) when the
+// process runs with FGS_MOE_TUNING=1 (read once), else null -- the
+// schedule's compiled-in choices are what every other process runs,
+// whatever else its environment holds.
+const char* tuning_env(const char* name);
 
 }  // namespace fgs

@@ -153,35 +153,6 @@ int launch_gemm2_direct(int dt, const GemmParams& p, int kw, hipStream_t stream)
 // the workgroups); needs (numel + 1) / 2 <= kw and n_out % 8 == 0.
 int launch_gemm2_pair(int dt, const GemmParams& p, int kw, hipStream_t stream);
 
-// Single-token fused path (decode.hip, bf16): GEMM1 + activation + GEMM2
-// per (slot, chunk of `chunk` intermediate columns) in one launch, fp32
-// partials part[slots][n_chunks][hidden], then the ordered reduction with
-// the top-k weights into out (bf16 [1, hidden]).
-constexpr int kDecodeMaxSlots = 16;
-constexpr int64_t kDecodeMaxHidden = 16384;  // x staged in LDS
-struct DecodeParams {
-  const void* x;          // [hidden] bf16
-  const void* w13;        // [E, 2*inter, hidden] bf16
-  const void* w2;         // [E, hidden, inter] bf16
-  const float* b13;       // [E, 2*inter] or null
-  const float* b2;        // [E, hidden] or null
-  const float* topk_w;    // [slots]
-  const int32_t* ids;     // [slots]; ids outside [0, num_experts) dropped
-  float* part;            // [slots][n_chunks][hidden] fp32
-  void* out;              // [hidden] bf16
-  int64_t hidden, inter;
-  int32_t slots, num_experts, chunk, n_chunks;
-  int32_t weight_on_input, act;
-  float alpha, limit;
-};
-// Chunk width (32 or 64) the launch uses for this shape.
-int decode_chunk(int64_t hidden, int64_t inter, int slots);
-// The two launches: the fused GEMMs (hidden % 256 == 0, hidden <=
-// kDecodeMaxHidden, inter % chunk == 0),
-// then the reduction into out.
-int launch_decode_fused(const DecodeParams& p, hipStream_t stream);
-int launch_decode_reduce(const DecodeParams& p, hipStream_t stream);
-
 // LDS-tiled MFMA kernels (bf16, fp8, int8): configuration per element type
 // and rows-per-expert regime, its row block, n_out granularity, launch.
 constexpr int kTiledConfigs = 5;  // row blocks 256, 128, 64, 32, 160

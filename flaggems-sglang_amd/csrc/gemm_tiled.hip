@@ -863,7 +863,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
 // Rasterization (FGS_MOE_GROUPM / FGS_MOE_GROUPN override; tuning aids read
 // once): row blocks per band, or, with bands off (0), column tiles per group.
 static int env_choice(const char* name, int dflt, int lo, int hi) {
-  const char* s = getenv(name);
+  const char* s = tuning_env(name);
   const int v = s ? atoi(s) : dflt;
   return (v >= lo && v <= hi) ? v : dflt;
 }
@@ -942,7 +942,7 @@ static const int kTileRows[kTiledConfigs] = {Cfg256::BM, Cfg128::BM, Cfg64::BM,
 // FGS_MOE_TILE (0..3) forces one configuration (a tuning aid; read once).
 static int forced_tile() {
   static const int forced = [] {
-    const char* s = getenv("FGS_MOE_TILE");
+    const char* s = tuning_env("FGS_MOE_TILE");
     if (!s) return -1;
     const int v = atoi(s);
     return (v >= 0 && v < kTiledConfigs) ? v : -1;

@@ -787,7 +787,7 @@ bool wide_supported(int dt, bool gemm1, const GemmParams& p) {
 // read once).
 static int wide_group_n_choice(bool gemm1, int n_ct, double rows_per_expert) {
   static const int g = [] {
-    const char* s = getenv("FGS_MOE_WIDE_GROUPN");
+    const char* s = tuning_env("FGS_MOE_WIDE_GROUPN");
     const int v = s ? atoi(s) : 0;
     return (v >= 1 && v <= 64) ? v : 0;
   }();

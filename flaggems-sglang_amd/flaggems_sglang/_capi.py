@@ -25,7 +25,6 @@ SCORING_SIGMOID = 1
 
 FLAG_ROUTER_WEIGHT_ON_INPUT = 0x1
 FLAG_ACT_GELU = 0x2
-FLAG_SINGLE_FUSED = 0x4
 FLAG_SEPARATE_QUANT = 0x8
 FLAG_FORCE_DECODE = 0x100
 FLAG_FORCE_PREFILL = 0x200
@@ -185,7 +184,7 @@ def check(rc: int, what: str) -> None:
 def schedule(m: int, hidden: int, inter: int, num_experts: int, topk: int,
              qmode: int = QMODE_BF16, flags: int = 0) -> str:
     """The schedule a fused call of this problem runs (``fgs_moe_schedule``):
-    "fused1 chunk=C", "direct", "direct_sum", "stream mt=T" or "tiled ..."."""
+    "direct", "direct_sum", "stream mt=T" or "tiled ..."."""
     buf = ctypes.create_string_buffer(96)
     check(load().fgs_moe_schedule(m, hidden, inter, num_experts, topk, qmode, flags,
                                   buf, len(buf)), "schedule")

@@ -48,7 +48,12 @@ class _ConversionCache:
     An entry belongs to the source's root tensor (a view's ``_base``, else
     the tensor itself), matched by object identity, and within it to the
     view's geometry (offset, shape, strides, dtype); it is served while the
-    root's version counter is unchanged (an in-place update converts again).
+    root's version counter and storage are unchanged: an in-place update
+    through the tensor (``w.copy_(...)``, ``w.add_(...)``) bumps the version
+    and a reassignment of ``param.data`` swaps the storage, and either
+    converts again. An update that goes through ``param.data`` in place
+    (``param.data.copy_(...)``, what many weight loaders do) changes neither
+    and cannot be seen here: after one, call :func:`clear_weight_cache`.
     ``weakref.finalize`` on the root drops its entries when the root is
     garbage-collected, so the cache holds exactly one converted copy per live
     weight -- a model with any number of MoE layers converts each weight
@@ -65,10 +70,11 @@ class _ConversionCache:
     def __call__(self, w: torch.Tensor) -> torch.Tensor:
         root = w._base if w._base is not None else w
         geometry = (w.storage_offset(), tuple(w.shape), tuple(w.stride()), w.dtype)
+        stamp = (root._version, root.untyped_storage().data_ptr())
         views = self._roots.get(id(root))
         if views is not None:
             hit = views.get(geometry)
-            if hit is not None and hit[0] == root._version:
+            if hit is not None and hit[0] == stamp:
                 return hit[1]
         out = self._fn(w)
         if out.untyped_storage().data_ptr() == w.untyped_storage().data_ptr():
@@ -76,7 +82,7 @@ class _ConversionCache:
         if views is None:
             views = self._roots[id(root)] = {}
             weakref.finalize(root, self._roots.pop, id(root), None)
-        views[geometry] = (root._version, out)
+        views[geometry] = (stamp, out)
         return out
 
     def __len__(self) -> int:
@@ -599,6 +605,16 @@ def _fused_routed(hidden_states, w1, w2, routing_data, gather_indx, *,
 # A weight passed as a transposed view of a native-layout tensor converts
 # for free.
 _native_layout = _ConversionCache(lambda t: t.transpose(-1, -2).contiguous())
+
+
+def clear_weight_cache() -> None:
+    """Drop every cached weight conversion (the reference-layout transposes
+    and the de-interleaved bias-variant weights). Call it after updating
+    weights in place through ``param.data`` (``param.data.copy_(...)``),
+    which the caches cannot detect; updates through the tensor itself and
+    reassignments of ``param.data`` are detected."""
+    for cache in (_native_layout, _deinterleaved, _transposed_deinterleaved):
+        cache.clear()
 
 
 def triton_kernel_fused_experts(

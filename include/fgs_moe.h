@@ -56,13 +56,6 @@ extern "C" {
 #define FGS_FLAG_SEPARATE_SUM 0x400
 /* schedule: a one-token call folds the weighted top-k sum into GEMM2 */
 #define FGS_FLAG_FOLD_SUM 0x800
-/* schedule: a one-token bf16 call runs GEMM1, the activation and GEMM2 in
- * one launch per (slot, chunk of intermediate columns), then an ordered
- * reduction (top-k <= 16, hidden % 256 == 0, hidden <= 16384,
- * inter % 16 == 0; measured at parity with the default two-GEMM schedule on
- * Qwen3-shaped layers and slower on Mixtral-shaped ones, so not the default;
- * the FGS_MOE_FUSED1=1 environment variable makes it the default) */
-#define FGS_FLAG_SINGLE_FUSED 0x4
 /* schedule: a one-token fp8 / int8 call quantises its activations with the
  * separate quantiser kernels; by default (top-k <= 64) its GEMMs quantise
  * their bf16 activation rows themselves (fp8: x and the GEMM1 output; int8:
@@ -217,8 +210,7 @@ int64_t fgs_moe_workspace_bytes(int64_t m, int64_t hidden, int64_t inter,
                                 int32_t qmode, int32_t flags);
 
 /* The schedule a fused call of this problem runs, as a short text into
- * buf (NUL-terminated, truncated to len - 1 bytes): "fused1 chunk=C" (one
- * bf16 token: both GEMMs in one launch, then the ordered reduction),
+ * buf (NUL-terminated, truncated to len - 1 bytes):
  * "direct" / "direct_sum" (one token, two streaming GEMMs, the top-k sum
  * separate / folded into GEMM2), "stream mt=T" (streaming GEMMs over the
  * aligned rows) or "tiled cfg=A cfg2=B [ksplit2=S] [tail2]" (LDS-tiled
@@ -268,7 +260,11 @@ int32_t fgs_moe_fused_bf16(const void* x, const void* w13, const void* w2,
  * launch. Every call on a GPU shares that GPU's scratch, which keeps the
  * last call's contents (no part of it needs to start at zero): calls that
  * overlap on one GPU -- on different streams, or from different threads
- * without ordering -- race. */
+ * without ordering -- race. The scratch is the current device's: a stream
+ * of another device is refused (FGS_EINVAL). Under HIP graph capture, make
+ * one eager call on the device first: the first call on a device takes the
+ * scratch address and sets kernel attributes, which must not happen inside
+ * a capture; the captured launches use no memset and allocate nothing. */
 #define FGS_NOALLOC_SCRATCH_BYTES (64ll << 20)
 int32_t fgs_moe_fused_bf16_noalloc(const void* x, const void* w13, const void* w2,
                                    const float* topk_weights, const int32_t* topk_ids,

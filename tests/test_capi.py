@@ -370,3 +370,55 @@ def test_weight_cache_zero_copy_views_not_stored():
     before = len(fm._native_layout)
     fm._native_layout(ref_layout)
     assert len(fm._native_layout) == before
+
+
+def _schedule_in_subprocess(env_extra):
+    import subprocess
+    import sys
+
+    code = ("import sys; sys.path[:0] = [{!r}, {!r}]\n"
+            "from flaggems_sglang import _capi\n"
+            "print(_capi.schedule(4096, 4096, 14336, 8, 2))\n").format(
+                ROOT, os.path.join(ROOT, "flaggems-sglang_amd"))
+    env = {k: v for k, v in os.environ.items() if not k.startswith("FGS_MOE_")}
+    env.update(env_extra)
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True,
+                         text=True, check=True)
+    return out.stdout.strip()
+
+
+def test_tuning_knobs_need_the_tuning_switch():
+    """Schedule knobs in the environment (here the GEMM2 k split and the
+    tail split) change nothing unless FGS_MOE_TUNING=1: the compiled-in
+    choices are the product."""
+    base = _schedule_in_subprocess({})
+    knobs = {"FGS_MOE_KSPLIT": "3", "FGS_MOE_TAIL": "0"}
+    assert _schedule_in_subprocess(knobs) == base
+    tuned = _schedule_in_subprocess({**knobs, "FGS_MOE_TUNING": "1"})
+    assert tuned != base and "ksplit2=3" in tuned
+
+
+def test_removed_single_token_fused_flag_is_rejected():
+    """0x4 (the former single-token fused schedule) is an unknown flag bit."""
+    lib = _capi.load()
+    assert lib.fgs_moe_validate(1, 256, 128, 4, 2, 0, 0x4, 1 << 30) == _capi.FGS_EINVAL
+    assert "unknown flag" in _capi.last_error()
+
+
+def test_weight_cache_sees_data_reassignment_and_clears_on_request():
+    """``param.data = new`` (a new storage) converts again. ``param.data.
+    copy_(new)`` bumps neither the version nor the storage, so the cache
+    serves the old conversion until clear_weight_cache() drops it."""
+    from flaggems_sglang.ops import fused_moe as fm
+
+    p = torch.nn.Parameter(torch.arange(6.0).reshape(1, 2, 3), requires_grad=False)
+    first = fm._native_layout(p)
+    assert torch.equal(first, p.transpose(-1, -2))
+    assert fm._native_layout(p) is first
+    p.data = torch.full((1, 2, 3), 5.0)
+    assert torch.equal(fm._native_layout(p), torch.full((1, 3, 2), 5.0))
+    p.data.copy_(torch.full((1, 2, 3), 9.0))
+    assert p._version == 0  # invisible to the version counter
+    assert torch.equal(fm._native_layout(p), torch.full((1, 3, 2), 5.0))  # stale
+    fm.clear_weight_cache()
+    assert torch.equal(fm._native_layout(p), torch.full((1, 3, 2), 9.0))

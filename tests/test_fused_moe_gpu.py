@@ -306,59 +306,6 @@ def test_single_token(gpu, mode, K, N, E, topk, variant, fold):
     _check(res.cpu(), ref, mode, f"M=1 {mode} {(K, N, E, topk)} {variant}")
 
 
-# One bf16 token with FLAG_SINGLE_FUSED runs the fused single-token path: per
-# (slot, chunk of 16, 32 or 64 intermediate columns) one workgroup computes
-# GEMM1, the activation and its chunk's GEMM2 partial, and an ordered
-# reduction adds the partials and the weighted slots. Covered: the three
-# chunk widths (16: under 256 workgroups of 32, e.g. Qwen3; 64: over 512,
-# e.g. Mixtral's 14336 columns), top-k 2 .. 16 (its limit), 3 (odd),
-# dropped slots, the router weight on the input, gelu.
-@pytest.mark.parametrize("K,N,E,topk", [(3072, 256, 8, 2), (3072, 256, 32, 3),
-                                        (1024, 512, 16, 4), (2048, 768, 128, 8),
-                                        (1024, 1536, 16, 8), (1024, 2048, 64, 16),
-                                        (4096, 14336, 8, 2)],
-                         ids=lambda v: str(v))
-@pytest.mark.parametrize("variant", ["plain", "dropped", "on_input", "gelu"])
-def test_single_token_fused(gpu, K, N, E, topk, variant):
-    F = _capi.FLAG_SINGLE_FUSED
-    assert _capi.schedule(1, K, N, E, topk, flags=F).startswith("fused1")
-    wts = testing.make_weights(K, N, E, "bf16", 0.1, device=gpu, seed=K + N + E + topk)
-    x, tw, ti = testing.make_tokens(1, K, E, topk, device=gpu, seed=K + E + topk + 1)
-    if variant == "dropped":
-        ti = ti.clone()
-        ti[0, 0] = -1
-        if topk > 2:
-            ti[0, -1] = E + 2
-    on_input = variant == "on_input"
-    act = "gelu" if variant == "gelu" else "silu"
-    res = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, apply_router_weight_on_input=on_input,
-                       activation=act, _flags=F)
-    ref = moe_ref.fused_moe(x, wts.w1, wts.w2, tw, ti, apply_router_weight_on_input=on_input,
-                            activation=act, return_mag=True)
-    _check(res.cpu(), ref, "bf16", f"M=1 fused {(K, N, E, topk)} {variant}")
-    assert torch.equal(fm.fused_moe(x, wts.w1, wts.w2, tw, ti,
-                                    apply_router_weight_on_input=on_input, activation=act,
-                                    _flags=F), res)  # deterministic
-    # the unfused direct kernels (separate sum) round at the same points
-    sep = fm.fused_moe(x, wts.w1, wts.w2, tw, ti, apply_router_weight_on_input=on_input,
-                       activation=act, _flags=_capi.FLAG_SEPARATE_SUM)
-    _check(res.cpu(), (sep.cpu().float(), ref[1]), "bf16",
-           f"M=1 fused vs direct {(K, N, E, topk)} {variant}")
-
-
-def test_single_token_fused_limits(gpu):
-    """Top-k above the fused path's 16 slots, quantised modes and the sum
-    flags keep the direct kernels; without the flag they are the default."""
-    F = _capi.FLAG_SINGLE_FUSED
-    assert not _capi.schedule(1, 3072, 256, 64, 17, flags=F).startswith("fused1")
-    assert _capi.schedule(1, 3072, 256, 64, 16, flags=F).startswith("fused1")
-    assert not _capi.schedule(1, 3072, 256, 64, 16, _capi.QMODE_FP8_BLOCK,
-                              F).startswith("fused1")
-    assert not _capi.schedule(1, 3072, 256, 64, 16, flags=F | _capi.FLAG_FOLD_SUM
-                              ).startswith("fused1")
-    assert not _capi.schedule(1, 3072, 256, 64, 16).startswith("fused1")
-
-
 # An fp8 token's GEMMs quantise x and the GEMM1 output themselves, an int8
 # token's GEMM2 the GEMM1 output (per-token scales; x keeps its quantiser);
 # with FLAG_SEPARATE_QUANT the quantiser kernels do. Same arithmetic, so the

@@ -76,3 +76,35 @@ def test_no_alloc_rejects_oversize(gpu):
                                         2, 0, None, None)
     assert rc == _capi.FGS_EUNSUPPORTED
     assert str(need) in _capi.last_error()
+
+
+@pytest.mark.parametrize("m", [300, 1])
+def test_no_alloc_under_graph_capture(gpu, m):
+    """Captured in a HIP graph after one eager call (the first call on a
+    device sets itself up outside the capture) and replayed several times
+    with new inputs copied into the captured buffers and eager work in
+    between: every replay gives the workspace entry point's bits."""
+    K, N, E, k = 1024, 512, 8, 2
+    wts = testing.make_weights(K, N, E, "bf16", 0.05, device=gpu, seed=K + N + E + 1)
+    x, tw, ti = testing.make_tokens(m, K, E, k, device=gpu, seed=m + 3)
+    _no_alloc(x, wts.w1, wts.w2, tw, ti)  # eager set-up call
+    torch.cuda.synchronize()
+    lib = _capi.load()
+    out = torch.empty((m, K), dtype=torch.bfloat16, device=gpu)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = lib.fgs_moe_fused_bf16_noalloc(x.data_ptr(), wts.w1.data_ptr(), wts.w2.data_ptr(),
+                                            tw.data_ptr(), ti.data_ptr(), m, K, N, E, k, 0,
+                                            out.data_ptr(), _stream())
+    _capi.check(rc, "fgs_moe_fused_bf16_noalloc (captured)")
+    for rep in range(4):
+        x2, tw2, ti2 = testing.make_tokens(m, K, E, k, device=gpu, seed=100 * rep + m)
+        x.copy_(x2)
+        tw.copy_(tw2)
+        ti.copy_(ti2)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        ref = _with_workspace(x, wts.w1, wts.w2, tw, ti)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep} differs from the eager entry point"

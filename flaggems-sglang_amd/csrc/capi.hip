@@ -78,7 +78,7 @@ struct Plan {
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
   int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail,
-      o_xst, o_rids, o_rw,
+      o_xst, o_rids, o_rw, o_plan,
       total;
 };
 
@@ -355,6 +355,9 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // gather costs what it saves)
   if (p.tiled && p.dt == kDtFp8 && p.tile_cfg == 0)
     p.o_xst = take((hidden / 128) * p.max_padded * 4);
+  // the 4-wave GEMM1's tile plan (256-row configuration)
+  p.o_plan = -1;
+  if (p.tiled && p.tile_cfg == 0 && p.dt != kDtFp8) p.o_plan = take(4 * wide_plan_words());
   // a call on the routing tuple: each flat slot's expert id and gate scale
   p.o_rids = take(numel * 4);
   p.o_rw = take(numel * 4);
@@ -590,6 +593,7 @@ static int run_fused(const FusedArgs& a) {
   g1.a_rows = a.m;
   g1.num_experts = a.e;
   g1.a_scale_kstride = p.o_xst >= 0 ? p.max_padded : 0;
+  g1.plan = p.o_plan >= 0 ? reinterpret_cast<int32_t*>(ws + p.o_plan) : nullptr;
   if (p.direct) {
     // slot j is row tile j; a2 holds the compact slot rows
     g1.direct_ids = topk_ids;

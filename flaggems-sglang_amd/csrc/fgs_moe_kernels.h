@@ -55,6 +55,9 @@ struct GemmParams {
   int64_t a_scale_kstride;    // tiled fp8: > 0 -> a_scale is k-block-major
                               // over the padded rows, a_scale[kb * stride +
                               // padded row]; 0 -> [rows][kblocks]
+  int32_t* plan;              // 4-wave GEMM1: workspace for its tile plan
+                              // (wide_plan_words ints; null: no plan, the
+                              // tiles are split over the XCDs by count)
   const int32_t* route_hist;  // direct rows of a call on the routing tuple
                               // (GEMM1): row j is gathered position j, its
                               // expert found from this histogram
@@ -171,5 +174,7 @@ bool wide_supported(int dt, bool gemm1, const GemmParams& p);
 int64_t wide_tail_part_bytes();
 int launch_gemm_wide(int dt, bool gemm1, const GemmParams& p, int row_blocks,
                      hipStream_t stream);
+// Ints of tile-plan workspace the 4-wave GEMM1 uses (gemm_wide.hip).
+int64_t wide_plan_words();
 
 }  // namespace fgs

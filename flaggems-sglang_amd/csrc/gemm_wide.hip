@@ -152,6 +152,136 @@ __device__ __forceinline__ WideTail wide_tail(int lo, int hi, bool on, int kt_al
 }
 constexpr int kWideTailSlots = 8 * 32;  // tail_part slots: 32 per XCD
 
+// ---- tile plan. Workgroup b runs on XCD b % 8 and takes position b / 8
+// of its XCD's tile range, walked in column groups (wide_walk). Tiles of a
+// row block whose rows are mostly padding (an expert's last few rows) cost
+// a fraction of a full tile -- measured per tile with in-kernel timestamps,
+// Mixtral M=4096 GEMM1: 84 vs 117 us -- and with few row blocks (about one
+// expert per XCD) the even split by count gave whole XCDs those cheap
+// tiles: their CUs went idle for the last ~8 % of GEMM1 while the other
+// XCDs finished full tiles. The plan, made by one workgroup before GEMM1:
+//  * costs each row block at base + the live 32-row blocks of its first
+//    wave row, ceil(live / 2) of 1..4 (a block of a few rows: 6/9 of a
+//    full one, measured 0.65-0.72);
+//  * cuts the row-block-major tile sequence into 8 contiguous ranges of
+//    equal cost (contiguous, so an XCD still holds about one expert in
+//    eight), or of equal count when an equal-cost range would hold more
+//    tiles than the launch has positions for.
+// plan[0..8]: the ranges' bounds in tile index (plan[0] = -1: no plan);
+// then one claim counter per XCD, each in its own 256-byte slot. The XCDs'
+// tiles still take different times (per XCD, full tiles averaged 113-121
+// us in one measurement), so the last kPlanClaimTail positions of each
+// range are claimed instead of fixed: a workgroup at such a position takes
+// the next unclaimed one from its XCD's counter (relaxed device-scope
+// atomics), and once its own tail is used up it tries one other XCD's tail
+// and otherwise exits. The launch gives every XCD positions beyond its
+// range, so an XCD that finishes early takes over tiles of slower ones;
+// every XCD's own workgroups still cover its whole range. Every workgroup
+// either takes a tile or exits, and a tile computes the same whichever CU
+// runs it. (Claiming every position, with the counters in one cache line,
+// made GEMM1 45 % slower: the atomics serialise.)
+// Measured (Mixtral M=4096, same box, alternating runs): GEMM1 1.729 ->
+// 1.680 ms (layer 2.678 -> 2.633 ms) with the plan and the claimed tails. Listing each XCD's full row blocks before
+// its light ones was slower everywhere (a light tile then no longer reads
+// its weight tiles while its expert's full tiles have them in L2), and
+// with hundreds of row blocks (Qwen3 / Qwen2 at M=8192: the cheap tiles
+// are spread over every XCD) the plan only adds its own time; GEMM2's tail
+// split already balances its last round.
+constexpr int kPlanThreads = 256;
+constexpr int kPlanMaxRows = 64;  // row blocks a launch may have for a plan
+constexpr int kPlanWords = 9;
+constexpr int kPlanClaimStride = 64;  // ints: one 256-byte slot per XCD counter
+constexpr int kPlanClaimTail = 64;    // positions at the end of a range that are claimed
+constexpr int kPlanBase = 5;
+
+__global__ __launch_bounds__(kPlanThreads) void wide_plan_kernel(
+    const int32_t* __restrict__ sorted_ids, const int32_t* __restrict__ num_post_pad, int numel,
+    int bm, int n_ct, int cap, int32_t* __restrict__ plan) {
+  __shared__ int pref_s[kPlanThreads];
+  __shared__ int bound_s[9];
+  const int tid = threadIdx.x;
+  if (tid < 8) plan[kPlanWords + tid * kPlanClaimStride] = 0;  // nothing claimed yet
+  const int rows = num_post_pad[0] / bm;
+  if (rows <= 0 || rows > kPlanMaxRows) {
+    if (tid == 0) plan[0] = -1;  // the kernel splits its tiles evenly
+    return;
+  }
+  int c = 0;
+  if (tid < rows) {
+    int sid[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sid[j] = 32 * j < bm ? sorted_ids[tid * bm + 32 * j] : numel;
+    int lb = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) lb += sid[j] < numel ? 1 : 0;
+    c = kPlanBase + (lb + 1) / 2;
+  }
+  // inclusive sums of the row costs (one wave: rows <= 64)
+  int incl = c;
+  if (tid < 64) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, 64);
+      if ((tid & 63) >= d) incl += o;
+    }
+    pref_s[tid] = incl;
+  }
+  __syncthreads();
+  const int64_t total_cost = static_cast<int64_t>(pref_s[63]) * n_ct;
+  const int64_t total_tiles = static_cast<int64_t>(rows) * n_ct;
+  // bound x: the first tile whose start cost reaches total_cost * x / 8 --
+  // in row tid when that row's cost range holds it
+  if (tid < rows) {
+    const int64_t lo_cost = static_cast<int64_t>(incl - c) * n_ct;
+    const int64_t hi_cost = static_cast<int64_t>(incl) * n_ct;
+    for (int x = 1; x < 8; ++x) {
+      const int64_t target = total_cost * x / 8;
+      if (target > lo_cost && target <= hi_cost) {
+        const int into = static_cast<int>(target - lo_cost);  // < n_ct * c
+        bound_s[x] = tid * n_ct + (into + c - 1) / c;
+      } else if (tid == 0 && target <= 0) {
+        bound_s[x] = 0;
+      }
+    }
+  }
+  if (tid == 0) {
+    bound_s[0] = 0;
+    bound_s[8] = static_cast<int>(total_tiles);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    bool even = false;
+    for (int x = 0; x < 8; ++x) even |= bound_s[x + 1] - bound_s[x] > cap;
+    for (int x = 0; x <= 8; ++x)
+      plan[x] = even ? static_cast<int>(total_tiles * x / 8) : bound_s[x];
+  }
+}
+
+int64_t wide_plan_words() { return kPlanWords + 8 * kPlanClaimStride; }
+
+// An XCD's range [lo, hi) of the row-block-major tile index: the plan's
+// (GEMM1 with few row blocks), else an even split by count.
+struct WideRange {
+  int lo, hi;
+  bool claims;  // positions are claimed from the plan's counters
+};
+__device__ __forceinline__ WideRange wide_range(const GemmParams& p, int total, int xcd) {
+  WideRange w;
+  w.claims = false;
+  if (p.plan) {
+    const int first = __builtin_amdgcn_readfirstlane(p.plan[0]);
+    if (first >= 0) {
+      w.lo = __builtin_amdgcn_readfirstlane(p.plan[xcd]);
+      w.hi = __builtin_amdgcn_readfirstlane(p.plan[xcd + 1]);
+      w.claims = true;
+      return w;
+    }
+  }
+  w.lo = static_cast<int>(static_cast<int64_t>(total) * xcd / 8);
+  w.hi = static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8);
+  return w;
+}
+
 template <int DT, bool GEMM1, class C>
 __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const GemmParams p) {
   using T = TiledType<DT>;
@@ -190,9 +320,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   const int rows_all = rb_live * p.ksplit;  // row-block index space over splits
   const int total = rows_all * n_ct;
   const int xcd = blockIdx.x % 8;
-  const int lo = static_cast<int>(static_cast<int64_t>(total) * xcd / 8);
-  const int hi = static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8);
-  const WideTail tail = wide_tail(lo, hi, !GEMM1 && p.tail_split, KT_all);
+  const WideRange range = wide_range(p, total, xcd);
+  const WideTail tail = wide_tail(range.lo, range.hi, !GEMM1 && p.tail_split, KT_all);
 
   struct Tile {
     int rb, ct, e, kt0, KT, ks;
@@ -200,7 +329,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   };
   // Workgroup position pos of the XCD: a whole tile of the walk, or (tail
   // split) a k piece of one of the last round's tiles.
-  auto live_tile = [&](int pos, Tile& t) -> bool {
+  auto live_tile = [&](const WideRange& rg, int pos, Tile& t) -> bool {
     int d = pos, piece = -1;
     if (tail.S > 1 && pos >= 32 * tail.R) {
       const int q = pos - 32 * tail.R;
@@ -208,9 +337,9 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
       d = 32 * tail.R + q / tail.S;
       piece = q % tail.S;
     }
-    if (d >= tail.T) return false;
+    if (d >= rg.hi - rg.lo) return false;  // (the owner's range: a claim may be another XCD's)
     int rball, ct;
-    if (!wide_walk(lo, hi, n_ct, p.group_n, d, &rball, &ct)) return false;
+    if (!wide_walk(rg.lo, rg.hi, n_ct, p.group_n, d, &rball, &ct)) return false;
     t.ct = ct;
     t.ks = rball / rb_live;
     t.rb = rball - t.ks * rb_live;
@@ -318,7 +447,39 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   }
 
   Tile cur;
-  if (!live_tile(static_cast<int>(blockIdx.x / 8), cur)) return;
+  if (GEMM1 && range.claims &&
+      static_cast<int>(blockIdx.x / 8) >= range.hi - range.lo - kPlanClaimTail) {
+    // a claimed position (one lane claims; the tile goes to every wave
+    // through the LDS table area, which the epilogue fills only later)
+    int* claim_s = reinterpret_cast<int*>(lds + C::TAB_OFF);
+    if (threadIdx.x == 0) {
+      const int me = static_cast<int>(blockIdx.x / 8);
+      int owner = -1, pos = 0;
+      for (int k = 0; k < 2 && owner < 0; ++k) {
+        // own tail first, then one other XCD's (spread by position)
+        const int x = k == 0 ? xcd : (xcd + 1 + me % 7) & 7;
+        const int n = p.plan[x + 1] - p.plan[x];
+        const int first = max(0, n - kPlanClaimTail);
+        pos = first + __hip_atomic_fetch_add(p.plan + kPlanWords + x * kPlanClaimStride, 1,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (pos < n) owner = x;
+      }
+      claim_s[0] = owner;
+      claim_s[1] = pos;
+    }
+    __syncthreads();
+    const int owner = __builtin_amdgcn_readfirstlane(claim_s[0]);
+    const int pos = __builtin_amdgcn_readfirstlane(claim_s[1]);
+    __syncthreads();
+    if (owner < 0) return;
+    WideRange rg;
+    rg.lo = __builtin_amdgcn_readfirstlane(p.plan[owner]);
+    rg.hi = __builtin_amdgcn_readfirstlane(p.plan[owner + 1]);
+    rg.claims = true;
+    if (!live_tile(rg, pos, cur)) return;
+  } else {
+    if (!live_tile(range, static_cast<int>(blockIdx.x / 8), cur)) return;
+  }
   Src src;
   make_src(cur, src);
   const int row0 = cur.rb * BM;
@@ -712,12 +873,11 @@ __global__ __launch_bounds__(256) void moe_wide_tail_fixup_kernel(const GemmPara
   const int npp = p.num_post_pad[0];
   const int n_ct = static_cast<int>(p.n_out / BNR);
   const int total = npp / BM * n_ct;  // ksplit is 1 with a tail split
-  const int lo = static_cast<int>(static_cast<int64_t>(total) * xcd / 8);
-  const int hi = static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8);
-  const WideTail tail = wide_tail(lo, hi, true, static_cast<int>(p.kdim * ESZ / SK));
+  const WideRange range = wide_range(p, total, xcd);
+  const WideTail tail = wide_tail(range.lo, range.hi, true, static_cast<int>(p.kdim * ESZ / SK));
   if (tail.S < 2 || t >= tail.rem) return;
   int rb, ct;
-  if (!wide_walk(lo, hi, n_ct, p.group_n, 32 * tail.R + t, &rb, &ct)) return;
+  if (!wide_walk(range.lo, range.hi, n_ct, p.group_n, 32 * tail.R + t, &rb, &ct)) return;
   const int lane = threadIdx.x & 63;
   const int slot0 = xcd * 32 + t * tail.S;
   // a wave's 8 rows in two batches of 4, every piece of a batch's rows in
@@ -795,6 +955,15 @@ static int wide_group_n_choice(bool gemm1, int n_ct, double rows_per_expert) {
   return gemm1 && n_ct >= 16 && rows_per_expert >= 512 ? 4 : 8;
 }
 
+// FGS_MOE_PLAN=0 turns the GEMM1 tile plan off (a tuning aid; read once).
+static bool plan_off() {
+  static const bool off = [] {
+    const char* v = tuning_env("FGS_MOE_PLAN");
+    return v && atoi(v) == 0;
+  }();
+  return off;
+}
+
 template <int DT, bool GEMM1>
 static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream) {
   using C = WideRing;
@@ -809,6 +978,8 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
     return fail(FGS_ELAUNCH, std::string("wide GEMM LDS opt-in: ") + hipGetErrorString(attr));
   GemmParams q = p;
   q.row_blocks = row_blocks;
+  // the plan: GEMM1 over few row blocks (see wide_plan_kernel)
+  if (!GEMM1 || row_blocks > kPlanMaxRows || plan_off()) q.plan = nullptr;
   if (GEMM1 || q.ksplit < 1) q.ksplit = 1;
   if (GEMM1 || !q.tail_part) q.tail_split = 0;
   if (q.tail_split) q.ksplit = 1;
@@ -821,7 +992,21 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
   // for the tail pieces of its last round
   const int n_ct = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   const int64_t total = static_cast<int64_t>(row_blocks) * q.ksplit * n_ct;
-  const int64_t n_pos = (total + 7) / 8 + (q.tail_split ? 32 : 0);
+  // positions per XCD for whole tiles: the even split needs total / 8; a
+  // cost-balanced plan may give an XCD up to a quarter more (its plan
+  // falls back to the even split beyond that)
+  int64_t cap = (total + 7) / 8;
+  int64_t extra = 0;  // positions past an XCD's range (claims of others' tails)
+  if (q.plan) {
+    cap = cap * 5 / 4 + 1;
+    extra = 32;
+    hipLaunchKernelGGL(wide_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, q.sorted_ids,
+                       q.num_post_pad, static_cast<int>(q.numel), C::BM, n_ct,
+                       static_cast<int>(cap), q.plan);
+    const int rc = check_launch("wide_plan_kernel");
+    if (rc) return rc;
+  }
+  const int64_t n_pos = cap + extra + (q.tail_split ? 32 : 0);
   const int grid = static_cast<int>(8 * n_pos);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(C::NW * 64), C::LDS_BYTES, stream, q);
   int rc = check_launch("moe_gemm_wide_kernel");

@@ -939,7 +939,7 @@ using Fp8Cfg32 = TileCfg<32, 256, 1, 4, 128, 3>;
 static const int kTileRows[kTiledConfigs] = {Cfg256::BM, Cfg128::BM, Cfg64::BM,
                                              Cfg32::BM, Cfg160::BM};
 
-// FGS_MOE_TILE (0..3) forces one configuration (a tuning aid; read once).
+// FGS_MOE_TILE (0..4) forces one configuration (a tuning aid; read once).
 static int forced_tile() {
   static const int forced = [] {
     const char* s = tuning_env("FGS_MOE_TILE");

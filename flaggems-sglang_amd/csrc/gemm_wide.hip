@@ -683,7 +683,6 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
           if (woi) tab[128 + t] = ok ? p.topk_w[sid] : 1.f;
         }
       }
-      auto tab_sid = [&](int i, int r) -> int { return tsid[i * 32 + r]; };
       auto row_sa = [&](int i) -> float {
         if constexpr (INT8) return tab[384 + i * 32 + (lane & 31)];
         else return 1.f;
@@ -734,17 +733,25 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
               }
             }
             stage_sync();
-            // 8 lanes per row, 8 rows per pass
+            // 8 lanes per row, 8 rows per pass. Every row of a live 32-row
+            // block is stored: a pad row has its own row in the padded
+            // order, which nothing reads, so the passes need no branch and
+            // their staged reads all issue ahead of the stores (one LDS
+            // round trip per block instead of one per pass)
+            constexpr int NP = 32 / (64 / CH);
+            uint4 val[NP];
 #pragma unroll
-            for (int k = 0; k < 32 / (64 / CH); ++k) {
+            for (int k = 0; k < NP; ++k) {
               const int sr = k * (64 / CH) + lane / CH;
               const int c = lane % CH;
-              const int rsid = tab_sid(i, sr);
-              const uint4 val = *reinterpret_cast<const uint4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
-              if (rsid < p.numel) {
-                const int64_t orow = row0 + i * 64 + wm * 32 + sr;
-                *reinterpret_cast<uint4*>(out + orow * p.n_out + col_base + c * 8) = val;
-              }
+              val[k] = *reinterpret_cast<const uint4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
+            }
+#pragma unroll
+            for (int k = 0; k < NP; ++k) {
+              const int sr = k * (64 / CH) + lane / CH;
+              const int c = lane % CH;
+              const int64_t orow = row0 + i * 64 + wm * 32 + sr;
+              *reinterpret_cast<uint4*>(out + orow * p.n_out + col_base + c * 8) = val[k];
             }
             stage_sync();
           }
@@ -801,20 +808,37 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
               }
               stage_sync();
               float* outf = static_cast<float*>(p.out);
+              // four passes' row slots and staged values first, then their
+              // stores (one LDS round trip per four passes instead of two
+              // per pass; four keep the registers within budget)
+              constexpr int NP = 32 / (64 / CH);
+              static_assert(NP % 4 == 0, "passes in groups of four");
 #pragma unroll
-              for (int k = 0; k < 32 / (64 / CH); ++k) {
-                const int sr = k * (64 / CH) + lane / CH;
-                const int c = lane % CH;
-                const int row_sid = tab_sid(i, sr);
-                const f32x4 val = *reinterpret_cast<const f32x4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
-                if (row_sid >= p.numel) continue;
-                float* dst;
-                if (cur.slot >= 0)  // tail piece: [slot][tile row][tile column]
-                  dst = p.tail_part + (static_cast<int64_t>(cur.slot) * BM + i * 64 + wm * 32 + sr) * BNR +
-                        wn * WCOLS + c * 4;
-                else
-                  dst = outf + (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out + col_base + c * 4;
-                *reinterpret_cast<f32x4*>(dst) = val;
+              for (int k0 = 0; k0 < NP; k0 += 4) {
+                f32x4 vals[4];
+                int sids[4];
+#pragma unroll
+                for (int kq = 0; kq < 4; ++kq) {
+                  const int sr = (k0 + kq) * (64 / CH) + lane / CH;
+                  const int c = lane % CH;
+                  sids[kq] = tsid[i * 32 + sr];
+                  vals[kq] = *reinterpret_cast<const f32x4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
+                }
+#pragma unroll
+                for (int kq = 0; kq < 4; ++kq) {
+                  const int sr = (k0 + kq) * (64 / CH) + lane / CH;
+                  const int c = lane % CH;
+                  const int row_sid = sids[kq];
+                  const f32x4 val = vals[kq];
+                  if (row_sid >= p.numel) continue;
+                  float* dst;
+                  if (cur.slot >= 0)  // tail piece: [slot][tile row][tile column]
+                    dst = p.tail_part + (static_cast<int64_t>(cur.slot) * BM + i * 64 + wm * 32 + sr) * BNR +
+                          wn * WCOLS + c * 4;
+                  else
+                    dst = outf + (static_cast<int64_t>(ks) * p.numel + row_sid) * p.n_out + col_base + c * 4;
+                  *reinterpret_cast<f32x4*>(dst) = val;
+                }
               }
               stage_sync();
             } else {
@@ -838,14 +862,28 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
                 }
               }
               stage_sync();
+              // four passes' row slots and staged values first, then their
+              // stores (one LDS round trip per four passes instead of two
+              // per pass; four keep the registers within budget)
+              constexpr int NP = 32 / (64 / CH);
+              static_assert(NP % 4 == 0, "passes in groups of four");
 #pragma unroll
-              for (int k = 0; k < 32 / (64 / CH); ++k) {
-                const int sr = k * (64 / CH) + lane / CH;
-                const int c = lane % CH;
-                const int row_sid = tab_sid(i, sr);
-                const uint4 val = *reinterpret_cast<const uint4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
-                if (row_sid < p.numel)
-                  *reinterpret_cast<uint4*>(out + static_cast<int64_t>(row_sid) * p.n_out + col_base + c * 8) = val;
+              for (int k0 = 0; k0 < NP; k0 += 4) {
+                u32x4 vals[4];
+                int sids[4];
+#pragma unroll
+                for (int kq = 0; kq < 4; ++kq) {
+                  const int sr = (k0 + kq) * (64 / CH) + lane / CH;
+                  const int c = lane % CH;
+                  sids[kq] = tsid[i * 32 + sr];
+                  vals[kq] = *reinterpret_cast<const u32x4*>(stg + sr * (CH * 16) + ((c ^ (sr % CH)) * 16));
+                }
+#pragma unroll
+                for (int kq = 0; kq < 4; ++kq) {
+                  const int c = lane % CH;
+                  if (sids[kq] < p.numel)
+                    *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(sids[kq]) * p.n_out + col_base + c * 8) = vals[kq];
+                }
               }
               stage_sync();
             }

@@ -133,12 +133,13 @@ __device__ __forceinline__ bool wide_walk(int lo, int hi, int n_ct, int gn, int 
 
 // Tail split of an XCD's walk (GEMM2, p.tail_split): its T tiles run as R =
 // T / 32 full rounds on the XCD's 32 CUs; the rem = T % 32 tiles of the last
-// round are each split over k into S = min(4, 32 / rem) pieces, so the last
+// round are each split over k into S = min(8, 32 / rem) pieces, so the last
 // round holds rem * S pieces instead of rem whole tiles. Piece i of tail
 // tile t writes fp32 partial sums to tail_part slot (xcd * 32 + t * S + i);
 // moe_wide_tail_fixup_kernel adds a tile's pieces in order. S = 1 (no
 // split) when rem is 0 or above 16; a piece keeps >= 2 stages of k (the
 // ring depth), so S <= KT_all / 2.
+constexpr int kWideMaxPieces = 8;
 struct WideTail {
   int T, R, rem, S;
 };
@@ -147,7 +148,7 @@ __device__ __forceinline__ WideTail wide_tail(int lo, int hi, bool on, int kt_al
   w.T = hi - lo;
   w.R = w.T / 32;
   w.rem = w.T - 32 * w.R;
-  w.S = on && w.rem > 0 ? max(1, min(min(4, 32 / w.rem), kt_all / 2)) : 1;
+  w.S = on && w.rem > 0 ? max(1, min(min(kWideMaxPieces, 32 / w.rem), kt_all / 2)) : 1;
   return w;
 }
 constexpr int kWideTailSlots = 8 * 32;  // tail_part slots: 32 per XCD
@@ -192,11 +193,15 @@ constexpr int kPlanMaxRows = 64;  // row blocks a launch may have for a plan
 constexpr int kPlanWords = 9;
 constexpr int kPlanClaimStride = 64;  // ints: one 256-byte slot per XCD counter
 constexpr int kPlanClaimTail = 64;    // positions at the end of a range that are claimed
-constexpr int kPlanBase = 5;
+// row-block cost = base + ceil(live 32-row blocks / 2): a block of a few
+// rows costs 6/9 of a full one in GEMM1 (measured 0.65-0.72) and 16/19 in
+// GEMM2 (measured 0.80-0.85: its k rows are longer)
+constexpr int kPlanBaseGemm1 = 5;
+constexpr int kPlanBaseGemm2 = 15;
 
 __global__ __launch_bounds__(kPlanThreads) void wide_plan_kernel(
     const int32_t* __restrict__ sorted_ids, const int32_t* __restrict__ num_post_pad, int numel,
-    int bm, int n_ct, int cap, int32_t* __restrict__ plan) {
+    int bm, int n_ct, int cap, int base, int32_t* __restrict__ plan) {
   __shared__ int pref_s[kPlanThreads];
   __shared__ int bound_s[9];
   const int tid = threadIdx.x;
@@ -214,7 +219,7 @@ __global__ __launch_bounds__(kPlanThreads) void wide_plan_kernel(
     int lb = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) lb += sid[j] < numel ? 1 : 0;
-    c = kPlanBase + (lb + 1) / 2;
+    c = base + (lb + 1) / 2;
   }
   // inclusive sums of the row costs (one wave: rows <= 64)
   int incl = c;
@@ -929,24 +934,34 @@ __global__ __launch_bounds__(256) void moe_wide_tail_fixup_kernel(const GemmPara
       tr[j] = rblk * 32 + (b * RW + j) * 4 + static_cast<int>(threadIdx.x >> 6);
       sid[j] = p.sorted_ids[rb * BM + tr[j]];
     }
-    f32x4 part[RW][4];
+    // pieces in order, ((p0 + p1) + p2) + ..., four at a time
+    f32x4 acc[RW];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i0 = 0; i0 < kWideMaxPieces; i0 += 4) {
+      if (i0 >= tail.S) break;
+      f32x4 part[RW][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < RW; ++j)
+          part[j][i] = i0 + i < tail.S && sid[j] < p.numel
+                           ? *reinterpret_cast<const f32x4*>(
+                                 p.tail_part +
+                                 (static_cast<int64_t>(slot0 + i0 + i) * BM + tr[j]) * BNR +
+                                 lane * 4)
+                           : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < RW; ++j)
-        part[j][i] = i < tail.S && sid[j] < p.numel
-                         ? *reinterpret_cast<const f32x4*>(
-                               p.tail_part + (static_cast<int64_t>(slot0 + i) * BM + tr[j]) * BNR +
-                               lane * 4)
-                         : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (i0 + i < tail.S) acc[j] = i0 + i == 0 ? part[j][0] : acc[j] + part[j][i];
+    }
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
       if (sid[j] >= p.numel) continue;
-      // pieces in order: ((p0 + p1) + p2) + p3; absent pieces add zero
-      const f32x4 acc = ((part[j][0] + part[j][1]) + part[j][2]) + part[j][3];
       uint2 v;
-      v.x = pack_bf16x2(acc[0], acc[1]);
-      v.y = pack_bf16x2(acc[2], acc[3]);
+      v.x = pack_bf16x2(acc[j][0], acc[j][1]);
+      v.y = pack_bf16x2(acc[j][2], acc[j][3]);
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + static_cast<int64_t>(sid[j]) * p.n_out +
                                 ct * BNR + lane * 4) = v;
     }
@@ -1016,11 +1031,11 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
     return fail(FGS_ELAUNCH, std::string("wide GEMM LDS opt-in: ") + hipGetErrorString(attr));
   GemmParams q = p;
   q.row_blocks = row_blocks;
-  // the plan: GEMM1 over few row blocks (see wide_plan_kernel)
-  if (!GEMM1 || row_blocks > kPlanMaxRows || plan_off()) q.plan = nullptr;
   if (GEMM1 || q.ksplit < 1) q.ksplit = 1;
   if (GEMM1 || !q.tail_part) q.tail_split = 0;
   if (q.tail_split) q.ksplit = 1;
+  // the plan: few row blocks, whole tiles (see wide_plan_kernel)
+  if (row_blocks > kPlanMaxRows || q.ksplit > 1 || plan_off()) q.plan = nullptr;
   const int n_ct_walk = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   const double rows_per_expert =
       p.num_experts > 0 ? static_cast<double>(p.numel) / p.num_experts : 0.0;
@@ -1037,10 +1052,10 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
   int64_t extra = 0;  // positions past an XCD's range (claims of others' tails)
   if (q.plan) {
     cap = cap * 5 / 4 + 1;
-    extra = 32;
+    extra = GEMM1 ? 32 : 0;
     hipLaunchKernelGGL(wide_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, q.sorted_ids,
                        q.num_post_pad, static_cast<int>(q.numel), C::BM, n_ct,
-                       static_cast<int>(cap), q.plan);
+                       static_cast<int>(cap), GEMM1 ? kPlanBaseGemm1 : kPlanBaseGemm2, q.plan);
     const int rc = check_launch("wide_plan_kernel");
     if (rc) return rc;
   }

@@ -157,13 +157,13 @@ constexpr int kWideTailSlots = 8 * 32;  // tail_part slots: 32 per XCD
 // of its XCD's tile range, walked in column groups (wide_walk). Tiles of a
 // row block whose rows are mostly padding (an expert's last few rows) cost
 // a fraction of a full tile -- measured per tile with in-kernel timestamps,
-// Mixtral M=4096 GEMM1: 84 vs 117 us -- and with few row blocks (about one
-// expert per XCD) the even split by count gave whole XCDs those cheap
-// tiles: their CUs went idle for the last ~8 % of GEMM1 while the other
-// XCDs finished full tiles. The plan, made by one workgroup before GEMM1:
-//  * costs each row block at base + the live 32-row blocks of its first
-//    wave row, ceil(live / 2) of 1..4 (a block of a few rows: 6/9 of a
-//    full one, measured 0.65-0.72);
+// Mixtral M=4096 GEMM1: 84 vs 117 us, GEMM2: 308-324 vs 361-386 us -- and
+// with few row blocks (about one expert per XCD) the even split by count
+// gave whole XCDs those cheap tiles: their CUs went idle for the last ~8 %
+// of GEMM1 while the other XCDs finished full tiles. The plan, made by one
+// workgroup before the GEMM:
+//  * costs each row block at base + ceil(live / 2), live = the live 32-row
+//    blocks of its first wave row (1..4);
 //  * cuts the row-block-major tile sequence into 8 contiguous ranges of
 //    equal cost (contiguous, so an XCD still holds about one expert in
 //    eight), or of equal count when an equal-cost range would hold more
@@ -171,23 +171,26 @@ constexpr int kWideTailSlots = 8 * 32;  // tail_part slots: 32 per XCD
 // plan[0..8]: the ranges' bounds in tile index (plan[0] = -1: no plan);
 // then one claim counter per XCD, each in its own 256-byte slot. The XCDs'
 // tiles still take different times (per XCD, full tiles averaged 113-121
-// us in one measurement), so the last kPlanClaimTail positions of each
-// range are claimed instead of fixed: a workgroup at such a position takes
-// the next unclaimed one from its XCD's counter (relaxed device-scope
-// atomics), and once its own tail is used up it tries one other XCD's tail
-// and otherwise exits. The launch gives every XCD positions beyond its
-// range, so an XCD that finishes early takes over tiles of slower ones;
-// every XCD's own workgroups still cover its whole range. Every workgroup
-// either takes a tile or exits, and a tile computes the same whichever CU
-// runs it. (Claiming every position, with the counters in one cache line,
-// made GEMM1 45 % slower: the atomics serialise.)
+// us in one measurement), so in GEMM1 the last kPlanClaimTail positions of
+// each range are claimed instead of fixed: a workgroup at such a position
+// takes the next unclaimed one from its XCD's counter (relaxed
+// device-scope atomics), and once its own tail is used up it tries one
+// other XCD's tail and otherwise exits. The launch gives every XCD
+// positions beyond its range, so an XCD that finishes early takes over
+// tiles of slower ones; every XCD's own workgroups still cover its whole
+// range. Every workgroup either takes a tile or exits, and a tile computes
+// the same whichever CU runs it. (Claiming every position, with the
+// counters in one cache line, made GEMM1 45 % slower: the atomics
+// serialise.) GEMM2 balances its last round by the tail split instead.
 // Measured (Mixtral M=4096, same box, alternating runs): GEMM1 1.729 ->
-// 1.680 ms (layer 2.678 -> 2.633 ms) with the plan and the claimed tails. Listing each XCD's full row blocks before
-// its light ones was slower everywhere (a light tile then no longer reads
-// its weight tiles while its expert's full tiles have them in L2), and
-// with hundreds of row blocks (Qwen3 / Qwen2 at M=8192: the cheap tiles
-// are spread over every XCD) the plan only adds its own time; GEMM2's tail
-// split already balances its last round.
+// 1.680 ms (layer 2.678 -> 2.633 ms) with the plan and the claimed tails.
+// Listing each XCD's full row blocks before its light ones was slower
+// everywhere (a light tile then no longer reads its weight tiles while its
+// expert's full tiles have them in L2), and with hundreds of row blocks
+// (Qwen3 / Qwen2 at M=8192: the cheap tiles are spread over every XCD) a
+// plan with claimed tails was slower (Qwen3 M=2048 GEMM1 +27 %, Qwen2 int8
+// M=1024 +15 %), so only launches of at most kPlanMaxRows row blocks get
+// one.
 constexpr int kPlanThreads = 256;
 constexpr int kPlanMaxRows = 64;  // row blocks a launch may have for a plan
 constexpr int kPlanWords = 9;

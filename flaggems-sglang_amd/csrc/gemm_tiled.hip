@@ -39,21 +39,28 @@ __device__ __forceinline__ bool tile_of(int pid, int grid, int n_rb, int n_ct,
                                         int group_m, int group_n, int* rb, int* ct) {
   const int logical = (pid % 8) * (grid / 8) + pid / 8;
   if (logical >= n_rb * n_ct) return false;
+  // both orders computed as values and stored once at the end (stores in
+  // each branch were merged into a store through a selected address, which
+  // kept rb / ct in scratch memory: a store and reload before every tile's
+  // first load)
+  int r, c;
   if (group_m > 0) {
     const int band_tiles = group_m * n_ct;
     const int band = logical / band_tiles;
     const int rem = logical - band * band_tiles;
     const int rows = min(group_m, n_rb - band * group_m);
-    *ct = rem / rows;
-    *rb = band * group_m + rem % rows;
-    return true;
+    c = rem / rows;
+    r = band * group_m + rem % rows;
+  } else {
+    const int span = n_rb * group_n;
+    const int group = logical / span;
+    const int idx = logical - group * span;
+    const int gsize = min(group_n, n_ct - group * group_n);
+    r = idx / gsize;
+    c = group * group_n + idx % gsize;
   }
-  const int span = n_rb * group_n;
-  const int group = logical / span;
-  const int idx = logical - group * span;
-  const int gsize = min(group_n, n_ct - group * group_n);
-  *rb = idx / gsize;
-  *ct = group * group_n + idx % gsize;
+  *rb = r;
+  *ct = c;
   return true;
 }
 
@@ -562,16 +569,31 @@ __device__ __forceinline__ void tiled_tile(const GemmParams& p, const int rb_id,
   };
   // writes the staged 32 x CH-chunk block: staged row sr goes to dst(sr)
   // (a byte address; null: not stored)
+  // (passes in groups of four: their staged values and row addresses --
+  // a lane shuffle each -- are read before their stores, so a group costs
+  // one LDS round trip instead of two per pass)
   auto drain = [&](auto ch_c, auto&& dst) {
     constexpr int CH = decltype(ch_c)::value;
+    constexpr int NP = 32 / (64 / CH);
+    constexpr int G = NP < 4 ? NP : 4;
+    static_assert(NP % G == 0, "passes in whole groups");
     stage_sync();
 #pragma unroll
-    for (int k = 0; k < 32 / (64 / CH); ++k) {
-      const int sr = k * (64 / CH) + lane / CH;
-      const int c = lane % CH;
-      const uint4 val = *reinterpret_cast<const uint4*>(slot_at(ch_c, sr, c));
-      uint8_t* d = dst(sr);
-      if (d) *reinterpret_cast<uint4*>(d + c * 16) = val;
+    for (int k0 = 0; k0 < NP; k0 += G) {
+      uint4 val[G];
+      uint8_t* d[G];
+#pragma unroll
+      for (int kq = 0; kq < G; ++kq) {
+        const int sr = (k0 + kq) * (64 / CH) + lane / CH;
+        const int c = lane % CH;
+        val[kq] = *reinterpret_cast<const uint4*>(slot_at(ch_c, sr, c));
+        d[kq] = dst(sr);
+      }
+#pragma unroll
+      for (int kq = 0; kq < G; ++kq) {
+        const int c = lane % CH;
+        if (d[kq]) *reinterpret_cast<uint4*>(d[kq] + c * 16) = val[kq];
+      }
     }
     stage_sync();
   };

@@ -995,19 +995,23 @@ bool wide_supported(int dt, bool gemm1, const GemmParams& p) {
   return p.a_rows > 0 && p.a_rows * row_bytes <= kMax && p.nrows_w * row_bytes <= kMax;
 }
 
-// Column-group width of the tile walk: 4 for a GEMM1 of >= 16 column tiles
-// over mostly full row blocks (>= 512 rows per expert; measured: Mixtral
-// M=4096 GEMM1 -1.1 %, layer -0.7 %, Qwen2 int8 M=8192 -0.3 %), else 8
-// (half-full blocks -- Mixtral M=512, Qwen2 M=1024 -- and Qwen3's 6-tile
-// GEMM1 are slower at 4). FGS_MOE_WIDE_GROUPN overrides it (a tuning aid,
-// read once).
-static int wide_group_n_choice(bool gemm1, int n_ct, double rows_per_expert) {
+// Column-group width of the tile walk. With a plan (few row blocks: about
+// one expert per XCD range) 8 for GEMM1 and 2 for GEMM2 (measured, Mixtral
+// M=4096, two runs each: GEMM1 1.700 ms at 8 against 1.712 at 4, GEMM2
+// 0.888 at 2 against 0.902 at 8). Without one, 4 for a GEMM1 of >= 16
+// column tiles over mostly full row blocks (>= 512 rows per expert: Qwen2
+// int8 M=8192 GEMM1 1.238 at 4 against 1.250 at 8), else 8 (half-full
+// blocks and Qwen3's 6-tile GEMM1 are slower at 4; Qwen2 int8 M=8192 GEMM2
+// 0.749 at 8 against 0.764 at 4). FGS_MOE_WIDE_GROUPN overrides it (a
+// tuning aid, read once).
+static int wide_group_n_choice(bool gemm1, int n_ct, double rows_per_expert, bool planned) {
   static const int g = [] {
     const char* s = tuning_env("FGS_MOE_WIDE_GROUPN");
     const int v = s ? atoi(s) : 0;
     return (v >= 1 && v <= 64) ? v : 0;
   }();
   if (g > 0) return g;
+  if (planned) return gemm1 ? 8 : 2;
   return gemm1 && n_ct >= 16 && rows_per_expert >= 512 ? 4 : 8;
 }
 
@@ -1042,7 +1046,8 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
   const int n_ct_walk = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   const double rows_per_expert =
       p.num_experts > 0 ? static_cast<double>(p.numel) / p.num_experts : 0.0;
-  if (q.group_n < 1) q.group_n = wide_group_n_choice(GEMM1, n_ct_walk, rows_per_expert);
+  if (q.group_n < 1)
+    q.group_n = wide_group_n_choice(GEMM1, n_ct_walk, rows_per_expert, q.plan != nullptr);
   // enough positions for the largest XCD walk the kernel can form from the
   // launched row blocks (it splits the live ones, known on the device), and
   // for the tail pieces of its last round

@@ -416,7 +416,8 @@ static int validate(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
 // ------------------------------------------------------ stage profiler ---
 // Per-thread record of HIP events around the stages of each fused call.
 struct StageProfiler {
-  int on = 0;  // 0 off, 1 every boundary, 2 the boundaries of stages 2..4
+  int on = 0;  // 0 off, 1 every boundary, 2 the boundaries of stages 2..4,
+               // 3 those of stage 2 (GEMM1) only
   std::vector<int> modes;  // the mode of each recorded call
   std::vector<std::array<hipEvent_t, FGS_PROFILE_STAGES + 1>> calls;
   std::vector<std::array<hipEvent_t, FGS_PROFILE_STAGES + 1>> pool;
@@ -445,7 +446,8 @@ struct StageProfiler {
     return true;
   }
   void mark(int i, hipStream_t s) {
-    if (cur && (on == 1 || (i >= 2 && i <= 5))) (void)hipEventRecord((*cur)[i], s);
+    if (cur && (on == 1 || (on == 2 && i >= 2 && i <= 5) || (on == 3 && (i == 2 || i == 3))))
+      (void)hipEventRecord((*cur)[i], s);
   }
 };
 static thread_local StageProfiler g_prof;
@@ -917,7 +919,7 @@ int32_t fgs_moe_validate(int64_t m, int64_t hidden, int64_t inter,
 }
 
 int32_t fgs_moe_profile_enable(int32_t on) {
-  if (on < 0 || on > 2) return fail(FGS_EINVAL, "profile mode must be 0, 1 or 2");
+  if (on < 0 || on > 3) return fail(FGS_EINVAL, "profile mode must be 0, 1, 2 or 3");
   g_prof.on = on;
   return FGS_OK;
 }
@@ -931,8 +933,9 @@ int32_t fgs_moe_profile_read(float* stage_ms, int32_t n_stages) {
     auto& ev = g_prof.calls[c];
     // stages whose two boundaries this call recorded (pooled events keep
     // older recordings, which must not be mixed in)
-    const bool all = g_prof.modes[c] == 1;
-    const int lo = all ? 0 : 2, hi = all ? FGS_PROFILE_STAGES : 5;
+    const int mode = g_prof.modes[c];
+    const int lo = mode == 1 ? 0 : 2;
+    const int hi = mode == 1 ? FGS_PROFILE_STAGES : mode == 2 ? 5 : 3;
     if (hipEventSynchronize(ev[hi]) != hipSuccess)
       return fail(FGS_ELAUNCH, "profile: event synchronisation failed");
     for (int i = lo; i < n_stages && i < hi; ++i) {

@@ -375,7 +375,8 @@ int32_t fgs_moe_fused_int8_channel(const void* x, const void* w13,
  * 3 GEMM2-input quantisation, 4 GEMM2, 5 top-k sum. Stages a mode does not
  * run read ~0. on = 1 records every stage boundary; on = 2 only those of
  * stages 2..4 (GEMM1 through GEMM2), so a timed run carries three fewer
- * events per call (the other stages then read 0); on = 0 stops. */
+ * events per call; on = 3 only GEMM1's two (the other stages then read
+ * 0); on = 0 stops. */
 #define FGS_PROFILE_STAGES 6
 int32_t fgs_moe_profile_enable(int32_t on);
 

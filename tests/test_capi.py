@@ -191,11 +191,11 @@ def test_entry_points_reject_bad_arguments_before_launch():
 
 
 def test_profile_modes():
-    """Stage profiler modes 0, 1 and 2 are accepted (host only); others fail."""
+    """Stage profiler modes 0..3 are accepted (host only); others fail."""
     lib = _capi.load()
-    for mode in (1, 2, 0):
+    for mode in (1, 2, 3, 0):
         assert lib.fgs_moe_profile_enable(mode) == 0
-    assert lib.fgs_moe_profile_enable(3) == _capi.FGS_EINVAL
+    assert lib.fgs_moe_profile_enable(4) == _capi.FGS_EINVAL
     assert "profile mode" in _capi.last_error()
     assert lib.fgs_moe_profile_enable(-1) == _capi.FGS_EINVAL
 

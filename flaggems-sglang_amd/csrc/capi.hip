@@ -355,7 +355,7 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   // gather costs what it saves)
   if (p.tiled && p.dt == kDtFp8 && p.tile_cfg == 0)
     p.o_xst = take((hidden / 128) * p.max_padded * 4);
-  // the 4-wave GEMM1's tile plan (256-row configuration)
+  // the 4-wave kernel's tile plan (256-row configuration; GEMM1, then GEMM2)
   p.o_plan = -1;
   if (p.tiled && p.tile_cfg == 0 && p.dt != kDtFp8) p.o_plan = take(4 * wide_plan_words());
   // a call on the routing tuple: each flat slot's expert id and gate scale

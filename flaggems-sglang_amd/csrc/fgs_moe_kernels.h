@@ -55,7 +55,7 @@ struct GemmParams {
   int64_t a_scale_kstride;    // tiled fp8: > 0 -> a_scale is k-block-major
                               // over the padded rows, a_scale[kb * stride +
                               // padded row]; 0 -> [rows][kblocks]
-  int32_t* plan;              // 4-wave GEMM1: workspace for its tile plan
+  int32_t* plan;              // 4-wave kernel: workspace for its tile plan
                               // (wide_plan_words ints; null: no plan, the
                               // tiles are split over the XCDs by count)
   const int32_t* route_hist;  // direct rows of a call on the routing tuple

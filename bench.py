@@ -525,8 +525,10 @@ def _kernel_stage(name, after_gemm1):
     x, after it the GEMM1 output."""
     if "fgs::" not in name:
         return None
-    if "align" in name:
+    if "align" in name or "routing_order" in name:  # the routing tuple's padded order
         return "align"
+    if "wide_plan" in name:  # the 4-wave kernel's tile plan, ahead of its GEMM
+        return "gemm2" if after_gemm1 else "gemm1"
     if "quant_" in name:
         return "quant_a2" if after_gemm1 else "quant_x"
     if "scale_gather" in name:  # x's scales into the padded row order

@@ -31,7 +31,7 @@
 
 namespace fgs {
 
-template <int SK_, int NS_>
+template <int SK_, int NS_, int NSB_>
 struct WideCfg {
   static constexpr int BM = 256;              // rows per tile (= alignment block)
   static constexpr int BNR = 256;             // weight rows per tile
@@ -41,7 +41,8 @@ struct WideCfg {
   static constexpr int RB = WROWS / 32;       // 32-row MFMA blocks per wave
   static constexpr int CB = WCOLS / 32;       // 32-col MFMA blocks per wave
   static constexpr int SK = SK_;              // k bytes per stage row
-  static constexpr int NS = NS_;              // ring slots
+  static constexpr int NS = NS_;              // activation ring slots
+  static constexpr int NSB = NSB_;            // weight ring slots
   static constexpr int KK = SK / 32;          // MFMA k steps per stage (32 bytes each)
   static constexpr int CPR = SK / 16;         // 16-byte chunks per stage row
   static constexpr int LR = 64 / CPR;         // rows one wave load (1 KiB) covers
@@ -50,19 +51,19 @@ struct WideCfg {
   static constexpr int NLB = BNR / (LR * NW);
   static constexpr int NL = NLA + NLB;
   static constexpr int SLOT = BM * SK;        // bytes per operand slot
-  static constexpr int B_OFF = NS * SLOT;
-  // past the ring: a 2 KiB table per wave of what the epilogue reads
-  // (column scales / bias, and per row the token slot and scales)
-  static constexpr int TAB_OFF = 2 * NS * SLOT;
+  static constexpr int B_OFF = NS * SLOT;     // the weight slots follow the activation slots
+  // a 2 KiB table per wave of what the epilogue reads (column scales /
+  // bias, and per row the token slot and scales), in an activation slot
+  // the last stage does not use
   static constexpr int TAB_BYTES = 2048;
-  static constexpr int LDS_BYTES = TAB_OFF + NW * TAB_BYTES;
+  static constexpr int LDS_BYTES = (NS + NSB) * SLOT;
   static_assert(BM == BNR, "one slot size for both operands");
   static_assert(KK % 2 == 0, "fragment double buffer wraps at a stage boundary");
-  static_assert(NS >= 2 && (NS - 2) * NL < 64, "ring depth / vmcnt range");
+  static_assert(NS == 2 && NSB == 3, "the refill schedule: weight rows a stage ahead");
+  static_assert(NW * TAB_BYTES <= SLOT, "the epilogue table fits a slot");
   static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KiB");
-  static_assert((NS - 1) * SLOT + (RB - 1) * 32 * SK < 65536, "ds_read offset range");
 };
-using WideRing = WideCfg<128, 2>;
+using WideRing = WideCfg<128, 2, 3>;
 
 // Position of logical 16-byte chunk c of stage row r: RPL rows share a
 // 256-byte bank line, and the XOR gives the 16 rows a fragment read serves
@@ -298,7 +299,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   constexpr bool INT8 = DT == kDtInt8;
   constexpr int ESZ = T::ESZ;
   constexpr int BM = C::BM, BNR = C::BNR, WCOLS = C::WCOLS;
-  constexpr int RB = C::RB, CB = C::CB, SK = C::SK, NS = C::NS, KK = C::KK;
+  constexpr int RB = C::RB, CB = C::CB, SK = C::SK, NS = C::NS, NSB = C::NSB, KK = C::KK;
   constexpr int NLA = C::NLA, NLB = C::NLB, NL = C::NL, SLOT = C::SLOT, B_OFF = C::B_OFF;
   static_assert(T::FC == 1, "one LDS chunk per fragment");
 
@@ -411,55 +412,57 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(p.a), 0, static_cast<int>(p.a_rows * row_bytes), kBufWord3);
   const int w_bytes = static_cast<int>(p.nrows_w * row_bytes);
-  // Loads of one stage (k offset kbyte) into ring slot `slot`.
-  auto issue = [&](const Src& s, int kbyte, int slot) {
+  // Loads of one stage (k offset kbyte) into the activation slot at byte
+  // offset oa and the weight slot at ob (of the weight slots).
+  auto issue = [&](const Src& s, int kbyte, int oa, int ob) {
     kbyte = __builtin_amdgcn_readfirstlane(kbyte);  // the scalar offset (uniform)
     const int e = __builtin_amdgcn_readfirstlane(s.e);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(p.w) + static_cast<int64_t>(e) * w_bytes, 0, w_bytes, kBufWord3);
-    uint8_t* a_dst = lds + slot * SLOT + wave * NLA * 1024;
-    uint8_t* b_dst = lds + B_OFF + slot * SLOT + wave * NLB * 1024;
+    uint8_t* a_dst = lds + oa + wave * NLA * 1024;
+    uint8_t* b_dst = lds + B_OFF + ob + wave * NLB * 1024;
 #pragma unroll
     for (int i = 0; i < NLA; ++i) lds_dma16_buf(ra, s.va[i], kbyte, a_dst + i * 1024);
 #pragma unroll
     for (int i = 0; i < NLB; ++i) lds_dma16_buf(rb, s.vb[i], kbyte, b_dst + i * 1024);
   };
-  // One operand's loads of a stage: PART 0 the activation rows, 1 the
-  // weight rows.
-  auto issue_part = [&](const Src& s, int kbyte, int slot, auto part_c) {
+  // One operand's loads of a stage: PART 0 the activation rows (into the
+  // activation slot at byte offset o), 1 the weight rows (the weight slot
+  // at o of the weight slots).
+  auto issue_part = [&](const Src& s, int kbyte, int o, auto part_c) {
     constexpr int PART = decltype(part_c)::value;
     kbyte = __builtin_amdgcn_readfirstlane(kbyte);
     if constexpr (PART == 0) {
-      uint8_t* a_dst = lds + slot * SLOT + wave * NLA * 1024;
+      uint8_t* a_dst = lds + o + wave * NLA * 1024;
 #pragma unroll
       for (int i = 0; i < NLA; ++i) lds_dma16_buf(ra, s.va[i], kbyte, a_dst + i * 1024);
     } else {
       const int e = __builtin_amdgcn_readfirstlane(s.e);
       const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<uint8_t*>(p.w) + static_cast<int64_t>(e) * w_bytes, 0, w_bytes, kBufWord3);
-      uint8_t* b_dst = lds + B_OFF + slot * SLOT + wave * NLB * 1024;
+      uint8_t* b_dst = lds + B_OFF + o + wave * NLB * 1024;
 #pragma unroll
       for (int i = 0; i < NLB; ++i) lds_dma16_buf(rb, s.vb[i], kbyte, b_dst + i * 1024);
     }
   };
 
   // Fragment reads: lane reads row (lane & 31) of a 32-row block, logical
-  // chunk 2*kk + (lane >> 5). Offsets within the wave's A / B region.
+  // chunk 2*kk + (lane >> 5): the lane's offset f_off[kk] within a block,
+  // the wave's blocks at a_base (block i of the wave: tile rows
+  // (2i + wm) * 32) and b_base (uniform) of a slot.
   const int fr = lane & 31;
-  int a_off[KK], b_off[KK];
+  int f_off[KK];
 #pragma unroll
-  for (int kk = 0; kk < KK; ++kk) {
-    const int o = fr * SK + wide_chunk<C>(fr, 2 * kk + (lane >> 5)) * 16;
-    a_off[kk] = wm * 32 * SK + o;  // block i of the wave: tile rows (2i + wm) * 32
-    b_off[kk] = B_OFF + wn * WCOLS * SK + o;
-  }
+  for (int kk = 0; kk < KK; ++kk) f_off[kk] = fr * SK + wide_chunk<C>(fr, 2 * kk + (lane >> 5)) * 16;
+  const int a_base = wm * 32 * SK;
+  const int b_base = B_OFF + wn * WCOLS * SK;
 
   Tile cur;
   if (GEMM1 && range.claims &&
       static_cast<int>(blockIdx.x / 8) >= range.hi - range.lo - kPlanClaimTail) {
     // a claimed position (one lane claims; the tile goes to every wave
-    // through the LDS table area, which the epilogue fills only later)
-    int* claim_s = reinterpret_cast<int*>(lds + C::TAB_OFF);
+    // through LDS, before any stage load writes it)
+    int* claim_s = reinterpret_cast<int*>(lds);
     if (threadIdx.x == 0) {
       const int me = static_cast<int>(blockIdx.x / 8);
       int owner = -1, pos = 0;
@@ -497,10 +500,11 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   int first_sid[RB];
 #pragma unroll
   for (int i = 0; i < RB; ++i) first_sid[i] = p.sorted_ids[row0 + i * 64 + wm * 32];
-  // stage s lives in ring slot s % NS; stages 0..NS-1 load first
+  // stage s lives in activation slot s % NS and weight slot s % NSB;
+  // stages 0 and 1 load first
   const int KT = cur.KT;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) issue(src, (cur.kt0 + s) * SK, s);
+  for (int s = 0; s < 2; ++s) issue(src, (cur.kt0 + s) * SK, s * SLOT, s * SLOT);
 
   // live 32-row blocks of this wave (pad rows are a suffix of the tile, so
   // the wave's live blocks are a prefix of i)
@@ -524,14 +528,15 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-    auto read_frags = [&](int slot, int kk, Frag (&a)[RB], Frag (&b)[CB]) {
-      const uint8_t* st = lds + slot * SLOT;
+    // (slots by byte offset: oa of the activation slots, ob of the weight
+    // slots)
+    auto read_frags = [&](int oa, int ob, int kk, Frag (&a)[RB], Frag (&b)[CB]) {
+      const uint8_t* sta = lds + (oa + a_base) + f_off[kk];
+      const uint8_t* stb = lds + (ob + b_base) + f_off[kk];
 #pragma unroll
-      for (int i = 0; i < RB; ++i)
-        a[i] = *reinterpret_cast<const Frag*>(st + a_off[kk] + i * 64 * SK);
+      for (int i = 0; i < RB; ++i) a[i] = *reinterpret_cast<const Frag*>(sta + i * 64 * SK);
 #pragma unroll
-      for (int j = 0; j < CB; ++j)
-        b[j] = *reinterpret_cast<const Frag*>(st + b_off[kk] + j * 32 * SK);
+      for (int j = 0; j < CB; ++j) b[j] = *reinterpret_cast<const Frag*>(stb + j * 32 * SK);
     };
     auto mma = [&](const Frag (&a)[RB], const Frag (&b)[CB]) {
 #pragma unroll
@@ -577,54 +582,51 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
       }
     };
     // The barrier before the last k step of stage s publishes stage s+1
-    // (every wave has waited for its own loads of it) and frees slot s % 2,
-    // which then takes stage s+2 when there is one: its activation rows
-    // right after the barrier, its weight rows during the first k step of
-    // stage s+1 (REFILL / PREV), so a CU's 64 loads of a stage are spread
-    // over two k steps instead of one (measured: Qwen3 M=8192 GEMM1 -6 %,
-    // GEMM2 -4 %, Qwen2 GEMM2 -4.5 %, Mixtral GEMM1 -1 %).
-    static_assert(NS == 2, "the refill schedule assumes a two-slot ring");
-    auto stage = [&](int s, auto refill_c, auto prev_c) {
+    // (every wave has waited for its own loads of it) and frees activation
+    // slot s % 2. Stage s+2, when there is one, loads its weight rows during
+    // the first k step of stage s (into weight slot (s+2) % 3, free since
+    // the barrier of stage s-1) and its activation rows right after that
+    // barrier (into slot s % 2), so a CU's 64 loads of a stage are spread
+    // over two k steps and the weight rows, which miss L2 more often, are
+    // in flight for seven k steps before a barrier waits for them.
+    // Slot byte offsets advance with the stage: activation 0, SLOT, 0, ...;
+    // weight 0, SLOT, 2 SLOT, 0, ...
+    auto next_b = [](int ob) { return ob == (NSB - 1) * SLOT ? 0 : ob + SLOT; };
+    auto prev_b = [](int ob) { return ob == 0 ? (NSB - 1) * SLOT : ob - SLOT; };
+    auto stage = [&](int s, int oa, int ob, auto refill_c) {
       constexpr bool REFILL = decltype(refill_c)::value;
-      constexpr bool PREV = decltype(prev_c)::value;
-      const int slot = s % NS;
 #pragma unroll
       for (int kk = 0; kk + 1 < KK; ++kk) {
-        read_frags(slot, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-        if (PREV && kk == 0)
-          issue_part(src, (cur.kt0 + s + 1) * SK, (s + 1) % NS, std::integral_constant<int, 1>{});
+        read_frags(oa, ob, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+        if (REFILL && kk == 0)  // weight slot (s + 2) % 3 = (s - 1) % 3
+          issue_part(src, (cur.kt0 + s + 2) * SK, prev_b(ob), std::integral_constant<int, 1>{});
         mma(fa[kk & 1], fb[kk & 1]);
-        if (PREV && kk == 0) sched_step(std::integral_constant<int, NLB>{});
+        if (REFILL && kk == 0) sched_step(std::integral_constant<int, NLB>{});
         else sched_step(std::integral_constant<int, 0>{});
         __builtin_amdgcn_sched_barrier(0);
       }
       wait_lgkm0();
-      wait_vmcnt<0>();
+      // stage s+2's weight rows may stay in flight
+      wait_vmcnt<REFILL ? NLB : 0>();
       wave_barrier_all();
-      read_frags((s + 1) % NS, 0, fa[0], fb[0]);
+      read_frags(oa ^ SLOT, next_b(ob), 0, fa[0], fb[0]);
       if constexpr (REFILL)
-        issue_part(src, (cur.kt0 + s + NS) * SK, slot, std::integral_constant<int, 0>{});
+        issue_part(src, (cur.kt0 + s + 2) * SK, oa, std::integral_constant<int, 0>{});
       mma(fa[1], fb[1]);
       sched_tail(std::integral_constant<int, REFILL ? NLA : 0>{});
       __builtin_amdgcn_sched_barrier(0);
     };
-    wait_vmcnt<(NS - 1) * NL>();
+    static_assert(NS == 2, "activation slot offsets toggle");
+    wait_vmcnt<NL>();
     wave_barrier_all();
-    read_frags(0, 0, fa[0], fb[0]);
-    int s = 0;
-    if (NS < KT) {
-      stage(0, std::true_type{}, std::false_type{});
-      for (s = 1; s + NS < KT; ++s) stage(s, std::true_type{}, std::true_type{});
-      if (s + 1 < KT) {
-        stage(s, std::false_type{}, std::true_type{});
-        ++s;
-      }
-    }
-    for (; s + 1 < KT; ++s) stage(s, std::false_type{}, std::false_type{});
-    const int slot = (KT - 1) % NS;
+    read_frags(0, 0, 0, fa[0], fb[0]);
+    int s = 0, oa = 0, ob = 0;
+    for (; s + 2 < KT; ++s, oa ^= SLOT, ob = next_b(ob)) stage(s, oa, ob, std::true_type{});
+    for (; s + 1 < KT; ++s, oa ^= SLOT, ob = next_b(ob)) stage(s, oa, ob, std::false_type{});
+    // the last stage (KT-1): oa, ob
 #pragma unroll
     for (int kk = 0; kk + 1 < KK; ++kk) {
-      read_frags(slot, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+      read_frags(oa, ob, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
       mma(fa[kk & 1], fb[kk & 1]);
       sched_step(std::integral_constant<int, 0>{});
       __builtin_amdgcn_sched_barrier(0);
@@ -635,10 +637,11 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     // (lane & 31) of each 32-row block and, per 32-column block, columns
     // 8*q + 4*(lane>>5) + {0..3} (accumulator registers 4q..4q+3). A store
     // straight from that layout would touch 32 output rows per
-    // instruction; instead each 32-row block goes through this wave's
-    // quarter of a free ring slot (stage KT-2's: no wave reads it again and
-    // no refill targets it) and leaves as whole row segments, 16 bytes per
-    // lane. Chunks (16 bytes) of a staged row are XOR-swizzled by the row so
+    // instruction; instead each 32-row block goes through this wave's half
+    // of a free weight slot (stage KT-2's for waves 0-1, the slot stage KT
+    // would take for waves 2-3: no wave reads them again and no refill
+    // targets them; other waves may still read stage KT-1's) and leaves as
+    // whole row segments, 16 bytes per lane. Chunks (16 bytes) of a staged row are XOR-swizzled by the row so
     // the column-major writes spread over the banks.
     {
       const int ks = cur.ks;
@@ -648,9 +651,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
       const int csub = 4 * (lane >> 5);
       const int half = lane >> 5;
       const float* wsc = INT8 ? p.w_scale + wbase : nullptr;
-      const int fslot = (KT - 2) % NS;
-      uint8_t* stg = lds + (wave < 2 ? fslot * SLOT + wave * (SLOT / 2)
-                                     : B_OFF + fslot * SLOT + (wave - 2) * (SLOT / 2));
+      const int fslot = wave < 2 ? (KT - 2) % NSB : KT % NSB;
+      uint8_t* stg = lds + B_OFF + fslot * SLOT + (wave % 2) * (SLOT / 2);
       static_assert(SLOT / 2 >= 32 * WCOLS * 4, "a 32-row fp32 block fits a wave's staging");
       auto value = [&](const Acc& a, int v, float sa, float sw) -> float {
         if constexpr (INT8) return static_cast<float>(a[v]) * sa * sw;
@@ -672,7 +674,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
       // scales (GEMM1: 64 gate, 64 up), [128, 256) bias (GEMM2) or router
       // weights (GEMM1), [256, 384) token slots, [384, 512) row scales;
       // row (block i, r) at i * 32 + r.
-      float* tab = reinterpret_cast<float*>(lds + C::TAB_OFF + wave * C::TAB_BYTES);
+      // (in stage KT-2's activation slot)
+      float* tab = reinterpret_cast<float*>(lds + ((KT - 2) % NS) * SLOT + wave * C::TAB_BYTES);
       int* tsid = reinterpret_cast<int*>(tab + 256);
       const bool woi = GEMM1 && p.weight_on_input;
       static_assert(RB * 32 <= 128, "table rows");

@@ -900,11 +900,11 @@ static int group_m_choice(int bm, const GemmParams& p) {
   if (g >= 0) return g;
   return bm == 128 && p.num_experts >= 64 && p.eid_shift == 0 ? 1 : 0;
 }
-// Which GEMMs of the 256-row configuration run the 4-wave kernel
-// (gemm_wide.hip): 1 (default) GEMM1 and short-k GEMM2s, 2 both always, 0
-// neither (FGS_MOE_WIDE, a tuning aid; read once).
+// Whether the GEMMs of the 256-row configuration run the 4-wave kernel
+// (gemm_wide.hip): 1 (default) both, 0 neither (FGS_MOE_WIDE, a tuning
+// aid; read once).
 static int wide_choice() {
-  static const int mode = env_choice("FGS_MOE_WIDE", 1, 0, 2);
+  static const int mode = env_choice("FGS_MOE_WIDE", 1, 0, 1);
   return mode;
 }
 static int group_n_choice() {
@@ -989,18 +989,20 @@ int tiled_config_supported(int dt, int cfg) {
 // * otherwise the 8-wave 128-row kernel from 24 rows (Mixtral M=256 -11 %,
 //   Qwen2 M=256 -6 %, DeepSeek M=1024 -4 %), and for many experts also from
 //   8 rows (Qwen2 M=64 -6 %, DeepSeek M=256/512 -3/-5 %, Qwen3 M=256 -7 %);
-// * the 32-row kernel below that (Mixtral M=32/64, DeepSeek M=32).
-// The 64-row configuration is no longer chosen; it stays for FGS_MOE_TILE.
+// * the 32-row kernel below that (Mixtral M=32/64, DeepSeek M=32);
+// * bf16 with few experts takes the 256-row configuration from 96 rows
+//   (Mixtral M=384 -1.5 %, 448 -4 %, 512 -3.5 %, 576 -10 %, 640 -3.5 %
+//   against the 160-row kernel that had those rows; M=256, 64 rows, stays
+//   on the 128-row kernel: +5 % on 256-row blocks).
+// The 64- and 160-row configurations are no longer chosen; they stay for
+// FGS_MOE_TILE.
 int tiled_config_for(int dt, double rows_per_expert, int num_experts) {
   const bool many = num_experts >= 32;
   int c = 3;
-  if (rows_per_expert >= 112 || (many && rows_per_expert >= 48)) c = 0;
+  if (rows_per_expert >= 112 || (many && rows_per_expert >= 48) ||
+      (dt == kDtBf16 && rows_per_expert >= 96))
+    c = 0;
   else if (rows_per_expert >= 24 || (many && rows_per_expert >= 8)) c = 1;
-  // bf16 with few experts at 96..159 rows each: 160-row blocks, one per
-  // expert (Mixtral M=512: 0.672 -> 0.600 ms; many-expert and fp8 layers
-  // lose with them: their 4-wave 160-row kernel keeps only one wave per
-  // SIMD on a long dependent MFMA / fold chain)
-  if (dt == kDtBf16 && !many && rows_per_expert >= 96 && rows_per_expert < 160) c = 4;
   if (forced_tile() >= 0) c = forced_tile();
   return c;
 }
@@ -1024,16 +1026,12 @@ int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
     return fail(FGS_EINVAL, "tiled GEMM: configuration " + std::to_string(cfg) +
                                 " not available for this element type");
   if (row_blocks <= 0) return FGS_OK;
-  // The 4-wave kernel runs GEMM1 of the 256-row configuration, and GEMM2
-  // where its k row is short (<= 8 KiB: Qwen3, Qwen2 int8 -2..-5 %); a long
-  // GEMM2 contraction (Mixtral, 28 KiB) keeps the 8-wave kernel (+6 % on
-  // the 4-wave one at M=4096). FGS_MOE_WIDE=2 forces it for every GEMM2.
-  const int64_t k_row = p.kdim * (dt == kDtBf16 ? 2 : 1);
-  const bool wide_gemm =
-      gemm1 ? wide_choice() >= 1
-            : (wide_choice() >= 2 ||
-               (wide_choice() == 1 && (k_row <= 8192 || (p.tail_split && p.tail_part))));
-  if (cfg == 0 && wide_gemm && wide_supported(dt, gemm1, p))
+  // The 4-wave kernel runs both GEMMs of the 256-row configuration: with
+  // its weight rows a stage ahead it also wins on the long GEMM2
+  // contraction it used to leave to the 8-wave kernel (Mixtral, 28 KiB k
+  // rows: M=512 with a k split GEMM2 0.192 -> 0.181 ms against the 160-row
+  // kernel, 0.210 against the 8-wave 256-row one; M=16384 3.35 -> 3.16 ms).
+  if (cfg == 0 && wide_choice() >= 1 && wide_supported(dt, gemm1, p))
     return launch_gemm_wide(dt, gemm1, p, row_blocks, stream);
   switch (dt) {
     case kDtBf16:

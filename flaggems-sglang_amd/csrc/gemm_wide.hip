@@ -11,12 +11,13 @@
 //   the pad rows of a partial block (a suffix) then fall evenly on both
 //   row halves, i.e. on all four SIMDs, whose all-pad blocks skip their
 //   MFMAs;
-// * operand tiles stream through an NS-slot LDS ring of SK-byte k stages
-//   (A slots first, then B slots) filled by buffer_load ... lds: one buffer
-//   resource per operand (the weight resource starts at the tile's expert),
-//   32-bit row offsets per lane and the k offset in the scalar offset, so a
-//   stage costs no address arithmetic. A stage's refill loads go out one
-//   between each pair of MFMAs of its last k step;
+// * operand tiles stream through an LDS ring of SK-byte k stages -- NS
+//   activation slots, then NSB weight slots -- filled by buffer_load ... lds:
+//   one buffer resource per operand (the weight resource starts at the
+//   tile's expert), 32-bit row offsets per lane and the k offset in the
+//   scalar offset, so a stage costs no address arithmetic. Stage s+2's
+//   weight rows go out during the first k step of stage s and its
+//   activation rows after stage s's barrier, each load between two MFMAs;
 // * tiles are ordered for the L2 of each XCD: the live tiles are cut into 8
 //   row-block-major ranges, one per XCD (about one expert in eight each),
 //   walked in column groups.

@@ -140,7 +140,7 @@ __device__ __forceinline__ bool wide_walk(int lo, int hi, int n_ct, int gn, int 
 // tile t writes fp32 partial sums to tail_part slot (xcd * 32 + t * S + i);
 // moe_wide_tail_fixup_kernel adds a tile's pieces in order. S = 1 (no
 // split) when rem is 0 or above 16; a piece keeps >= 2 stages of k (the
-// ring depth), so S <= KT_all / 2.
+// two stages the prologue loads), so S <= KT_all / 2.
 constexpr int kWideMaxPieces = 8;
 struct WideTail {
   int T, R, rem, S;
@@ -642,8 +642,9 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     // of a free weight slot (stage KT-2's for waves 0-1, the slot stage KT
     // would take for waves 2-3: no wave reads them again and no refill
     // targets them; other waves may still read stage KT-1's) and leaves as
-    // whole row segments, 16 bytes per lane. Chunks (16 bytes) of a staged row are XOR-swizzled by the row so
-    // the column-major writes spread over the banks.
+    // whole row segments, 16 bytes per lane. Chunks (16 bytes) of a staged
+    // row are XOR-swizzled by the row so the column-major writes spread over
+    // the banks.
     {
       const int ks = cur.ks;
       const int64_t wbase = static_cast<int64_t>(cur.e) * p.nrows_w;

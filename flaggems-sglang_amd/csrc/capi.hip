@@ -230,8 +230,8 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
       p.tile_cfg2 = 1;
       p.eid_shift2 = 1;
     }
-    // (the 160-row configuration is chosen below 160 rows per expert: about
-    // one block per touched expert)
+    // (the 160-row configuration, when forced, runs below 160 rows per
+    // expert: about one block per touched expert)
     p.ksplit2 = pick_ksplit(numel, e, tiled_block_m(p.tile_cfg2), hidden, inter * esz,
                             p.tile_cfg2 == 4 && rows_per_expert < 160);
     // a forced split still keeps >= 8 LDS stages of k per split

@@ -15,9 +15,11 @@
 //   activation slots, then NSB weight slots -- filled by buffer_load ... lds:
 //   one buffer resource per operand (the weight resource starts at the
 //   tile's expert), 32-bit row offsets per lane and the k offset in the
-//   scalar offset, so a stage costs no address arithmetic. Stage s+2's
-//   weight rows go out during the first k step of stage s and its
-//   activation rows after stage s's barrier, each load between two MFMAs;
+//   scalar offset, so a stage costs no address arithmetic. One operand has
+//   three slots and goes out two stages ahead, during the first k step of
+//   stage s; the other has two and goes out after stage s's barrier, each
+//   load between two MFMAs (the weight rows early, or for GEMM2 on large
+//   row counts the activation rows);
 // * tiles are ordered for the L2 of each XCD: the live tiles are cut into 8
 //   row-block-major ranges, one per XCD (about one expert in eight each),
 //   walked in column groups.
@@ -53,18 +55,22 @@ struct WideCfg {
   static constexpr int NL = NLA + NLB;
   static constexpr int SLOT = BM * SK;        // bytes per operand slot
   static constexpr int B_OFF = NS * SLOT;     // the weight slots follow the activation slots
+  // the operand with three slots is issued a stage earlier than the other
+  static constexpr bool EARLY_A = NS > NSB;
   // a 2 KiB table per wave of what the epilogue reads (column scales /
-  // bias, and per row the token slot and scales), in an activation slot
-  // the last stage does not use
+  // bias, and per row the token slot and scales), in a slot of the
+  // two-slot ring the last stage does not use
   static constexpr int TAB_BYTES = 2048;
   static constexpr int LDS_BYTES = (NS + NSB) * SLOT;
   static_assert(BM == BNR, "one slot size for both operands");
   static_assert(KK % 2 == 0, "fragment double buffer wraps at a stage boundary");
-  static_assert(NS == 2 && NSB == 3, "the refill schedule: weight rows a stage ahead");
+  static_assert((NS == 2 && NSB == 3) || (NS == 3 && NSB == 2),
+                "the refill schedule: one operand a stage ahead");
   static_assert(NW * TAB_BYTES <= SLOT, "the epilogue table fits a slot");
   static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KiB");
 };
-using WideRing = WideCfg<128, 2, 3>;
+using WideRing = WideCfg<128, 2, 3>;   // weight rows early
+using WideRingA = WideCfg<128, 3, 2>;  // activation rows early
 
 // Position of logical 16-byte chunk c of stage row r: RPL rows share a
 // 256-byte bank line, and the XOR gives the 16 rows a fragment read serves
@@ -583,47 +589,54 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
       }
     };
     // The barrier before the last k step of stage s publishes stage s+1
-    // (every wave has waited for its own loads of it) and frees activation
-    // slot s % 2. Stage s+2, when there is one, loads its weight rows during
-    // the first k step of stage s (into weight slot (s+2) % 3, free since
-    // the barrier of stage s-1) and its activation rows right after that
-    // barrier (into slot s % 2), so a CU's 64 loads of a stage are spread
-    // over two k steps and the weight rows, which miss L2 more often, are
-    // in flight for seven k steps before a barrier waits for them.
-    // Slot byte offsets advance with the stage: activation 0, SLOT, 0, ...;
-    // weight 0, SLOT, 2 SLOT, 0, ...
-    auto next_b = [](int ob) { return ob == (NSB - 1) * SLOT ? 0 : ob + SLOT; };
-    auto prev_b = [](int ob) { return ob == 0 ? (NSB - 1) * SLOT : ob - SLOT; };
+    // (every wave has waited for its own loads of it) and frees stage s's
+    // slots. Stage s+2, when there is one, loads its early operand (the one
+    // with three slots) during the first k step of stage s, into slot
+    // (s+2) % 3, free since the barrier of stage s-1, and its other operand
+    // right after that barrier, into slot s % 2. A CU's 64 loads of a stage
+    // are spread over two k steps, and the operand that misses L2 more often
+    // (the weight rows; in GEMM2 on large row counts the activation rows,
+    // gathered from an intermediate too large for the caches) is in flight
+    // for seven k steps before a barrier waits for it, the other for four.
+    // Slot byte offsets advance with the stage: 0, SLOT, 0, ... in the
+    // two-slot ring, 0, SLOT, 2 SLOT, 0, ... in the three-slot one.
+    auto next_a = [](int o) { return o == (NS - 1) * SLOT ? 0 : o + SLOT; };
+    auto prev_a = [](int o) { return o == 0 ? (NS - 1) * SLOT : o - SLOT; };
+    auto next_b = [](int o) { return o == (NSB - 1) * SLOT ? 0 : o + SLOT; };
+    auto prev_b = [](int o) { return o == 0 ? (NSB - 1) * SLOT : o - SLOT; };
+    constexpr bool EA = C::EARLY_A;
+    constexpr int NLE = EA ? NLA : NLB, NLL = EA ? NLB : NLA;  // early / late loads
     auto stage = [&](int s, int oa, int ob, auto refill_c) {
       constexpr bool REFILL = decltype(refill_c)::value;
 #pragma unroll
       for (int kk = 0; kk + 1 < KK; ++kk) {
         read_frags(oa, ob, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-        if (REFILL && kk == 0)  // weight slot (s + 2) % 3 = (s - 1) % 3
-          issue_part(src, (cur.kt0 + s + 2) * SK, prev_b(ob), std::integral_constant<int, 1>{});
+        if (REFILL && kk == 0)  // three-slot ring: slot (s + 2) % 3 = (s - 1) % 3
+          issue_part(src, (cur.kt0 + s + 2) * SK, EA ? prev_a(oa) : prev_b(ob),
+                     std::integral_constant<int, EA ? 0 : 1>{});
         mma(fa[kk & 1], fb[kk & 1]);
-        if (REFILL && kk == 0) sched_step(std::integral_constant<int, NLB>{});
+        if (REFILL && kk == 0) sched_step(std::integral_constant<int, NLE>{});
         else sched_step(std::integral_constant<int, 0>{});
         __builtin_amdgcn_sched_barrier(0);
       }
       wait_lgkm0();
-      // stage s+2's weight rows may stay in flight
-      wait_vmcnt<REFILL ? NLB : 0>();
+      // stage s+2's early loads may stay in flight
+      wait_vmcnt<REFILL ? NLE : 0>();
       wave_barrier_all();
-      read_frags(oa ^ SLOT, next_b(ob), 0, fa[0], fb[0]);
+      read_frags(next_a(oa), next_b(ob), 0, fa[0], fb[0]);
       if constexpr (REFILL)
-        issue_part(src, (cur.kt0 + s + 2) * SK, oa, std::integral_constant<int, 0>{});
+        issue_part(src, (cur.kt0 + s + 2) * SK, EA ? ob : oa,
+                   std::integral_constant<int, EA ? 1 : 0>{});
       mma(fa[1], fb[1]);
-      sched_tail(std::integral_constant<int, REFILL ? NLA : 0>{});
+      sched_tail(std::integral_constant<int, REFILL ? NLL : 0>{});
       __builtin_amdgcn_sched_barrier(0);
     };
-    static_assert(NS == 2, "activation slot offsets toggle");
     wait_vmcnt<NL>();
     wave_barrier_all();
     read_frags(0, 0, 0, fa[0], fb[0]);
     int s = 0, oa = 0, ob = 0;
-    for (; s + 2 < KT; ++s, oa ^= SLOT, ob = next_b(ob)) stage(s, oa, ob, std::true_type{});
-    for (; s + 1 < KT; ++s, oa ^= SLOT, ob = next_b(ob)) stage(s, oa, ob, std::false_type{});
+    for (; s + 2 < KT; ++s, oa = next_a(oa), ob = next_b(ob)) stage(s, oa, ob, std::true_type{});
+    for (; s + 1 < KT; ++s, oa = next_a(oa), ob = next_b(ob)) stage(s, oa, ob, std::false_type{});
     // the last stage (KT-1): oa, ob
 #pragma unroll
     for (int kk = 0; kk + 1 < KK; ++kk) {
@@ -639,9 +652,9 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     // 8*q + 4*(lane>>5) + {0..3} (accumulator registers 4q..4q+3). A store
     // straight from that layout would touch 32 output rows per
     // instruction; instead each 32-row block goes through this wave's half
-    // of a free weight slot (stage KT-2's for waves 0-1, the slot stage KT
-    // would take for waves 2-3: no wave reads them again and no refill
-    // targets them; other waves may still read stage KT-1's) and leaves as
+    // of a free slot of the three-slot ring (stage KT-2's for waves 0-1, the
+    // slot stage KT would take for waves 2-3: no wave reads them again and
+    // no refill targets them; other waves may still read stage KT-1's) and leaves as
     // whole row segments, 16 bytes per lane. Chunks (16 bytes) of a staged
     // row are XOR-swizzled by the row so the column-major writes spread over
     // the banks.
@@ -653,8 +666,9 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
       const int csub = 4 * (lane >> 5);
       const int half = lane >> 5;
       const float* wsc = INT8 ? p.w_scale + wbase : nullptr;
-      const int fslot = wave < 2 ? (KT - 2) % NSB : KT % NSB;
-      uint8_t* stg = lds + B_OFF + fslot * SLOT + (wave % 2) * (SLOT / 2);
+      constexpr int R3 = EA ? 0 : B_OFF, R2 = EA ? B_OFF : 0;  // three- / two-slot ring
+      const int fslot = wave < 2 ? (KT - 2) % 3 : KT % 3;
+      uint8_t* stg = lds + R3 + fslot * SLOT + (wave % 2) * (SLOT / 2);
       static_assert(SLOT / 2 >= 32 * WCOLS * 4, "a 32-row fp32 block fits a wave's staging");
       auto value = [&](const Acc& a, int v, float sa, float sw) -> float {
         if constexpr (INT8) return static_cast<float>(a[v]) * sa * sw;
@@ -676,8 +690,8 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
       // scales (GEMM1: 64 gate, 64 up), [128, 256) bias (GEMM2) or router
       // weights (GEMM1), [256, 384) token slots, [384, 512) row scales;
       // row (block i, r) at i * 32 + r.
-      // (in stage KT-2's activation slot)
-      float* tab = reinterpret_cast<float*>(lds + ((KT - 2) % NS) * SLOT + wave * C::TAB_BYTES);
+      // (in stage KT-2's slot of the two-slot ring)
+      float* tab = reinterpret_cast<float*>(lds + R2 + ((KT - 2) % 2) * SLOT + wave * C::TAB_BYTES);
       int* tsid = reinterpret_cast<int*>(tab + 256);
       const bool woi = GEMM1 && p.weight_on_input;
       static_assert(RB * 32 <= 128, "table rows");
@@ -982,7 +996,7 @@ int64_t wide_tail_part_bytes() {
 
 // Whether the 4-wave kernel covers a launch: bf16 / int8, GEMM1 with
 // the silu activation and no bias (gelu and the swiglu bias variant keep the
-// 8-wave kernel), k split into >= NS stages per split, output tiles that
+// 8-wave kernel), k split into >= 2 stages per split, output tiles that
 // divide n_out, and operands whose byte offsets fit the 32-bit buffer
 // addressing.
 bool wide_supported(int dt, bool gemm1, const GemmParams& p) {
@@ -994,7 +1008,7 @@ bool wide_supported(int dt, bool gemm1, const GemmParams& p) {
   const int64_t row_bytes = p.kdim * esz;
   if (row_bytes % C::SK != 0) return false;
   const int ks = std::max(1, gemm1 ? 1 : p.ksplit);
-  if (row_bytes / C::SK < static_cast<int64_t>(C::NS) * ks) return false;
+  if (row_bytes / C::SK < 2 * ks) return false;  // the prologue loads two stages
   if (p.n_out % (gemm1 ? C::BNR / 2 : C::BNR) != 0) return false;
   constexpr int64_t kMax = (int64_t{1} << 31) - 1;
   return p.a_rows > 0 && p.a_rows * row_bytes <= kMax && p.nrows_w * row_bytes <= kMax;
@@ -1029,9 +1043,25 @@ static bool plan_off() {
   return off;
 }
 
-template <int DT, bool GEMM1>
+// GEMM2's ring orientation: activation rows early from 512 rows per expert,
+// where its gathered intermediate rows outgrow the caches (measured, same
+// box, twice, GEMM2 with activation against weight rows early: Mixtral
+// M=2048 / 4096 -4.2 % / -1.7 %, Qwen2 int8 M=8192 -1.3 %, Qwen3 M=8192 and
+// Qwen2 int8 M=4096 level; below 512 rows weight rows early: Mixtral M=512
+// by 4 %, Qwen3 M=4096 by 1.5 %, Mixtral M=1024 level). FGS_MOE_WIDE_EARLY=0
+// / 1 forces weight / activation rows early (a tuning aid, read once).
+static bool wide_early_a_choice(const GemmParams& p) {
+  static const int forced = [] {
+    const char* s = tuning_env("FGS_MOE_WIDE_EARLY");
+    const int v = s ? atoi(s) : -1;
+    return (v == 0 || v == 1) ? v : -1;
+  }();
+  if (forced >= 0) return forced == 1;
+  return p.num_experts > 0 && p.numel >= 512LL * p.num_experts;
+}
+
+template <int DT, bool GEMM1, class C>
 static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream) {
-  using C = WideRing;
   auto kern = moe_gemm_wide_kernel<DT, GEMM1, C>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
@@ -1087,11 +1117,15 @@ int launch_gemm_wide(int dt, bool gemm1, const GemmParams& p, int row_blocks,
   if (!wide_supported(dt, gemm1, p))
     return fail(FGS_EINVAL, "wide GEMM: launch not covered by the 4-wave kernel");
   if (row_blocks <= 0) return FGS_OK;
-  if (dt == kDtBf16)
-    return gemm1 ? launch_wide_t<kDtBf16, true>(p, row_blocks, stream)
-                 : launch_wide_t<kDtBf16, false>(p, row_blocks, stream);
-  return gemm1 ? launch_wide_t<kDtInt8, true>(p, row_blocks, stream)
-               : launch_wide_t<kDtInt8, false>(p, row_blocks, stream);
+  const bool early_a = !gemm1 && wide_early_a_choice(p);
+  if (dt == kDtBf16) {
+    if (gemm1) return launch_wide_t<kDtBf16, true, WideRing>(p, row_blocks, stream);
+    return early_a ? launch_wide_t<kDtBf16, false, WideRingA>(p, row_blocks, stream)
+                   : launch_wide_t<kDtBf16, false, WideRing>(p, row_blocks, stream);
+  }
+  if (gemm1) return launch_wide_t<kDtInt8, true, WideRing>(p, row_blocks, stream);
+  return early_a ? launch_wide_t<kDtInt8, false, WideRingA>(p, row_blocks, stream)
+                 : launch_wide_t<kDtInt8, false, WideRing>(p, row_blocks, stream);
 }
 
 }  // namespace fgs

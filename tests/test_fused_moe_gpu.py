@@ -430,21 +430,27 @@ def _routing_with_counts(counts, device, seed):
     return w.to(device), ids.to(device)
 
 
-@pytest.mark.parametrize("mode,N", [("bf16", 256), ("bf16", 128), ("int8", 256),
-                                    ("fp8", 256)])
-def test_block_remainders(gpu, mode, N):
+_REMAINDER_CASES = [("bf16", 256, 1), ("bf16", 128, 1), ("int8", 256, 1), ("fp8", 256, 1),
+                    ("bf16", 256, 2), ("bf16", 128, 2), ("int8", 256, 2)]
+
+
+@pytest.mark.parametrize("mode,N,full", _REMAINDER_CASES,
+                         ids=[f"{m}-{n}-{f}" for m, n, f in _REMAINDER_CASES])
+def test_block_remainders(gpu, mode, N, full):
     """256-row tiles (the 4-wave kernel) on experts whose last block holds
-    1, 8, 31..33, 63..65 or 200 rows after one or two full blocks -- the
-    partially filled 32-row MFMA blocks and the all-pad ones the kernel
-    skips -- every token checked (N=128: a GEMM2 of two k stages, the ring
-    depth). fp8 (the 8-wave kernel): blocks of up to 160 rows run its
-    compact 4-slot ring, fuller ones the 3-slot ring over all 256 rows, so
-    its remainders straddle that edge."""
+    1, 8, 31..33, 63..65 or 200 rows after `full` or `full` + 1 full blocks
+    -- the partially filled 32-row MFMA blocks and the all-pad ones the
+    kernel skips -- every token checked (N=128: a GEMM2 of two k stages, the
+    ring depth; full=2: ~690 rows per expert, where GEMM2 issues its
+    activation rows rather than its weight rows a stage early). fp8 (the
+    8-wave kernel): blocks of up to 160 rows run its compact 4-slot ring,
+    fuller ones the 3-slot ring over all 256 rows, so its remainders
+    straddle that edge."""
     K, E = 512, 10
     rem = [1, 8, 31, 32, 33, 63, 64, 65, 200, 1]
     if mode == "fp8":
         rem = [1, 33, 128, 159, 160, 161, 200, 255, 65, 8]
-    counts = [256 * (1 + e % 2) + r for e, r in enumerate(rem)]
+    counts = [256 * (full + e % 2) + r for e, r in enumerate(rem)]
     w, ids = _routing_with_counts(counts, gpu, seed=N)
     M = ids.shape[0]
     wts = testing.make_weights(K, N, E, mode, 0.05, device=gpu, seed=K + N + 7)

@@ -16,8 +16,38 @@
 #include <string>
 
 #include "fgs_common.h"
+#include "fgs_moe_kernels.h"
 
 namespace fgs {
+
+// The 4-wave GEMMs' tile plans from the per-expert counts (one wave, once
+// the padded offsets are final): lane r costs row block r from the live rows
+// the expert holding it has there -- what wide_plan_kernel reads back from
+// the padded order -- so the GEMM launches need no plan kernel. The plans
+// need block_size 256 (the 4-wave kernel's row block).
+__device__ __forceinline__ void align_write_plans(int lane, const int32_t* off,
+                                                  const int32_t* tot, int E, int block_size,
+                                                  const WidePlanReq& r0, const WidePlanReq& r1) {
+  const int rows = off[E] / block_size;
+  int live = 0;
+  if (rows <= kPlanMaxRows && lane < rows) {
+    const int pos = lane * block_size;
+    // the expert holding padded position pos: the last e with off[e] <= pos
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (off[mid] <= pos) lo = mid;
+      else hi = mid - 1;
+    }
+    live = min(block_size, tot[lo] - (pos - off[lo]));
+  }
+  if (r0.plan)
+    wide_plan_write(lane, rows, live > 0 ? wide_plan_cost(live, r0.base) : 0, r0.n_ct, r0.cap,
+                    r0.plan);
+  if (r1.plan)
+    wide_plan_write(lane, rows, live > 0 ? wide_plan_cost(live, r1.base) : 0, r1.n_ct, r1.cap,
+                    r1.plan);
+}
 
 constexpr int kAlignWaves = 16;
 constexpr int64_t kAlignMultiMin = 4096;  // slots from which the multi-WG path runs
@@ -27,7 +57,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int num_experts,
     int block_size, int id_bits, int32_t* __restrict__ sorted_ids,
     int32_t* __restrict__ expert_ids, int32_t* __restrict__ num_post_pad,
-    int64_t max_padded) {
+    int64_t max_padded, WidePlanReq plan0, WidePlanReq plan1) {
   // cnt[w * E + e]: pass 1 count, then (after pass 2) the slot cursor.
   extern __shared__ int32_t smem[];
   int32_t* cnt = smem;                                  // [16][E]
@@ -100,6 +130,8 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     num_post_pad[0] = carry;
   }
   __syncthreads();
+  if (wave == 0 && (plan0.plan || plan1.plan))
+    align_write_plans(lane, off, tot, E, block_size, plan0, plan1);
 
   const int total_padded = off[E];
 
@@ -184,7 +216,8 @@ __global__ __launch_bounds__(kChunkThreads) void moe_align_scatter_kernel(
     const int32_t* __restrict__ ids, int64_t numel, int num_experts,
     int block_size, int id_bits, const int32_t* __restrict__ counts,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
-    int32_t* __restrict__ num_post_pad, int64_t max_padded) {
+    int32_t* __restrict__ num_post_pad, int64_t max_padded, WidePlanReq plan0,
+    WidePlanReq plan1) {
   extern __shared__ int32_t smem[];
   const int E = num_experts;
   int32_t* cnt = smem;                         // [4][E]: wave counts, then cursors
@@ -257,6 +290,8 @@ __global__ __launch_bounds__(kChunkThreads) void moe_align_scatter_kernel(
     if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
   }
   __syncthreads();
+  if (c == 0 && wave == 0 && (plan0.plan || plan1.plan))
+    align_write_plans(lane, off, tot, E, block_size, plan0, plan1);
   // cursors: expert offset + earlier chunks + earlier waves of this chunk
   for (int e = tid; e < E; e += kChunkThreads) {
     int run = off[e] + pre[e];
@@ -377,9 +412,16 @@ size_t align_smem_bytes(int num_experts) {
 int launch_align(const int32_t* ids, int64_t numel, int num_experts,
                  int block_size, int32_t* sorted_ids, int32_t* expert_ids,
                  int32_t* num_post_pad, int64_t max_padded,
-                 hipStream_t stream, int32_t* scratch) {
+                 hipStream_t stream, int32_t* scratch, const WidePlanReq* plans,
+                 bool* planned) {
   int id_bits = 0;
   while ((1 << id_bits) < num_experts) ++id_bits;
+  WidePlanReq plan0{}, plan1{};
+  if (plans && block_size == 256) {
+    plan0 = plans[0];
+    plan1 = plans[1];
+  }
+  if (planned) *planned = false;
   if (numel <= kWave) {
     hipLaunchKernelGGL(moe_align_wave_kernel, dim3(1), dim3(kWave), 0, stream, ids,
                        static_cast<int>(numel), num_experts, block_size, id_bits,
@@ -396,8 +438,10 @@ int launch_align(const int32_t* ids, int64_t numel, int num_experts,
     if (rc) return rc;
     hipLaunchKernelGGL(moe_align_scatter_kernel, dim3(nchunks), dim3(kChunkThreads),
                        smem2, stream, ids, numel, num_experts, block_size, id_bits,
-                       scratch, sorted_ids, expert_ids, num_post_pad, max_padded);
-    return check_launch("moe_align_scatter_kernel");
+                       scratch, sorted_ids, expert_ids, num_post_pad, max_padded, plan0, plan1);
+    rc = check_launch("moe_align_scatter_kernel");
+    if (!rc && planned) *planned = plan0.plan || plan1.plan;
+    return rc;
   }
   const size_t smem = align_smem_bytes(num_experts);
   if (smem > 64 * 1024) {
@@ -416,8 +460,10 @@ int launch_align(const int32_t* ids, int64_t numel, int num_experts,
   }
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), smem,
                      stream, ids, numel, num_experts, block_size, id_bits,
-                     sorted_ids, expert_ids, num_post_pad, max_padded);
-  return check_launch("moe_align_kernel");
+                     sorted_ids, expert_ids, num_post_pad, max_padded, plan0, plan1);
+  const int rc = check_launch("moe_align_kernel");
+  if (!rc && planned) *planned = plan0.plan || plan1.plan;
+  return rc;
 }
 
 }  // namespace fgs

@@ -78,7 +78,7 @@ struct Plan {
   int64_t max_padded, n_blocks, n_launch;
   // workspace layout (byte offsets)
   int64_t o_sorted, o_eids, o_npp, o_alg, o_a2, o_xq, o_xs, o_a2q, o_a2s, o_y, o_tail,
-      o_xst, o_rids, o_rw, o_plan,
+      o_xst, o_rids, o_rw, o_plan, o_plan2,
       total;
 };
 
@@ -356,8 +356,11 @@ static int make_plan(int64_t m, int64_t hidden, int64_t inter, int e, int topk,
   if (p.tiled && p.dt == kDtFp8 && p.tile_cfg == 0)
     p.o_xst = take((hidden / 128) * p.max_padded * 4);
   // the 4-wave kernel's tile plan (256-row configuration; GEMM1, then GEMM2)
-  p.o_plan = -1;
-  if (p.tiled && p.tile_cfg == 0 && p.dt != kDtFp8) p.o_plan = take(4 * wide_plan_words());
+  p.o_plan = p.o_plan2 = -1;
+  if (p.tiled && p.tile_cfg == 0 && p.dt != kDtFp8) {
+    p.o_plan = take(4 * wide_plan_words());   // GEMM1's tile plan
+    p.o_plan2 = take(4 * wide_plan_words());  // GEMM2's
+  }
   // a call on the routing tuple: each flat slot's expert id and gate scale
   p.o_rids = take(numel * 4);
   p.o_rw = take(numel * 4);
@@ -518,6 +521,7 @@ static int run_fused(const FusedArgs& a) {
   g_prof.mark(0, a.stream);
   int32_t* rids = reinterpret_cast<int32_t*>(ws + p.o_rids);
   const int32_t* route_hist = nullptr;
+  float* rw = p.o_rw >= 0 ? reinterpret_cast<float*>(ws + p.o_rw) : nullptr;
   if (routed && p.direct) {
     // one token: its gathered order is its slots' ascending expert order,
     // so GEMM rows are gathered positions, weighted by gate_scal as it
@@ -528,50 +532,32 @@ static int run_fused(const FusedArgs& a) {
     route_hist = a.expt_hist;
   } else if (routed) {
     // the routing tuple's gathered order is the alignment's order: one
-    // launch gives the padded order and each slot's expert and gate scale
-    float* rw = reinterpret_cast<float*>(ws + p.o_rw);
-    rc = launch_routing_order(a.gate_scal, a.gather_src, a.expt_hist, numel, a.e, p.block_m,
-                              p.max_padded, sorted, eids, npp, rids, rw, a.stream);
-    if (rc) return rc;
+    // launch (below) gives the padded order and each slot's expert and
+    // gate scale
     topk_w = rw;
     topk_ids = rids;
-  } else if (!p.direct) {
-    rc = launch_align(topk_ids, numel, a.e, p.block_m, sorted, eids, npp,
-                      p.max_padded, a.stream,
-                      p.o_alg >= 0 ? reinterpret_cast<int32_t*>(ws + p.o_alg) : nullptr);
-    if (rc) return rc;
   }
-  g_prof.mark(1, a.stream);
 
+  // operands of the two GEMMs (the quantised copies are written below)
   const bool on_input = (a.flags & FGS_FLAG_ROUTER_WEIGHT_ON_INPUT) != 0;
   const uint8_t* act = static_cast<const uint8_t*>(a.x);
   const float* act_scale = nullptr;
   if (p.qfold1) {
     // GEMM1 quantises x itself
   } else if (p.dt == kDtFp8) {
-    rc = launch_quant_fp8_group(a.x, ws + p.o_xq,
-                                reinterpret_cast<float*>(ws + p.o_xs), a.m,
-                                a.hidden, 128, a.stream);
-    if (rc) return rc;
     act = ws + p.o_xq;
-    act_scale = reinterpret_cast<const float*>(ws + p.o_xs);
-    if (p.o_xst >= 0) {
-      float* xst = reinterpret_cast<float*>(ws + p.o_xst);
-      rc = launch_scale_gather(act_scale, static_cast<int>(a.hidden / 128), sorted, npp, numel,
-                               a.topk, p.block_m, p.max_padded, xst, a.stream);
-      if (rc) return rc;
-      act_scale = xst;
-    }
+    act_scale = reinterpret_cast<const float*>(ws + (p.o_xst >= 0 ? p.o_xst : p.o_xs));
   } else if (p.dt == kDtInt8) {
-    rc = launch_quant_int8_token(a.x, reinterpret_cast<int8_t*>(ws + p.o_xq),
-                                 reinterpret_cast<float*>(ws + p.o_xs), a.m,
-                                 a.hidden, a.stream);
-    if (rc) return rc;
     act = ws + p.o_xq;
     act_scale = reinterpret_cast<const float*>(ws + p.o_xs);
   }
+  const uint8_t* act2 = reinterpret_cast<const uint8_t*>(a2);
+  const float* act2_scale = nullptr;
+  if (!p.qfold && p.dt != kDtBf16) {
+    act2 = ws + p.o_a2q;
+    act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
+  }
 
-  g_prof.mark(2, a.stream);
   GemmParams g1{};
   g1.a = act;
   g1.a_scale = act_scale;
@@ -603,42 +589,7 @@ static int run_fused(const FusedArgs& a) {
     g1.route_ids = rids;
   }
   if (p.qfold1) g1.a_src = static_cast<const uint16_t*>(a.x);
-  rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, static_cast<int>(p.n_launch),
-                                   a.stream)
-               : launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
-                                    static_cast<int>(p.direct ? numel : p.n_launch),
-                                    a.stream);
-  if (rc) return rc;
-  g_prof.mark(3, a.stream);
 
-  const uint8_t* act2 = reinterpret_cast<const uint8_t*>(a2);
-  const float* act2_scale = nullptr;
-  // direct rows: the compact slot rows; else only the padded rows in use
-  // (num_tokens_post_padded, on the device)
-  const int64_t a2_rows = p.direct ? numel : p.max_padded;
-  const int32_t* a2_npp = p.direct ? nullptr : npp;
-  const int32_t* a2_sorted = p.direct ? nullptr : sorted;
-  if (p.qfold) {
-    // GEMM2 quantises the a2 slot rows itself
-  } else if (p.dt == kDtFp8) {
-    // tiled: the scales k-block-major over the padded rows (see o_xst)
-    rc = launch_quant_fp8_group(a2, ws + p.o_a2q,
-                                reinterpret_cast<float*>(ws + p.o_a2s),
-                                a2_rows, a.inter, 128, a.stream, a2_npp, a2_sorted, numel,
-                                p.tiled ? p.max_padded : 0);
-    if (rc) return rc;
-    act2 = ws + p.o_a2q;
-    act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
-  } else if (p.dt == kDtInt8) {
-    rc = launch_quant_int8_token(a2, reinterpret_cast<int8_t*>(ws + p.o_a2q),
-                                 reinterpret_cast<float*>(ws + p.o_a2s),
-                                 a2_rows, a.inter, a.stream, a2_npp, a2_sorted, numel);
-    if (rc) return rc;
-    act2 = ws + p.o_a2q;
-    act2_scale = reinterpret_cast<const float*>(ws + p.o_a2s);
-  }
-
-  g_prof.mark(4, a.stream);
   GemmParams g2 = g1;
   g2.route_hist = nullptr;
   g2.a = act2;
@@ -657,6 +608,82 @@ static int run_fused(const FusedArgs& a) {
   g2.eid_shift = p.tiled ? p.eid_shift2 : 0;
   g2.a_src = p.qfold ? a2 : nullptr;
   g2.a_scale_kstride = p.tiled && p.dt == kDtFp8 ? p.max_padded : 0;
+  g2.plan = p.o_plan2 >= 0 ? reinterpret_cast<int32_t*>(ws + p.o_plan2) : nullptr;
+  const int rows1 = static_cast<int>(p.n_launch);
+  const int rows2 = static_cast<int>(p.n_launch << p.eid_shift2);
+
+  if (routed && !p.direct) {
+    rc = launch_routing_order(a.gate_scal, a.gather_src, a.expt_hist, numel, a.e, p.block_m,
+                              p.max_padded, sorted, eids, npp, rids, rw, a.stream);
+    if (rc) return rc;
+  } else if (!p.direct) {
+    // the alignment also writes the 4-wave GEMMs' tile plans (their launches
+    // then skip the plan kernel)
+    WidePlanReq req[2] = {};
+    if (p.tiled) {
+      tiled_plan_request(p.dt, p.tile_cfg, true, g1, rows1, &req[0]);
+      tiled_plan_request(p.dt, p.tile_cfg2, false, g2, rows2, &req[1]);
+    }
+    bool planned = false;
+    rc = launch_align(topk_ids, numel, a.e, p.block_m, sorted, eids, npp,
+                      p.max_padded, a.stream,
+                      p.o_alg >= 0 ? reinterpret_cast<int32_t*>(ws + p.o_alg) : nullptr,
+                      req, &planned);
+    if (rc) return rc;
+    g1.plan_ready = planned && req[0].plan ? 1 : 0;
+    g2.plan_ready = planned && req[1].plan ? 1 : 0;
+  }
+  g_prof.mark(1, a.stream);
+
+  if (p.dt == kDtFp8 && !p.qfold1) {
+    rc = launch_quant_fp8_group(a.x, ws + p.o_xq,
+                                reinterpret_cast<float*>(ws + p.o_xs), a.m,
+                                a.hidden, 128, a.stream);
+    if (rc) return rc;
+    if (p.o_xst >= 0) {
+      float* xst = reinterpret_cast<float*>(ws + p.o_xst);
+      rc = launch_scale_gather(reinterpret_cast<const float*>(ws + p.o_xs),
+                               static_cast<int>(a.hidden / 128), sorted, npp, numel,
+                               a.topk, p.block_m, p.max_padded, xst, a.stream);
+      if (rc) return rc;
+    }
+  } else if (p.dt == kDtInt8 && !p.qfold1) {
+    rc = launch_quant_int8_token(a.x, reinterpret_cast<int8_t*>(ws + p.o_xq),
+                                 reinterpret_cast<float*>(ws + p.o_xs), a.m,
+                                 a.hidden, a.stream);
+    if (rc) return rc;
+  }
+
+  g_prof.mark(2, a.stream);
+  rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg, true, g1, rows1, a.stream)
+               : launch_gemm_stream(p.dt, true, g1, p.mt, p.kw1,
+                                    static_cast<int>(p.direct ? numel : p.n_launch),
+                                    a.stream);
+  if (rc) return rc;
+  g_prof.mark(3, a.stream);
+
+  // direct rows: the compact slot rows; else only the padded rows in use
+  // (num_tokens_post_padded, on the device)
+  const int64_t a2_rows = p.direct ? numel : p.max_padded;
+  const int32_t* a2_npp = p.direct ? nullptr : npp;
+  const int32_t* a2_sorted = p.direct ? nullptr : sorted;
+  if (p.qfold) {
+    // GEMM2 quantises the a2 slot rows itself
+  } else if (p.dt == kDtFp8) {
+    // tiled: the scales k-block-major over the padded rows (see o_xst)
+    rc = launch_quant_fp8_group(a2, ws + p.o_a2q,
+                                reinterpret_cast<float*>(ws + p.o_a2s),
+                                a2_rows, a.inter, 128, a.stream, a2_npp, a2_sorted, numel,
+                                p.tiled ? p.max_padded : 0);
+    if (rc) return rc;
+  } else if (p.dt == kDtInt8) {
+    rc = launch_quant_int8_token(a2, reinterpret_cast<int8_t*>(ws + p.o_a2q),
+                                 reinterpret_cast<float*>(ws + p.o_a2s),
+                                 a2_rows, a.inter, a.stream, a2_npp, a2_sorted, numel);
+    if (rc) return rc;
+  }
+
+  g_prof.mark(4, a.stream);
   if (p.direct_sum) {
     // out = the weighted top-k sum, straight from GEMM2
     g2.out = a.out;
@@ -667,8 +694,7 @@ static int run_fused(const FusedArgs& a) {
     g_prof.mark(6, a.stream);
     return FGS_OK;
   }
-  rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg2, false, g2,
-                                   static_cast<int>(p.n_launch << p.eid_shift2), a.stream)
+  rc = p.tiled ? launch_gemm_tiled(p.dt, p.tile_cfg2, false, g2, rows2, a.stream)
                : launch_gemm_stream(p.dt, false, g2, p.mt, p.kw2,
                                     static_cast<int>(p.direct ? numel : p.n_launch),
                                     a.stream);

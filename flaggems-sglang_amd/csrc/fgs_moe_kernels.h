@@ -3,6 +3,7 @@
 #pragma once
 
 #include "fgs_common.h"
+#include "wide_plan.h"
 
 namespace fgs {
 
@@ -58,6 +59,9 @@ struct GemmParams {
   int32_t* plan;              // 4-wave kernel: workspace for its tile plan
                               // (wide_plan_words ints; null: no plan, the
                               // tiles are split over the XCDs by count)
+  int32_t plan_ready;         // 1: the alignment has written that plan (for
+                              // this launch's tiled_plan_request), so the
+                              // launch skips the plan kernel
   const int32_t* route_hist;  // direct rows of a call on the routing tuple
                               // (GEMM1): row j is gathered position j, its
                               // expert found from this histogram
@@ -80,10 +84,14 @@ size_t align_smem_bytes(int num_experts);
 int64_t align_scratch_bytes(int64_t numel, int num_experts);
 // With `scratch` (align_scratch_bytes of it) large inputs run on many
 // workgroups; without it, one workgroup. Same output either way.
+// `plans` (two requests, or null): the 4-wave GEMMs' tile plans, written
+// from the per-expert counts by the same launch; *planned says whether they
+// were (not on the single-wave path for at most 64 slots).
 int launch_align(const int32_t* ids, int64_t numel, int num_experts,
                  int block_size, int32_t* sorted_ids, int32_t* expert_ids,
                  int32_t* num_post_pad, int64_t max_padded, hipStream_t stream,
-                 int32_t* scratch = nullptr);
+                 int32_t* scratch = nullptr, const WidePlanReq* plans = nullptr,
+                 bool* planned = nullptr);
 
 // Routing-format conversion (routing.hip): the triton_kernels routing tuple
 // of _standard_topk_to_triton_kernels, block metadata for block_m in
@@ -165,6 +173,11 @@ int tiled_block_m(int cfg);
 int tiled_n_align(bool gemm1);
 int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
                       int row_blocks, hipStream_t stream);
+// The tile plan the launch of launch_gemm_tiled(dt, cfg, gemm1, p,
+// row_blocks, ...) would make (the 4-wave kernel with a plan), for the
+// alignment to write in its place; req->plan null: none.
+void tiled_plan_request(int dt, int cfg, bool gemm1, const GemmParams& p, int row_blocks,
+                        WidePlanReq* req);
 
 // 4-wave kernel of the 256-row configuration (bf16, int8): whether it
 // covers a launch, and the launch.
@@ -174,6 +187,8 @@ bool wide_supported(int dt, bool gemm1, const GemmParams& p);
 int64_t wide_tail_part_bytes();
 int launch_gemm_wide(int dt, bool gemm1, const GemmParams& p, int row_blocks,
                      hipStream_t stream);
+// The plan request of a launch_gemm_wide launch (req->plan null: no plan).
+void wide_plan_request(bool gemm1, const GemmParams& p, int row_blocks, WidePlanReq* req);
 // Ints of tile-plan workspace the 4-wave GEMM1 uses (gemm_wide.hip).
 int64_t wide_plan_words();
 

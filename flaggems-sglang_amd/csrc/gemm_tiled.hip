@@ -1020,6 +1020,14 @@ static int launch_cfg(bool gemm1, const GemmParams& p, int row_blocks,
                : launch_tiled<DT, C, false>(p, row_blocks, stream);
 }
 
+void tiled_plan_request(int dt, int cfg, bool gemm1, const GemmParams& p, int row_blocks,
+                        WidePlanReq* req) {
+  *req = WidePlanReq{};
+  if (tiled_config_supported(dt, cfg) && row_blocks > 0 && cfg == 0 && wide_choice() >= 1 &&
+      wide_supported(dt, gemm1, p))
+    wide_plan_request(gemm1, p, row_blocks, req);
+}
+
 int launch_gemm_tiled(int dt, int cfg, bool gemm1, const GemmParams& p,
                       int row_blocks, hipStream_t stream) {
   if (!tiled_config_supported(dt, cfg))

@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "gemm_tiled_common.h"
+#include "wide_plan.h"
 
 namespace fgs {
 
@@ -168,14 +169,17 @@ constexpr int kWideTailSlots = 8 * 32;  // tail_part slots: 32 per XCD
 // Mixtral M=4096 GEMM1: 84 vs 117 us, GEMM2: 308-324 vs 361-386 us -- and
 // with few row blocks (about one expert per XCD) the even split by count
 // gave whole XCDs those cheap tiles: their CUs went idle for the last ~8 %
-// of GEMM1 while the other XCDs finished full tiles. The plan, made by one
-// workgroup before the GEMM:
+// of GEMM1 while the other XCDs finished full tiles. The plan, made before
+// the GEMM:
 //  * costs each row block at base + ceil(live / 2), live = the live 32-row
 //    blocks of its first wave row (1..4);
 //  * cuts the row-block-major tile sequence into 8 contiguous ranges of
 //    equal cost (contiguous, so an XCD still holds about one expert in
 //    eight), or of equal count when an equal-cost range would hold more
 //    tiles than the launch has positions for.
+// The alignment writes both GEMMs' plans from its per-expert counts when it
+// runs in the same call (wide_plan.h); otherwise wide_plan_kernel writes a
+// GEMM's plan from the padded order, ahead of it.
 // plan[0..8]: the ranges' bounds in tile index (plan[0] = -1: no plan);
 // then one claim counter per XCD, each in its own 256-byte slot. The XCDs'
 // tiles still take different times (per XCD, full tiles averaged 113-121
@@ -199,78 +203,24 @@ constexpr int kWideTailSlots = 8 * 32;  // tail_part slots: 32 per XCD
 // plan with claimed tails was slower (Qwen3 M=2048 GEMM1 +27 %, Qwen2 int8
 // M=1024 +15 %), so only launches of at most kPlanMaxRows row blocks get
 // one.
-constexpr int kPlanThreads = 256;
-constexpr int kPlanMaxRows = 64;  // row blocks a launch may have for a plan
-constexpr int kPlanWords = 9;
-constexpr int kPlanClaimStride = 64;  // ints: one 256-byte slot per XCD counter
-constexpr int kPlanClaimTail = 64;    // positions at the end of a range that are claimed
-// row-block cost = base + ceil(live 32-row blocks / 2): a block of a few
-// rows costs 6/9 of a full one in GEMM1 (measured 0.65-0.72) and 16/19 in
-// GEMM2 (measured 0.80-0.85: its k rows are longer)
-constexpr int kPlanBaseGemm1 = 5;
-constexpr int kPlanBaseGemm2 = 15;
-
-__global__ __launch_bounds__(kPlanThreads) void wide_plan_kernel(
+// The plan from the padded order (calls whose alignment did not write it):
+// one wave, lane r costs row block r from its 32-row groups' first slots.
+__global__ __launch_bounds__(kWave) void wide_plan_kernel(
     const int32_t* __restrict__ sorted_ids, const int32_t* __restrict__ num_post_pad, int numel,
     int bm, int n_ct, int cap, int base, int32_t* __restrict__ plan) {
-  __shared__ int pref_s[kPlanThreads];
-  __shared__ int bound_s[9];
-  const int tid = threadIdx.x;
-  if (tid < 8) plan[kPlanWords + tid * kPlanClaimStride] = 0;  // nothing claimed yet
+  const int lane = threadIdx.x;
   const int rows = num_post_pad[0] / bm;
-  if (rows <= 0 || rows > kPlanMaxRows) {
-    if (tid == 0) plan[0] = -1;  // the kernel splits its tiles evenly
-    return;
-  }
   int c = 0;
-  if (tid < rows) {
+  if (rows <= kPlanMaxRows && lane < rows) {
     int sid[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sid[j] = 32 * j < bm ? sorted_ids[tid * bm + 32 * j] : numel;
+    for (int j = 0; j < 8; ++j) sid[j] = 32 * j < bm ? sorted_ids[lane * bm + 32 * j] : numel;
     int lb = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) lb += sid[j] < numel ? 1 : 0;
-    c = base + (lb + 1) / 2;
+    c = wide_plan_cost(32 * lb, base);
   }
-  // inclusive sums of the row costs (one wave: rows <= 64)
-  int incl = c;
-  if (tid < 64) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(incl, d, 64);
-      if ((tid & 63) >= d) incl += o;
-    }
-    pref_s[tid] = incl;
-  }
-  __syncthreads();
-  const int64_t total_cost = static_cast<int64_t>(pref_s[63]) * n_ct;
-  const int64_t total_tiles = static_cast<int64_t>(rows) * n_ct;
-  // bound x: the first tile whose start cost reaches total_cost * x / 8 --
-  // in row tid when that row's cost range holds it
-  if (tid < rows) {
-    const int64_t lo_cost = static_cast<int64_t>(incl - c) * n_ct;
-    const int64_t hi_cost = static_cast<int64_t>(incl) * n_ct;
-    for (int x = 1; x < 8; ++x) {
-      const int64_t target = total_cost * x / 8;
-      if (target > lo_cost && target <= hi_cost) {
-        const int into = static_cast<int>(target - lo_cost);  // < n_ct * c
-        bound_s[x] = tid * n_ct + (into + c - 1) / c;
-      } else if (tid == 0 && target <= 0) {
-        bound_s[x] = 0;
-      }
-    }
-  }
-  if (tid == 0) {
-    bound_s[0] = 0;
-    bound_s[8] = static_cast<int>(total_tiles);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    bool even = false;
-    for (int x = 0; x < 8; ++x) even |= bound_s[x + 1] - bound_s[x] > cap;
-    for (int x = 0; x <= 8; ++x)
-      plan[x] = even ? static_cast<int>(total_tiles * x / 8) : bound_s[x];
-  }
+  wide_plan_write(lane, rows, c, n_ct, cap, plan);
 }
 
 int64_t wide_plan_words() { return kPlanWords + 8 * kPlanClaimStride; }
@@ -1060,6 +1010,39 @@ static bool wide_early_a_choice(const GemmParams& p) {
   return p.num_experts > 0 && p.numel >= 512LL * p.num_experts;
 }
 
+// A launch's normalised parameters (k split, tail split, whether it has a
+// plan) and the positions per XCD its whole tiles may take: the even split
+// needs total / 8; a cost-balanced plan may give an XCD up to a quarter more
+// (the plan falls back to the even split beyond that).
+static void wide_launch_shape(bool gemm1, const GemmParams& p, int row_blocks, GemmParams* q,
+                              int64_t* cap) {
+  using C = WideRing;
+  *q = p;
+  q->row_blocks = row_blocks;
+  if (gemm1 || q->ksplit < 1) q->ksplit = 1;
+  if (gemm1 || !q->tail_part) q->tail_split = 0;
+  if (q->tail_split) q->ksplit = 1;
+  // the plan: few row blocks, whole tiles (see wide_plan_kernel)
+  if (row_blocks > kPlanMaxRows || q->ksplit > 1 || plan_off()) q->plan = nullptr;
+  const int n_ct = static_cast<int>(gemm1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
+  const int64_t total = static_cast<int64_t>(row_blocks) * q->ksplit * n_ct;
+  *cap = (total + 7) / 8;
+  if (q->plan) *cap = *cap * 5 / 4 + 1;
+}
+
+void wide_plan_request(bool gemm1, const GemmParams& p, int row_blocks, WidePlanReq* req) {
+  using C = WideRing;
+  GemmParams q;
+  int64_t cap;
+  wide_launch_shape(gemm1, p, row_blocks, &q, &cap);
+  *req = WidePlanReq{};
+  if (!q.plan) return;
+  req->plan = q.plan;
+  req->n_ct = static_cast<int32_t>(gemm1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
+  req->cap = static_cast<int32_t>(cap);
+  req->base = gemm1 ? kPlanBaseGemm1 : kPlanBaseGemm2;
+}
+
 template <int DT, bool GEMM1, class C>
 static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream) {
   auto kern = moe_gemm_wide_kernel<DT, GEMM1, C>;
@@ -1071,13 +1054,9 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
   });
   if (attr != hipSuccess)
     return fail(FGS_ELAUNCH, std::string("wide GEMM LDS opt-in: ") + hipGetErrorString(attr));
-  GemmParams q = p;
-  q.row_blocks = row_blocks;
-  if (GEMM1 || q.ksplit < 1) q.ksplit = 1;
-  if (GEMM1 || !q.tail_part) q.tail_split = 0;
-  if (q.tail_split) q.ksplit = 1;
-  // the plan: few row blocks, whole tiles (see wide_plan_kernel)
-  if (row_blocks > kPlanMaxRows || q.ksplit > 1 || plan_off()) q.plan = nullptr;
+  GemmParams q;
+  int64_t cap;
+  wide_launch_shape(GEMM1, p, row_blocks, &q, &cap);
   const int n_ct_walk = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   const double rows_per_expert =
       p.num_experts > 0 ? static_cast<double>(p.numel) / p.num_experts : 0.0;
@@ -1087,20 +1066,17 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
   // launched row blocks (it splits the live ones, known on the device), and
   // for the tail pieces of its last round
   const int n_ct = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
-  const int64_t total = static_cast<int64_t>(row_blocks) * q.ksplit * n_ct;
-  // positions per XCD for whole tiles: the even split needs total / 8; a
-  // cost-balanced plan may give an XCD up to a quarter more (its plan
-  // falls back to the even split beyond that)
-  int64_t cap = (total + 7) / 8;
   int64_t extra = 0;  // positions past an XCD's range (claims of others' tails)
   if (q.plan) {
-    cap = cap * 5 / 4 + 1;
     extra = GEMM1 ? 32 : 0;
-    hipLaunchKernelGGL(wide_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, q.sorted_ids,
-                       q.num_post_pad, static_cast<int>(q.numel), C::BM, n_ct,
-                       static_cast<int>(cap), GEMM1 ? kPlanBaseGemm1 : kPlanBaseGemm2, q.plan);
-    const int rc = check_launch("wide_plan_kernel");
-    if (rc) return rc;
+    if (!q.plan_ready) {
+      hipLaunchKernelGGL(wide_plan_kernel, dim3(1), dim3(kWave), 0, stream, q.sorted_ids,
+                         q.num_post_pad, static_cast<int>(q.numel), C::BM, n_ct,
+                         static_cast<int>(cap), GEMM1 ? kPlanBaseGemm1 : kPlanBaseGemm2,
+                         q.plan);
+      const int rc = check_launch("wide_plan_kernel");
+      if (rc) return rc;
+    }
   }
   const int64_t n_pos = cap + extra + (q.tail_split ? 32 : 0);
   const int grid = static_cast<int>(8 * n_pos);

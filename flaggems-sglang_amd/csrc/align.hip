@@ -5,7 +5,8 @@
 // flattened expert ids (:134) and a per-expert histogram (:137-139). The
 // output is the block-padded, expert-grouped order the grouped GEMMs consume.
 //
-// One workgroup of 16 wave64s. Wave w owns the contiguous slot segment
+// One workgroup of 16 wave64s (and, asked for tile plans, a second that
+// writes them). Wave w owns the contiguous slot segment
 // [w*seg, (w+1)*seg). Pass 1 counts ids per (wave, expert) in LDS; pass 2
 // turns the counts into per-expert padded offsets plus per-wave offsets
 // inside each expert (exclusive over waves, so lower slots come first);
@@ -24,7 +25,10 @@ namespace fgs {
 // the padded offsets are final): lane r costs row block r from the live rows
 // the expert holding it has there -- what wide_plan_kernel reads back from
 // the padded order -- so the GEMM launches need no plan kernel. The plans
-// need block_size 256 (the 4-wave kernel's row block).
+// need block_size 256 (the 4-wave kernel's row block). An extra workgroup of
+// the alignment launch writes them: it redoes the counts and the padded
+// scan beside the others and stops there, so the plans stay off the
+// critical path of the scatter.
 __device__ __forceinline__ void align_write_plans(int lane, const int32_t* off,
                                                   const int32_t* tot, int E, int block_size,
                                                   const WidePlanReq& r0, const WidePlanReq& r1) {
@@ -127,11 +131,13 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
   if (tid == 0) {
     off[E] = carry;
-    num_post_pad[0] = carry;
+    if (blockIdx.x == 0) num_post_pad[0] = carry;
   }
   __syncthreads();
-  if (wave == 0 && (plan0.plan || plan1.plan))
-    align_write_plans(lane, off, tot, E, block_size, plan0, plan1);
+  if (blockIdx.x == 1) {  // the plan workgroup
+    if (wave == 0) align_write_plans(lane, off, tot, E, block_size, plan0, plan1);
+    return;
+  }
 
   const int total_padded = off[E];
 
@@ -229,7 +235,8 @@ __global__ __launch_bounds__(kChunkThreads) void moe_align_scatter_kernel(
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int c = blockIdx.x;
-  const int nchunks = gridDim.x;
+  // with plans, the last workgroup writes them and scatters nothing
+  const int nchunks = gridDim.x - (plan0.plan || plan1.plan ? 1 : 0);
 
   for (int e = tid; e < E; e += kChunkThreads) {
     // 16 chunks' counts in flight at a time (integer sums: any order)
@@ -281,6 +288,11 @@ __global__ __launch_bounds__(kChunkThreads) void moe_align_scatter_kernel(
   }
   if (tid == 0) off[E] = carry;
   if (c == 0 && tid == 0) num_post_pad[0] = carry;
+  if (c == nchunks) {  // the plan workgroup
+    __syncthreads();
+    if (wave == 0) align_write_plans(lane, off, tot, E, block_size, plan0, plan1);
+    return;
+  }
 
   // this chunk's per-(wave, expert) counts; each wave owns 256 slots
   const int64_t wbeg = static_cast<int64_t>(c) * kChunk + wave * (kChunk / kChunkWaves);
@@ -290,8 +302,6 @@ __global__ __launch_bounds__(kChunkThreads) void moe_align_scatter_kernel(
     if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
   }
   __syncthreads();
-  if (c == 0 && wave == 0 && (plan0.plan || plan1.plan))
-    align_write_plans(lane, off, tot, E, block_size, plan0, plan1);
   // cursors: expert offset + earlier chunks + earlier waves of this chunk
   for (int e = tid; e < E; e += kChunkThreads) {
     int run = off[e] + pre[e];
@@ -436,7 +446,9 @@ int launch_align(const int32_t* ids, int64_t numel, int num_experts,
                        smem1, stream, ids, numel, num_experts, scratch);
     int rc = check_launch("moe_align_count_kernel");
     if (rc) return rc;
-    hipLaunchKernelGGL(moe_align_scatter_kernel, dim3(nchunks), dim3(kChunkThreads),
+    const bool with_plans = plan0.plan || plan1.plan;
+    hipLaunchKernelGGL(moe_align_scatter_kernel, dim3(nchunks + (with_plans ? 1 : 0)),
+                       dim3(kChunkThreads),
                        smem2, stream, ids, numel, num_experts, block_size, id_bits,
                        scratch, sorted_ids, expert_ids, num_post_pad, max_padded, plan0, plan1);
     rc = check_launch("moe_align_scatter_kernel");
@@ -458,7 +470,8 @@ int launch_align(const int32_t* ids, int64_t numel, int num_experts,
       return fail(FGS_ELAUNCH, std::string("moe_align_kernel LDS opt-in: ") +
                                    hipGetErrorString(attr_err));
   }
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), smem,
+  const bool with_plans = plan0.plan || plan1.plan;
+  hipLaunchKernelGGL(moe_align_kernel, dim3(with_plans ? 2 : 1), dim3(kAlignThreads), smem,
                      stream, ids, numel, num_experts, block_size, id_bits,
                      sorted_ids, expert_ids, num_post_pad, max_padded, plan0, plan1);
   const int rc = check_launch("moe_align_kernel");

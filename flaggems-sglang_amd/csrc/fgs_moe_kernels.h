@@ -31,6 +31,10 @@ struct GemmParams {
   int64_t nrows_w;
   int64_t numel;
   int32_t topk;
+  // slot / topk as (t + ((slot - t) >> topk_sh1)) >> topk_sh2, t = the high
+  // word of topk_magic * slot (set by the 4-wave kernel's launch)
+  uint32_t topk_magic;
+  int32_t topk_sh1, topk_sh2;
   int32_t weight_on_input;
   int32_t row_blocks;     // row blocks of the launch (tiled kernels)
   int32_t group_m;        // row blocks per rasterization band (tiled; 0: off)

@@ -309,8 +309,6 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     t.ct = ct;
     t.ks = rball / rb_live;
     t.rb = rball - t.ks * rb_live;
-    t.e = __builtin_amdgcn_readfirstlane(p.expert_ids[t.rb]);
-    if (t.e < 0) return false;
     if (piece >= 0) {
       t.kt0 = piece * KT_all / tail.S;
       t.KT = (piece + 1) * KT_all / tail.S - t.kt0;
@@ -329,11 +327,15 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     int e;  // expert of the weight rows
     uint32_t va[NLA], vb[NLB];
   };
+  // slot / topk without a division (the launch's magic number)
+  auto div_topk = [&](int n) -> int {
+    const uint32_t t1 = __umulhi(p.topk_magic, static_cast<uint32_t>(n));
+    return static_cast<int>((t1 + ((static_cast<uint32_t>(n) - t1) >> p.topk_sh1)) >> p.topk_sh2);
+  };
   const int lrow = lane / C::CPR;   // row of a load this lane copies
   const int lchunk = lane % C::CPR;  // its physical chunk
   auto make_src = [&](const Tile& t, Src& s) {
     const int row0 = t.rb * BM;
-    s.e = t.e;
     // all token slots first: computing a row (GEMM1 divides by topk for
     // real rows only) compiles to a branch, which would otherwise hold each
     // load back until the previous row is done
@@ -344,7 +346,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     for (int i = 0; i < NLA; ++i) {
       const int r = (wave * NLA + i) * C::LR + lrow;
       const bool ok = sid[i] < p.numel;
-      const int64_t arow = GEMM1 ? (ok ? sid[i] / p.topk : 0) : row0 + (ok ? r : 0);
+      const int64_t arow = GEMM1 ? (ok ? div_topk(sid[i]) : 0) : row0 + (ok ? r : 0);
       s.va[i] = static_cast<uint32_t>(arow * row_bytes + wide_chunk<C>(r, lchunk) * 16);
     }
 #pragma unroll
@@ -448,8 +450,14 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
   } else {
     if (!live_tile(range, static_cast<int>(blockIdx.x / 8), cur)) return;
   }
+  // the tile's expert loads beside its token slots (make_src), so the two
+  // round trips overlap
+  const int e_tile = p.expert_ids[cur.rb];
   Src src;
   make_src(cur, src);
+  cur.e = __builtin_amdgcn_readfirstlane(e_tile);
+  if (cur.e < 0) return;
+  src.e = cur.e;
   const int row0 = cur.rb * BM;
   // the first token slot of each of the wave's 32-row blocks, loaded before
   // the stage loads: the counter drains in issue order, so waiting on these
@@ -656,7 +664,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
           const int t = i * 32 + (lane & 31);
           tsid[t] = sid;
           if constexpr (INT8)
-            tab[384 + t] = p.a_scale[GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? rr : 0)];
+            tab[384 + t] = p.a_scale[GEMM1 ? (ok ? div_topk(sid) : 0) : row0 + (ok ? rr : 0)];
           if (woi) tab[128 + t] = ok ? p.topk_w[sid] : 1.f;
         }
       }
@@ -1010,6 +1018,20 @@ static bool wide_early_a_choice(const GemmParams& p) {
   return p.num_experts > 0 && p.numel >= 512LL * p.num_experts;
 }
 
+// Division by topk as a multiply and two shifts (Granlund and Montgomery,
+// "Division by Invariant Integers using Multiplication", PLDI 1994, unsigned
+// case, exact for every 32-bit numerator): l = ceil(log2 d), magic =
+// floor(2^32 (2^l - d) / d) + 1, q = (t + ((n - t) >> min(l, 1))) >>
+// max(l - 1, 0) with t = the high word of magic * n.
+static void set_topk_magic(GemmParams* q) {
+  const uint32_t d = static_cast<uint32_t>(std::max(1, q->topk));
+  int l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  q->topk_magic = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+  q->topk_sh1 = std::min(l, 1);
+  q->topk_sh2 = std::max(l - 1, 0);
+}
+
 // A launch's normalised parameters (k split, tail split, whether it has a
 // plan) and the positions per XCD its whole tiles may take: the even split
 // needs total / 8; a cost-balanced plan may give an XCD up to a quarter more
@@ -1057,6 +1079,7 @@ static int launch_wide_t(const GemmParams& p, int row_blocks, hipStream_t stream
   GemmParams q;
   int64_t cap;
   wide_launch_shape(GEMM1, p, row_blocks, &q, &cap);
+  set_topk_magic(&q);
   const int n_ct_walk = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   const double rows_per_expert =
       p.num_experts > 0 ? static_cast<double>(p.numel) / p.num_experts : 0.0;

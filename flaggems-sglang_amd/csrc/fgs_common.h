@@ -32,10 +32,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) |
-         (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+// Two f32 -> one word of two bf16 (round to nearest even, lo in the low
+// half): one v_cvt_pk_bf16_f32 (converting the halves separately costs a
+// conversion each plus a shift and an or).
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return cvt_pk_bf16(lo, hi); }
 
 // The expert whose range of a routing tuple's gathered order holds position
 // j: expert e owns [raw[e], raw[e] + h[e]) with raw the running sums of the
@@ -114,13 +120,6 @@ __device__ __forceinline__ uint16_t gemm1_epilogue(float g, float u, bool scale,
   return f32_to_bf16_bits(act == kActGelu ? gelu_mul(g, u) : silu_mul(g, u));
 }
 
-// Two f32 -> one word of two bf16 (round to nearest even), one
-// v_cvt_pk_bf16_f32.
-typedef __attribute__((ext_vector_type(2))) float f32x2;
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
-}
 
 // gemm1_epilogue's silu path for two adjacent outputs, word-packed: the same
 // roundings (g and u to bf16, silu(g) * u in fp32, bf16 out) with the

@@ -838,10 +838,13 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
                   const f32x4 bb = cb4(j * 32 + csub + 8 * g4);
                   const int v = 4 * g4;
                   uint2 v2;
-                  v2.x = pack_bf16x2(value(acc[i][j], v, sa, sw[0]) + bb[0],
-                                     value(acc[i][j], v + 1, sa, sw[1]) + bb[1]);
-                  v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, sw[2]) + bb[2],
-                                     value(acc[i][j], v + 3, sa, sw[3]) + bb[3]);
+                  // (no bias: no add, so the pair converts straight from
+                  // the accumulators)
+                  auto with_b = [&](float x, float b) { return BIAS ? x + b : x; };
+                  v2.x = pack_bf16x2(with_b(value(acc[i][j], v, sa, sw[0]), bb[0]),
+                                     with_b(value(acc[i][j], v + 1, sa, sw[1]), bb[1]));
+                  v2.y = pack_bf16x2(with_b(value(acc[i][j], v + 2, sa, sw[2]), bb[2]),
+                                     with_b(value(acc[i][j], v + 3, sa, sw[3]), bb[3]));
                   const int c = j * 4 + g4;
                   *reinterpret_cast<uint2*>(stg + r * (CH * 16) + ((c ^ (r % CH)) * 16) + half * 8) = v2;
                 }

@@ -830,11 +830,14 @@ __device__ __forceinline__ void tiled_tile(const GemmParams& p, const int rb_id,
                 const f32x4 w = scale_at(j, g4);
                 const f32x4 b = bias_at(j, g4);
                 const int v = 4 * g4;
+                // (no bias: no add, so the pair converts straight from
+                // the accumulators)
+                auto with_b = [&](float x, float bv) { return BIAS ? x + bv : x; };
                 uint2 v2;
-                v2.x = pack_bf16x2(value(acc[i][j], v, sa, w[0]) + b[0],
-                                   value(acc[i][j], v + 1, sa, w[1]) + b[1]);
-                v2.y = pack_bf16x2(value(acc[i][j], v + 2, sa, w[2]) + b[2],
-                                   value(acc[i][j], v + 3, sa, w[3]) + b[3]);
+                v2.x = pack_bf16x2(with_b(value(acc[i][j], v, sa, w[0]), b[0]),
+                                   with_b(value(acc[i][j], v + 1, sa, w[1]), b[1]));
+                v2.y = pack_bf16x2(with_b(value(acc[i][j], v + 2, sa, w[2]), b[2]),
+                                   with_b(value(acc[i][j], v + 3, sa, w[3]), b[3]));
                 *reinterpret_cast<uint2*>(slot_at(ch, r, jl * 4 + g4) + half * 8) = v2;
               }
             }

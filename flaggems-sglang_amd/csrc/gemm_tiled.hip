@@ -179,7 +179,7 @@ __device__ __forceinline__ void tiled_tile(const GemmParams& p, const int rb_id,
   auto act_row = [&](int r) -> int64_t {
     const int sid = p.sorted_ids[row0 + r];
     const bool ok = sid < p.numel;
-    return GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? r : 0);
+    return GEMM1 ? (ok ? div_topk(p, sid) : 0) : row0 + (ok ? r : 0);
   };
 
   // ---- this lane's source of each LDS-DMA load: row lane/CPR, chunk lane%CPR
@@ -196,7 +196,7 @@ __device__ __forceinline__ void tiled_tile(const GemmParams& p, const int rb_id,
   for (int i = 0; i < NLA; ++i) {
     const int r = (wave * NLA + i) * C::LR + lrow;
     const bool ok = a_sid[i] < p.numel;
-    const int64_t arow = GEMM1 ? (ok ? a_sid[i] / p.topk : 0) : row0 + (ok ? r : 0);
+    const int64_t arow = GEMM1 ? (ok ? div_topk(p, a_sid[i]) : 0) : row0 + (ok ? r : 0);
     a_src[i] = p.a + arow * row_bytes + chunk_pos<C>(r, lchunk) * 16;
   }
   const uint8_t* b_src[NLB];
@@ -328,7 +328,7 @@ __device__ __forceinline__ void tiled_tile(const GemmParams& p, const int rb_id,
   // activation row (a_scale index) of tile row rr holding slot sid
   auto act_of = [&](int rr, int sid) -> int64_t {
     const bool ok = sid < p.numel;
-    return GEMM1 ? (ok ? sid / p.topk : 0) : row0 + (ok ? rr : 0);
+    return GEMM1 ? (ok ? div_topk(p, sid) : 0) : row0 + (ok ? rr : 0);
   };
 #pragma unroll
   for (int s = 0; s < STAGES; ++s) {
@@ -870,14 +870,21 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_tiled_kernel(
   // split-K (GEMM2 only): the row-block index space repeats once per split
   const int ks = rb_id / p.row_blocks;
   rb_id -= ks * p.row_blocks;
-  if (rb_id * BM >= p.num_post_pad[0]) return;
+  // Every word the early exits read, loaded together: none depends on
+  // another, so one round trip instead of up to four (blocks past the
+  // padded count hold -1 experts and pad slots, so the loads stay in the
+  // buffers whatever the block).
+  const int npp = p.num_post_pad[0];
   // row blocks smaller than the alignment block (eid_shift > 0): the expert
   // of the enclosing block; a block that is all padding has nothing to do
   const int e = p.expert_ids[rb_id >> p.eid_shift];
+  const int sid_first = p.eid_shift > 0 ? p.sorted_ids[rb_id * BM] : 0;
+  const int sid_bma = C::BMA < BM ? p.sorted_ids[rb_id * BM + (C::BMA < BM ? C::BMA : 0)] : 0;
+  if (rb_id * BM >= npp) return;
   if (e < 0) return;
-  if (p.eid_shift > 0 && p.sorted_ids[rb_id * BM] >= p.numel) return;
+  if (p.eid_shift > 0 && sid_first >= p.numel) return;
   if constexpr (C::BMA < BM) {
-    if (p.sorted_ids[rb_id * BM + C::BMA] >= p.numel) {
+    if (sid_bma >= p.numel) {
       tiled_tile<DT, C, GEMM1, true>(p, rb_id, tile_n, ks, e);
       return;
     }
@@ -931,6 +938,7 @@ static int launch_tiled(const GemmParams& p, int row_blocks, hipStream_t stream)
   const int tiles_n = static_cast<int>(GEMM1 ? p.n_out / (C::BNR / 2) : p.n_out / C::BNR);
   GemmParams q = p;
   q.row_blocks = row_blocks;
+  set_topk_magic(&q);
   q.group_m = group_m_choice(C::BM, p);
   q.group_n = group_n_choice();
   if (GEMM1 || q.ksplit < 1) q.ksplit = 1;

@@ -9,6 +9,25 @@
 
 namespace fgs {
 
+// Division by topk as a multiply and two shifts (Granlund and Montgomery,
+// "Division by Invariant Integers using Multiplication", PLDI 1994, unsigned
+// case, exact for every 32-bit numerator): l = ceil(log2 d), magic =
+// floor(2^32 (2^l - d) / d) + 1, q = (t + ((n - t) >> min(l, 1))) >>
+// max(l - 1, 0) with t = the high word of magic * n. The launch sets the
+// magic; the kernels divide token slots by topk with it.
+inline void set_topk_magic(GemmParams* q) {
+  const uint32_t d = static_cast<uint32_t>(q->topk > 1 ? q->topk : 1);
+  int l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  q->topk_magic = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+  q->topk_sh1 = l < 1 ? l : 1;
+  q->topk_sh2 = l > 1 ? l - 1 : 0;
+}
+__device__ __forceinline__ int div_topk(const GemmParams& p, int n) {
+  const uint32_t t = __umulhi(p.topk_magic, static_cast<uint32_t>(n));
+  return static_cast<int>((t + ((static_cast<uint32_t>(n) - t) >> p.topk_sh1)) >> p.topk_sh2);
+}
+
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

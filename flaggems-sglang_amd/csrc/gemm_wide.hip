@@ -327,11 +327,6 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     int e;  // expert of the weight rows
     uint32_t va[NLA], vb[NLB];
   };
-  // slot / topk without a division (the launch's magic number)
-  auto div_topk = [&](int n) -> int {
-    const uint32_t t1 = __umulhi(p.topk_magic, static_cast<uint32_t>(n));
-    return static_cast<int>((t1 + ((static_cast<uint32_t>(n) - t1) >> p.topk_sh1)) >> p.topk_sh2);
-  };
   const int lrow = lane / C::CPR;   // row of a load this lane copies
   const int lchunk = lane % C::CPR;  // its physical chunk
   auto make_src = [&](const Tile& t, Src& s) {
@@ -346,7 +341,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
     for (int i = 0; i < NLA; ++i) {
       const int r = (wave * NLA + i) * C::LR + lrow;
       const bool ok = sid[i] < p.numel;
-      const int64_t arow = GEMM1 ? (ok ? div_topk(sid[i]) : 0) : row0 + (ok ? r : 0);
+      const int64_t arow = GEMM1 ? (ok ? div_topk(p, sid[i]) : 0) : row0 + (ok ? r : 0);
       s.va[i] = static_cast<uint32_t>(arow * row_bytes + wide_chunk<C>(r, lchunk) * 16);
     }
 #pragma unroll
@@ -664,7 +659,7 @@ __global__ __launch_bounds__(C::NW * 64, 1) void moe_gemm_wide_kernel(const Gemm
           const int t = i * 32 + (lane & 31);
           tsid[t] = sid;
           if constexpr (INT8)
-            tab[384 + t] = p.a_scale[GEMM1 ? (ok ? div_topk(sid) : 0) : row0 + (ok ? rr : 0)];
+            tab[384 + t] = p.a_scale[GEMM1 ? (ok ? div_topk(p, sid) : 0) : row0 + (ok ? rr : 0)];
           if (woi) tab[128 + t] = ok ? p.topk_w[sid] : 1.f;
         }
       }
@@ -1019,20 +1014,6 @@ static bool wide_early_a_choice(const GemmParams& p) {
   }();
   if (forced >= 0) return forced == 1;
   return p.num_experts > 0 && p.numel >= 512LL * p.num_experts;
-}
-
-// Division by topk as a multiply and two shifts (Granlund and Montgomery,
-// "Division by Invariant Integers using Multiplication", PLDI 1994, unsigned
-// case, exact for every 32-bit numerator): l = ceil(log2 d), magic =
-// floor(2^32 (2^l - d) / d) + 1, q = (t + ((n - t) >> min(l, 1))) >>
-// max(l - 1, 0) with t = the high word of magic * n.
-static void set_topk_magic(GemmParams* q) {
-  const uint32_t d = static_cast<uint32_t>(std::max(1, q->topk));
-  int l = 0;
-  while ((uint64_t{1} << l) < d) ++l;
-  q->topk_magic = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
-  q->topk_sh1 = std::min(l, 1);
-  q->topk_sh2 = std::max(l - 1, 0);
 }
 
 // A launch's normalised parameters (k split, tail split, whether it has a

@@ -235,10 +235,14 @@ __device__ __forceinline__ WideRange wide_range(const GemmParams& p, int total, 
   WideRange w;
   w.claims = false;
   if (p.plan) {
+    // the three words load together (one round trip): the plan always holds
+    // all nine bounds, valid or not
     const int first = __builtin_amdgcn_readfirstlane(p.plan[0]);
+    const int lo = __builtin_amdgcn_readfirstlane(p.plan[xcd]);
+    const int hi = __builtin_amdgcn_readfirstlane(p.plan[xcd + 1]);
     if (first >= 0) {
-      w.lo = __builtin_amdgcn_readfirstlane(p.plan[xcd]);
-      w.hi = __builtin_amdgcn_readfirstlane(p.plan[xcd + 1]);
+      w.lo = lo;
+      w.hi = hi;
       w.claims = true;
       return w;
     }
